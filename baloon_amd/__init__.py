@@ -1,0 +1,167 @@
+"""baloon_amd -- MI355X-native gated delta-rule (GDN) path.
+
+The product is ``libixgdn.so`` (HIP, gfx950), whose C ABI is ``include/ix_gdn.h``. This
+module binds it with ctypes and mirrors the reference's launcher interface
+(src/ix_gdn.cu:108-136): the same names, the same argument order and meaning, and the same
+error behaviour -- every call returns a ``hipError_t`` code (0 = success), with
+``hipErrorInvalidValue`` (1) for shapes the reference rejects.
+
+PyTorch is only plumbing here: tensors supply device memory and the current stream. Every
+tensor argument must live on the GPU; the functions pass raw device pointers to the C ABI.
+There is no CPU fallback: if the library is missing, :func:`lib` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libixgdn.so")
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+HIP_ERROR_NOT_SUPPORTED = 801
+
+HEAD_MOD = 0   # src = h mod h_k (reference pairing, src/ix_gdn.cu:38)
+HEAD_DIV = 1   # src = h / (h_v / h_k)
+ACT_NONE = 0   # conv output used as is (reference, src/ix_gdn.cu:64-67)
+ACT_SILU = 1
+
+# Every symbol include/ix_gdn.h declares.
+EXPORTS = (
+    "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
+    "ix_gdn_channels", "ix_gdn_decode", "ix_gdn_prefill_workspace_size", "ix_gdn_prefill",
+    "ix_gdn_version",
+)
+
+
+class IxGdnError(RuntimeError):
+    def __init__(self, name: str, code: int):
+        super().__init__(f"{name} returned hipError_t {code}")
+        self.code = code
+
+
+class Cfg(ctypes.Structure):
+    """``ix_gdn_cfg`` (include/ix_gdn.h)."""
+
+    _fields_ = [
+        ("h_k", ctypes.c_int), ("h_v", ctypes.c_int),
+        ("d_k", ctypes.c_int), ("d_v", ctypes.c_int),
+        ("d_conv", ctypes.c_int), ("head_map", ctypes.c_int), ("conv_act", ctypes.c_int),
+        ("q_scale", ctypes.c_float), ("l2_eps", ctypes.c_float),
+    ]
+
+    @property
+    def channels(self) -> int:
+        return 2 * self.h_k * self.d_k + self.h_v * self.d_v
+
+
+def make_cfg(h_k=16, h_v=32, d_k=128, d_v=128, d_conv=4, head_map=HEAD_MOD, conv_act=ACT_NONE,
+             q_scale=1.0, l2_eps=1e-6) -> Cfg:
+    """Layer description; defaults are the reference's semantics at the Qwen3-Next shape."""
+    return Cfg(h_k, h_v, d_k, d_v, d_conv, head_map, conv_act, q_scale, l2_eps)
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libixgdn.so (built by ``python -m baloon_amd.build``); raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m baloon_amd.build`")
+    L = ctypes.CDLL(LIB_PATH)
+    P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    sig = {
+        "ix_gdn_step": ([P, P, P, P, P, P, P, I, I, I, P], I),
+        "ix_gdn_conv_step": ([P, P, P, P, I, I, P], I),
+        "ix_gdn_l2_norm": ([P, I, I, F, P], I),
+        "ix_gdn_beta_gate": ([P, I, P], I),
+        "ix_gdn_out_norm": ([P, P, P, P, I, I, F, P], I),
+        "ix_gdn_channels": ([P], I),
+        "ix_gdn_decode": ([P, I, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_gdn_prefill_workspace_size": ([P, I, I], Z),
+        "ix_gdn_prefill": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
+        "ix_gdn_version": ([], ctypes.c_char_p),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _ptr(t) -> int | None:
+    """Device pointer of a CUDA tensor (None for None)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("baloon_amd: tensors must be on the GPU")
+    if not t.is_contiguous():
+        raise ValueError("baloon_amd: tensors must be contiguous")
+    return t.data_ptr()
+
+
+def _stream(s) -> int | None:
+    if s is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    return getattr(s, "cuda_stream", s)
+
+
+def check(name: str, code: int) -> None:
+    if code != HIP_SUCCESS:
+        raise IxGdnError(name, code)
+
+
+# ---- legacy entry points (src/ix_gdn.cu:108-136), return hipError_t --------------------------
+
+def ix_gdn_step(state, q, k, v, gate, beta, o, S, h_k, h_v, s=None) -> int:
+    return lib().ix_gdn_step(_ptr(state), _ptr(q), _ptr(k), _ptr(v), _ptr(gate), _ptr(beta), _ptr(o),
+                             S, h_k, h_v, _stream(s))
+
+
+def ix_gdn_conv_step(conv_state, x, kW, out, channels, d_conv, s=None) -> int:
+    return lib().ix_gdn_conv_step(_ptr(conv_state), _ptr(x), _ptr(kW), _ptr(out), channels, d_conv, _stream(s))
+
+
+def ix_gdn_l2_norm(x, rows, cols, eps, s=None) -> int:
+    return lib().ix_gdn_l2_norm(_ptr(x), rows, cols, eps, _stream(s))
+
+
+def ix_gdn_beta_gate(beta, h_v, s=None) -> int:
+    return lib().ix_gdn_beta_gate(_ptr(beta), h_v, _stream(s))
+
+
+def ix_gdn_out_norm(o, z, ssm_norm, y, h_v, S, eps, s=None) -> int:
+    return lib().ix_gdn_out_norm(_ptr(o), _ptr(z), _ptr(ssm_norm), _ptr(y), h_v, S, eps, _stream(s))
+
+
+# ---- fused layer entry points ------------------------------------------------------------------
+
+def ix_gdn_decode(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
+                  s=None) -> int:
+    """One decode token for B sequences. bf16 tensors may be torch.bfloat16 or int16/uint16 bits."""
+    return lib().ix_gdn_decode(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b),
+                               _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), _stream(s))
+
+
+def ix_gdn_prefill_workspace_size(cfg: Cfg, n_seq: int, total_T: int) -> int:
+    return lib().ix_gdn_prefill_workspace_size(ctypes.byref(cfg), n_seq, total_T)
+
+
+def ix_gdn_prefill(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, a, b, A_log, dt_bias, state,
+                   o=None, o_bf16=None, workspace=None, workspace_bytes=0, s=None) -> int:
+    return lib().ix_gdn_prefill(ctypes.byref(cfg), n_seq, total_T, _ptr(cu_seqlens), _ptr(x), _ptr(conv_state),
+                                _ptr(conv_w), _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o),
+                                _ptr(o_bf16), _ptr(workspace), workspace_bytes, _stream(s))
+
+
+def version() -> str:
+    return lib().ix_gdn_version().decode()
+
+
+from .layer import GdnLayer  # noqa: E402,F401

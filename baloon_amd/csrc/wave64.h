@@ -1,0 +1,72 @@
+// wave64.h -- CDNA4 (gfx950) wavefront primitives for the GDN kernels.
+//
+// Replaces the role of the reference's src/ix_compat.h (IX_WARP_SIZE and the 64-lane
+// butterfly reductions, ix_compat.h:12, :22-46, and ix_bf16_to_f32, :158-163) with native
+// gfx950 code: DPP row operations for the in-row steps, v_permlane16_swap /
+// v_permlane32_swap for the cross-row steps, and the hardware bf16 convert.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ixg {
+
+constexpr int kWave = 64;
+
+// DPP controls (GCN/CDNA encoding).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141; // lane i <- 7-i within each 8 lanes
+constexpr int kDppRowMirror = 0x140;     // lane i <- 15-i within each 16-lane row
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xF, 0xF, false));
+}
+
+// v[l] + v[l ^ 32] in every lane (v_permlane32_swap: the two results hold the lower half
+// swapped up and the upper half swapped down; their sum is the pair sum in both halves).
+__device__ __forceinline__ float pair_sum32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// v[l] + v[l ^ 16] in every lane (v_permlane16_swap on 16-lane rows).
+__device__ __forceinline__ float pair_sum16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 16 lanes of each row, result in every lane of the row.
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<kDppQuadXor1>(v);
+    v += dpp_f32<kDppQuadXor2>(v);
+    v += dpp_f32<kDppRowHalfMirror>(v);
+    v += dpp_f32<kDppRowMirror>(v);
+    return v;
+}
+
+// Sum over all 64 lanes, result in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+    return pair_sum32(pair_sum16(row_sum16(v)));
+}
+
+// Double-precision 64-lane sum, result in every lane (xor butterfly on ds_swizzle/bpermute).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+// bf16 <-> fp32. bf16 -> fp32 is exact; fp32 -> bf16 uses the gfx950 hardware convert,
+// round to nearest even.
+__device__ __forceinline__ float bf16_to_f32(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// Scalar math with the reference's definitions (src/ix_gdn.cu:22-23).
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+}  // namespace ixg

@@ -1,0 +1,187 @@
+#!/usr/bin/env python3
+"""Benchmark of the GDN decode hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--batch 64] [--layers 4]
+
+Workload (configuration 2 of the benchmark set): batched GDN decode, B = 64 independent
+sequences, 16 q/k heads and 32 v heads, d_k = d_v = 128, fp32 state 128 MiB per layer,
+fused conv (4 taps over 8192 channels), one ix_gdn_decode launch per step. A "step" is one
+decode token for all B sequences of one layer; steps rotate over --layers independent layers
+(state, conv state, weights), so the working set (4 x 128 MiB) exceeds the 256 MB Infinity
+Cache and the state really streams from HBM. Inputs are synthetic, resident in HBM before the
+timed region. Every kernel launch is bracketed by HIP events on the launch stream.
+
+Prints one JSON line: decode tokens/s (value), the state-traffic roofline of the decode
+kernel, and the oracle (CPU port of the reference recurrence) timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E spec
+STATE_TILE = 128 * 128 * 4     # bytes per (sequence, v head)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--inputs", type=int, default=8, help="distinct input sets cycled through")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget per CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+def decode_bench(args):
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    B, L, P = args.batch, args.layers, args.inputs
+    C, hv = cfg.channels, cfg.h_v
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6D4E0002)
+    layers = []
+    for _ in range(L):
+        layers.append(dict(
+            w=(torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16),
+            A_log=torch.rand(hv, generator=g, device=dev) * float(torch.log(torch.tensor(16.0))),
+            dt=torch.randn(hv, generator=g, device=dev) * 0.1,
+            state=torch.randn(B, hv, 128, 128, generator=g, device=dev) * 0.02,
+            cs=torch.randn(B, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16),
+        ))
+    ins = [dict(x=torch.randn(B, C, generator=g, device=dev).to(torch.bfloat16),
+                a=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16),
+                b=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16)) for _ in range(P)]
+    o = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+    lib = bx.lib()
+    import ctypes
+    cfg_ref = ctypes.byref(cfg)
+    s_ptr = stream.cuda_stream
+
+    def launch(i):
+        Ly, In = layers[i % L], ins[i % P]
+        return lib.ix_gdn_decode(cfg_ref, B, In["x"].data_ptr(), Ly["cs"].data_ptr(), Ly["w"].data_ptr(),
+                                 In["a"].data_ptr(), In["b"].data_ptr(), Ly["A_log"].data_ptr(), Ly["dt"].data_ptr(),
+                                 Ly["state"].data_ptr(), None, o.data_ptr(), s_ptr)
+
+    for i in range(args.warmup):
+        bx.check("ix_gdn_decode", launch(i))
+    torch.cuda.synchronize()
+    K = args.steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(K)]
+    torch.cuda.synchronize()
+    for i in range(K):
+        ev[i][0].record(stream)
+        rc = launch(i)
+        ev[i][1].record(stream)
+        if rc:
+            bx.check("ix_gdn_decode", rc)
+    torch.cuda.synchronize()
+    total_ms = ev[0][0].elapsed_time(ev[-1][1])
+    kern_ms = [a.elapsed_time(b) for a, b in ev]
+    avg_kernel_s = sum(kern_ms) / K / 1e3
+    state_bytes = 2 * B * hv * STATE_TILE
+    achieved = state_bytes / avg_kernel_s / 1e9
+    return dict(
+        tokens_per_s=B * K / (total_ms / 1e3),
+        ms_per_step=total_ms / K,
+        avg_kernel_us=avg_kernel_s * 1e6,
+        min_kernel_us=min(kern_ms) * 1e3,
+        state_bytes_per_launch=state_bytes,
+        state_gbs=state_bytes * K / (total_ms / 1e3) / 1e9,
+        roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None),
+    )
+
+
+def cpu_baseline(args):
+    """Oracle (C port of the reference's double recurrence, tests/test_gdn.cu:22-26, extended
+    with the fused conv/gates/L2) timed on this host's cores over a bounded sample of the same
+    workload: B = 64 sequences, decode steps until the time budget is used."""
+    import numpy as np
+
+    import oracle
+    from oracle import inputs
+
+    cfg = oracle.make_cfg()
+    B = args.batch
+    seed = inputs.seed_for(2)
+    p = inputs.layer_params(cfg, seed)
+    s = inputs.initial_states(cfg, seed, B)
+    toks = [inputs.token_inputs(cfg, seed, B, step=i) for i in range(2)]
+    ncores = min(16, os.cpu_count() or 1)
+    out = {}
+    for cores in sorted({1, ncores}):
+        cs, st = s["conv_state"], s["state"].astype(np.float64)
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            t = toks[steps % 2]
+            cs, st, _ = oracle.decode(cfg, B, t["x"], cs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], st,
+                                      nthreads=cores)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds or steps >= 256:
+                break
+        out[cores] = (B * steps / el, steps, el)
+    best = max(out)
+    v, steps, el = out[best]
+    return dict(value=round(v, 1), unit="tokens/s", cores=best, kind="port",
+                sample=f"B={B} decode, {steps} steps in {el:.1f} s on {best} threads (oracle/gdn_oracle.c, double)",
+                value_1core=round(out[1][0], 1))
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the GDN path is benchmarked on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.synchronize()
+    d = decode_bench(args)
+    cpu = None if args.no_cpu else cpu_baseline(args)
+    line = {
+        "metric": "GDN decode tokens/s at B=64 (32 v-heads, 128x128 fp32 state) + state HBM GB/s",
+        "value": round(d["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "C2 batched GDN decode: B=64, h_k=16, h_v=32, d=128, fused conv k=4, "
+                               f"{args.layers} layers rotated (state {args.layers}x128 MiB)",
+                   "B": args.batch, "layers": args.layers, "parallelism": "single-gpu"},
+        "state_gbs": round(d["state_gbs"], 1),
+        "state_frac_of_peak": round(d["state_gbs"] / HBM_PEAK_GBS, 4),
+        "avg_kernel_us": round(d["avg_kernel_us"], 2),
+        "roofline": d["roofline"],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,130 @@
+/*
+ * ix_gdn.h -- C ABI of libixgdn.so, the MI355X (gfx950) gated delta-rule (GDN) library.
+ *
+ * The first five entry points replace the reference's header-only inline launchers in
+ * src/ix_gdn.cu one for one: same names, same parameter order and meaning, same shape
+ * validation (hipErrorInvalidValue before any launch), same asynchronous contract (work is
+ * enqueued on `s`, nothing is allocated, the caller synchronises). They are exported with C
+ * linkage so any FFI can bind them; C++ callers get the reference's `s = 0` default.
+ *
+ * The fused decode and the chunked prefill are additions (no reference counterpart) for
+ * serving a whole GDN layer: bf16 activations in, fp32 recurrent state, conv fused ahead of
+ * the recurrence.
+ *
+ * Pointers are device pointers unless stated otherwise. bf16 values are passed as their
+ * 16-bit patterns (uint16_t).
+ */
+#ifndef IX_GDN_H
+#define IX_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+#define IX_GDN_DEFAULT_STREAM = 0
+extern "C" {
+#else
+#define IX_GDN_DEFAULT_STREAM
+#endif
+
+/* ---------------------------------------------------------------------------------------
+ * Legacy entry points (all fp32)
+ * --------------------------------------------------------------------------------------- */
+
+/* One decode token of the delta rule for h_v heads. Replaces ix_gdn_step, src/ix_gdn.cu:108-114.
+ * state [S][h_v][S] (element (h,i,j) at (i*h_v+h)*S+j, updated in place); q, k [h_k][S];
+ * v, o [h_v][S]; gate, beta [h_v] (gate is a log-decay, beta already sigmoided).
+ * For head h: src = h mod h_k, S_h <- exp(gate) S_h; d = beta (v - S_h^T k); S_h += k d^T;
+ * o = S_h^T q. Requires 0 < S <= 128, h_k > 0, h_v > 0. */
+hipError_t ix_gdn_step(float* state, const float* q, const float* k, const float* v, const float* gate,
+                       const float* beta, float* o, int S, int h_k, int h_v, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Depthwise causal conv over `channels` with a rolling state. Replaces ix_gdn_conv_step,
+ * src/ix_gdn.cu:115-120. conv_state [channels][d_conv-1] oldest first (shifted in place, x
+ * appended); kW [channels][d_conv]; out [channels] = sum(state*kW[..d_conv-1]) + x*kW[d_conv-1].
+ * Requires channels > 0, d_conv >= 2. */
+hipError_t ix_gdn_conv_step(float* conv_state, const float* x, const float* kW, float* out, int channels,
+                            int d_conv, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* In-place row L2 normalisation x <- x / sqrt(sum x^2 + eps) (double accumulation).
+ * Replaces ix_gdn_l2_norm, src/ix_gdn.cu:121-125. Requires rows > 0, 0 < cols <= 1024. */
+hipError_t ix_gdn_l2_norm(float* x, int rows, int cols, float eps, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* In-place beta <- sigmoid(beta). Replaces ix_gdn_beta_gate, src/ix_gdn.cu:126-130.
+ * Requires beta != NULL, h_v > 0. */
+hipError_t ix_gdn_beta_gate(float* beta, int h_v, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Gated RMS output norm y = o / sqrt(mean(o^2) + eps) * ssm_norm * sigmoid(z), per head.
+ * Replaces ix_gdn_out_norm, src/ix_gdn.cu:131-136. o, z, y [h_v][S]; ssm_norm [S].
+ * Requires h_v > 0, S > 0. */
+hipError_t ix_gdn_out_norm(const float* o, const float* z, const float* ssm_norm, float* y, int h_v, int S,
+                           float eps, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused layer entry points (additions; no reference counterpart)
+ * --------------------------------------------------------------------------------------- */
+
+enum { IX_GDN_HEAD_MOD = 0,   /* src = h mod h_k (the reference's pairing, src/ix_gdn.cu:38) */
+       IX_GDN_HEAD_DIV = 1 }; /* src = h / (h_v / h_k) (contiguous groups) */
+enum { IX_GDN_ACT_NONE = 0,   /* conv output used as is (the reference, src/ix_gdn.cu:64-67) */
+       IX_GDN_ACT_SILU = 1 }; /* SiLU after the conv */
+
+/* Host-side layer description (read on the host at call time). */
+typedef struct ix_gdn_cfg {
+    int h_k, h_v;     /* q/k heads and v heads */
+    int d_k, d_v;     /* head dims; the fused kernels require d_k = d_v = 128 */
+    int d_conv;       /* conv taps, 2..4 */
+    int head_map;     /* IX_GDN_HEAD_MOD or IX_GDN_HEAD_DIV */
+    int conv_act;     /* IX_GDN_ACT_NONE or IX_GDN_ACT_SILU */
+    float q_scale;    /* multiplies the normalised q (1.0 in the reference) */
+    float l2_eps;     /* q, k <- x / sqrt(sum x^2 + eps) */
+} ix_gdn_cfg;
+
+/* Mixed-projection channel count C = 2*h_k*d_k + h_v*d_v (order q | k | v). */
+int ix_gdn_channels(const ix_gdn_cfg* cfg);
+
+/* One decode token for B independent sequences of one GDN layer, in one launch:
+ * causal conv over the mixed q|k|v channels with its rolling state, per-head L2 norm of q
+ * and k, gates g = exp(-exp(A_log) * softplus(a + dt_bias)) and beta = sigmoid(b), head map
+ * of h_k q/k heads onto h_v v heads, and the delta-rule update of the fp32 state with the
+ * output o = S'^T q.
+ *   x          [B][C] bf16 (pre-conv mixed projection)
+ *   conv_state [B][C][d_conv-1] bf16, oldest first, updated in place
+ *   conv_w     [C][d_conv] bf16
+ *   a, b       [B][h_v] bf16 gate and beta logits
+ *   A_log, dt_bias [h_v] fp32
+ *   state      [B][h_v][d_k][d_v] fp32 (v index fastest), updated in place
+ *   o          [B][h_v][d_v] fp32, or NULL
+ *   o_bf16     [B][h_v][d_v] bf16 (round to nearest even of the fp32 output), or NULL
+ * Each state, conv-state and output element is touched by exactly one workgroup, so the
+ * in-place updates are race free. Calls on one stream are ordered; two streams must not
+ * share a state or conv-state buffer. */
+hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                         const uint16_t* conv_w, const uint16_t* a, const uint16_t* b, const float* A_log,
+                         const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
+                         hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Bytes of device workspace ix_gdn_prefill needs for n_seq sequences and total_T tokens. */
+size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
+
+/* Chunked (WY-form, chunk 64) prefill of n_seq packed sequences, the same math as
+ * total_T applications of ix_gdn_decode:
+ *   cu_seqlens [n_seq+1] int32 device offsets (cu_seqlens[0] = 0, non-decreasing)
+ *   x [total_T][C] bf16; a, b [total_T][h_v] bf16
+ *   conv_state [n_seq][C][d_conv-1] bf16 in/out; state [n_seq][h_v][d_k][d_v] fp32 in/out
+ *   o [total_T][h_v][d_v] fp32 or NULL; o_bf16 likewise
+ *   workspace: device memory of ix_gdn_prefill_workspace_size() bytes, 256-byte aligned. */
+hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
+                          const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                          const uint16_t* b, const float* A_log, const float* dt_bias, float* state, float* o,
+                          uint16_t* o_bf16, void* workspace, size_t workspace_bytes,
+                          hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Library version string. */
+const char* ix_gdn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IX_GDN_H */

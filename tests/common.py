@@ -1,0 +1,55 @@
+"""Shared helpers for the GDN tests: numpy <-> device tensors and the comparison norms."""
+from __future__ import annotations
+
+import numpy as np
+
+import oracle
+from oracle import bf16, inputs
+
+TOL_O_ABS = 1e-3       # fp32 outputs vs the double oracle, absolute
+TOL_STATE_REL = 1e-4   # fp32 state vs the double oracle, max|d| / max|ref|
+
+
+def dev(a, dtype=None):
+    """numpy array -> contiguous cuda tensor. uint16 arrays become bfloat16 (bit-exact)."""
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    t = torch.from_numpy(a.copy())
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def host(t) -> np.ndarray:
+    """cuda tensor -> numpy (bfloat16 -> uint16 bits)."""
+    import torch
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def bf16_excess_err(got_bits: np.ndarray, ref_f64: np.ndarray) -> float:
+    """max(|bf16 - ref| - half a bf16 ulp of ref): the error beyond bf16's own rounding."""
+    ref = np.asarray(ref_f64, dtype=np.float64)
+    got = bf16.to_f32(got_bits).astype(np.float64)
+    mag = np.abs(ref.astype(np.float32)).view(np.uint32) & np.uint32(0x7F800000)   # 2^e of |ref|
+    ulp = (mag.view(np.float32).astype(np.float64)) * 2.0 ** -7
+    half = np.maximum(ulp / 2, 2.0 ** -133)
+    return float(np.max(np.abs(got - ref) - half)) if ref.size else 0.0
+
+
+def bf16_ulp_diff(got_bits: np.ndarray, ref_f64: np.ndarray) -> int:
+    """Max distance in bf16 ulps between bf16 outputs and RNE(fp32(ref))."""
+    ref_bits = bf16.from_f32(np.asarray(ref_f64, dtype=np.float32)).astype(np.int32)
+    g = np.asarray(got_bits).astype(np.int32)
+
+    def ordered(u):  # map bf16 bit patterns to a monotonic integer line
+        return np.where(u & 0x8000, -(u & 0x7FFF), u & 0x7FFF)
+
+    return int(np.max(np.abs(ordered(g) - ordered(ref_bits)))) if g.size else 0
+
+
+__all__ = ["oracle", "bf16", "inputs", "dev", "host", "bf16_ulp_diff", "bf16_excess_err", "TOL_O_ABS", "TOL_STATE_REL"]

@@ -1,0 +1,89 @@
+"""The C ABI boundary, checked without a GPU: the library loads, exports every symbol that
+include/ix_gdn.h declares, and rejects the shapes the reference rejects (src/ix_gdn.cu:110,
+:117, :122, :127, :133) before touching the device. No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import baloon_amd as bx
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ix_gdn.h")
+INVALID = bx.HIP_ERROR_INVALID_VALUE
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(ix_gdn_[a-z0-9_]+)\s*\(",
+                                 text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    assert declared_functions() == sorted(bx.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    L = bx.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    assert bx.version().startswith("ixgdn")
+
+
+def test_resource_usage_has_no_scratch():
+    report = os.path.join(ROOT, "baloon_amd", "_build", "resource_usage.txt")
+    if not os.path.exists(report):
+        pytest.skip("library built without the resource report")
+    lines = [ln for ln in open(report) if ln.strip()]
+    assert lines, "empty resource report"
+    for ln in lines:
+        fields = dict(kv.split("=", 1) for kv in ln.split() if "=" in kv)
+        assert fields.get("ScratchSize") == "0", ln
+        assert fields.get("VGPRs Spill", "0") in ("0", None) or "Spill=0" in ln, ln
+
+
+NULL = None
+
+
+@pytest.mark.parametrize("S,hk,hv", [(0, 1, 1), (129, 1, 1), (-1, 1, 1), (128, 0, 1), (128, 1, 0)])
+def test_step_rejects_bad_shapes(S, hk, hv):
+    assert bx.lib().ix_gdn_step(NULL, NULL, NULL, NULL, NULL, NULL, NULL, S, hk, hv, NULL) == INVALID
+
+
+@pytest.mark.parametrize("C,dc", [(0, 4), (-3, 4), (8, 1), (8, 0)])
+def test_conv_rejects_bad_shapes(C, dc):
+    assert bx.lib().ix_gdn_conv_step(NULL, NULL, NULL, NULL, C, dc, NULL) == INVALID
+
+
+@pytest.mark.parametrize("rows,cols", [(0, 8), (4, 0), (4, 1025), (-1, 8)])
+def test_l2_rejects_bad_shapes(rows, cols):
+    assert bx.lib().ix_gdn_l2_norm(NULL, rows, cols, ctypes.c_float(1e-6), NULL) == INVALID
+
+
+def test_beta_rejects_null_and_bad_count():
+    assert bx.lib().ix_gdn_beta_gate(NULL, 4, NULL) == INVALID
+    assert bx.lib().ix_gdn_beta_gate(ctypes.c_void_p(16), 0, NULL) == INVALID
+
+
+@pytest.mark.parametrize("hv,S", [(0, 8), (4, 0)])
+def test_out_norm_rejects_bad_shapes(hv, S):
+    assert bx.lib().ix_gdn_out_norm(NULL, NULL, NULL, NULL, hv, S, ctypes.c_float(1e-6), NULL) == INVALID
+
+
+def test_fused_cfg_validation():
+    L = bx.lib()
+    good = bx.make_cfg()
+    assert L.ix_gdn_channels(ctypes.byref(good)) == 8192
+    bad = [bx.make_cfg(d_k=64), bx.make_cfg(d_conv=1), bx.make_cfg(d_conv=5), bx.make_cfg(h_k=0),
+           bx.make_cfg(head_map=2), bx.make_cfg(h_k=3, h_v=32, head_map=bx.HEAD_DIV), bx.make_cfg(conv_act=7)]
+    for c in bad:
+        rc = L.ix_gdn_decode(ctypes.byref(c), 1, *([ctypes.c_void_p(256)] * 8), NULL, NULL, NULL)
+        assert rc == INVALID
+    p = ctypes.c_void_p(256)
+    assert L.ix_gdn_decode(ctypes.byref(good), 0, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+    assert L.ix_gdn_decode(ctypes.byref(good), 1, NULL, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+    assert L.ix_gdn_decode(ctypes.byref(good), 1, p, p, p, p, p, p, p, ctypes.c_void_p(260), NULL, NULL,
+                           NULL) == INVALID           # state must be 16-byte aligned
+    assert L.ix_gdn_decode(None, 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
