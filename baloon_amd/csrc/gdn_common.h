@@ -1,0 +1,73 @@
+// gdn_common.h -- layer description and per-channel helpers shared by the fused decode and
+// the chunked prefill kernels (gfx950).
+//
+// Semantics follow the reference's GDN path (src/ix_gdn.cu): modulo head pairing
+// (src = h mod h_k, :38), causal depthwise conv with a rolling history, oldest first
+// (:58-70), softplus with threshold 20 and sigmoid (:22-23). The layer-level extensions
+// (gate from A_log/dt_bias, beta = sigmoid(b), optional SiLU after the conv, the
+// contiguous head map) are selected by ix_gdn_cfg.
+#pragma once
+#include "ix_gdn.h"
+#include "wave64.h"
+
+namespace ixg {
+
+constexpr int kD = 128;   // d_k = d_v handled by the fused kernels
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Device copy of the fields of ix_gdn_cfg the kernels use, plus the layer parameters.
+struct Layer {
+    const uint16_t* conv_w;   // [C][dc] bf16
+    const float* A_log;       // [h_v]
+    const float* dt_bias;     // [h_v]
+    int h_k, h_v, C, dc, head_map, conv_act, per_src;
+    float q_scale, l2_eps;
+};
+
+inline Layer make_layer(const ix_gdn_cfg* c, const uint16_t* conv_w, const float* A_log, const float* dt_bias) {
+    Layer L;
+    L.conv_w = conv_w; L.A_log = A_log; L.dt_bias = dt_bias;
+    L.h_k = c->h_k; L.h_v = c->h_v; L.C = 2 * c->h_k * c->d_k + c->h_v * c->d_v; L.dc = c->d_conv;
+    L.head_map = c->head_map; L.conv_act = c->conv_act;
+    L.per_src = c->head_map == IX_GDN_HEAD_DIV ? c->h_v / c->h_k : 0;
+    L.q_scale = c->q_scale; L.l2_eps = c->l2_eps;
+    return L;
+}
+
+// v heads mapped onto q/k head `src`: slot m of `mapped_count` (ascending head index).
+__device__ __forceinline__ int mapped_head(const Layer& L, int src, int m) {
+    return L.head_map == IX_GDN_HEAD_MOD ? src + m * L.h_k : src * L.per_src + m;
+}
+__device__ __forceinline__ int mapped_count(const Layer& L, int src) {
+    if (L.head_map == IX_GDN_HEAD_MOD) return src < L.h_v ? (L.h_v - src + L.h_k - 1) / L.h_k : 0;
+    return L.per_src;
+}
+// q/k head feeding v head h.
+__device__ __forceinline__ int src_of(const Layer& L, int h) {
+    return L.head_map == IX_GDN_HEAD_MOD ? h % L.h_k : h / L.per_src;
+}
+
+// Channel offsets in the mixed projection (order q | k | v).
+__device__ __forceinline__ int q_channel(const Layer& L, int src, int i) { return src * kD + i; }
+__device__ __forceinline__ int k_channel(const Layer& L, int src, int i) { return (L.h_k + src) * kD + i; }
+__device__ __forceinline__ int v_channel(const Layer& L, int h, int j) { return (2 * L.h_k + h) * kD + j; }
+
+// Conv output of one channel from its history (oldest first, dc-1 values) and the current
+// input; the accumulation order is the one both fused kernels use.
+__device__ __forceinline__ float conv_eval(const Layer& L, const float* hist, float x, const uint16_t* w) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        if (i < L.dc - 1) acc = fmaf(hist[i], bf16_to_f32(w[i]), acc);
+    acc = fmaf(x, bf16_to_f32(w[L.dc - 1]), acc);
+    if (L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
+    return acc;
+}
+
+// Log decay -exp(A_log) * softplus(a + dt_bias); the decay is exp() of it.
+__device__ __forceinline__ float log_gate(const Layer& L, int h, float a) {
+    return -expf(L.A_log[h]) * softplus_f(a + L.dt_bias[h]);
+}
+
+}  // namespace ixg

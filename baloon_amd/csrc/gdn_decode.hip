@@ -6,206 +6,206 @@
 // the delta-rule update of the fp32 state with output o = S'^T q. The reference does these
 // as separate launches (src/ix_gdn.cu:58-70, :73-84, :102-105, :25-56) and has no batch.
 //
-// Work decomposition: one workgroup per (sequence b, q/k head src). It owns the q and k
-// channels of src and every v head mapped to src, so each conv-state channel and each state
-// tile is read and written by exactly one workgroup: the in-place updates are race free
-// without any cross-workgroup synchronisation.
+// Work decomposition: one 256-thread workgroup per (sequence b, q/k head src). It owns the
+// q and k channels of src and every v head mapped to src, so each conv-state channel and
+// each state element is read and written by exactly one workgroup: the in-place updates
+// are race free without any cross-workgroup synchronisation.
 //
-// The state is the traffic (2 x 64 KiB per v head per token, ~0.9 FLOP/B): HBM-bound. Each
-// 128x128 fp32 tile is handled by 4 waves; lane (c = lane & 31, r = lane >> 5) of wave w
-// holds columns 4c..4c+3 of rows w*32 + 2m + r (m = 0..15) as 16 float4 registers, so every
-// load/store instruction of a wave moves 1 KiB of contiguous state. The tile is loaded once
-// (loads issued before the conv so HBM latency overlaps it), reduced once for both S^T k
-// and S^T q (in-thread over 16 rows, v_permlane32_swap across the two row halves of a wave,
-// LDS across the 4 waves), and written once:
-//   u = g S^T k,  d = beta (v - u),  S' = g S + k d^T,  o = g S^T q + d (k . q).
-#include "ix_gdn.h"
-#include "wave64.h"
+// The state is the traffic (2 x 64 KiB per v head per token, ~0.9 FLOP/B): HBM-bound. A
+// workgroup streams its tiles as 16 KiB slabs of 128 rows x 32 columns. Columns are
+// independent in the update, so a slab is a complete unit of work:
+//   u = g S^T k,  d = beta (v - u),  S' = g S + k d^T,  o = g S^T q + d (k . q)
+// (the output identity lets one sweep produce both contractions, so every state element
+// is read once and written once). Thread (c4 = tid & 7, r0 = tid >> 3) holds float4 column
+// group c4 of rows r0 + 32 m, m = 0..3: each wave load/store instruction moves 8 full
+// 128-byte lines. Column sums are reduced in-thread over 4 rows, across the 8 row groups of
+// a wave with DPP row_ror and v_permlane16/32_swap, and across the 4 waves through LDS.
+// Slabs are loaded two ahead of the one being processed (the first ones before the conv,
+// so HBM latency overlaps it), with nontemporal loads and stores: the state is streamed
+// once per token and never reused from cache.
+#include "gdn_common.h"
 
 namespace ixg {
 namespace {
 
-constexpr int kD = 128;                 // d_k = d_v
-constexpr int kTileThreads = 256;       // 4 waves per 128x128 tile
-constexpr int kRowsPerLane = kD / (kTileThreads / 32);  // 16 rows (float4 column groups: 32 per row)
+constexpr int kThreads = 256;                        // 4 waves
+constexpr int kSlabCols = 32;                        // state columns per slab
+constexpr int kSlabsPerTile = kD / kSlabCols;        // 4
+constexpr int kRowsPerThread = kD / (kThreads / 8);  // 4: rows r0 + 32 m
+constexpr int kMaxHeadsPerGroup = 16;                // v heads per q/k head
 
 struct DecodeParams {
+    Layer L;
     const uint16_t* x;          // [B][C]
     uint16_t* conv_state;       // [B][C][dc-1]
-    const uint16_t* conv_w;     // [C][dc]
     const uint16_t* a;          // [B][h_v]
     const uint16_t* b;          // [B][h_v]
-    const float* A_log;         // [h_v]
-    const float* dt_bias;       // [h_v]
     float* state;               // [B][h_v][128][128]
     float* o;                   // [B][h_v][128] or null
     uint16_t* o_bf16;           // [B][h_v][128] or null
-    int h_k, h_v, C, dc, head_map, conv_act, per_src;
-    float q_scale, l2_eps;
 };
 
-__device__ __forceinline__ int mapped_head(const DecodeParams& p, int src, int m) {
-    return p.head_map == IX_GDN_HEAD_MOD ? src + m * p.h_k : src * p.per_src + m;
+// Sum over the 8 row groups of a wave (lanes that share lane & 7), result in every lane.
+__device__ __forceinline__ float rowgroup_sum(float v) {
+    v += dpp_f32<kDppRowRor8>(v);
+    return pair_sum32(pair_sum16(v));
 }
 
-__device__ __forceinline__ int mapped_count(const DecodeParams& p, int src) {
-    if (p.head_map == IX_GDN_HEAD_MOD) return src < p.h_v ? (p.h_v - src + p.h_k - 1) / p.h_k : 0;
-    return p.per_src;
-}
-
-// Conv of one channel of one sequence; shifts the rolling state and returns the output.
-__device__ __forceinline__ float conv_channel(const DecodeParams& p, int bseq, int ch) {
-    const size_t row = (size_t)bseq * p.C + ch;
-    uint16_t* st = p.conv_state + row * (p.dc - 1);
-    const uint16_t* w = p.conv_w + (size_t)ch * p.dc;
+// Conv of one channel of sequence bseq: reads and shifts its bf16 history in place.
+__device__ __forceinline__ float conv_step_channel(const DecodeParams& p, int bseq, int ch) {
+    const Layer& L = p.L;
+    const size_t row = (size_t)bseq * L.C + ch;
+    uint16_t* st = p.conv_state + row * (L.dc - 1);
     const uint16_t xu = p.x[row];
-    uint16_t hist[3];
+    uint16_t hu[3];
+    float hist[3];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) hist[i] = (i < p.dc - 1) ? st[i] : (uint16_t)0;
-    float acc = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 3; ++i)
-        if (i < p.dc - 1) acc = fmaf(bf16_to_f32(hist[i]), bf16_to_f32(w[i]), acc);
-    acc = fmaf(bf16_to_f32(xu), bf16_to_f32(w[p.dc - 1]), acc);
+    for (int i = 0; i < 3; ++i) {
+        hu[i] = (i < L.dc - 1) ? st[i] : (uint16_t)0;
+        hist[i] = bf16_to_f32(hu[i]);
+    }
+    const float y = conv_eval(L, hist, bf16_to_f32(xu), L.conv_w + (size_t)ch * L.dc);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-        if (i < p.dc - 2) st[i] = hist[i + 1];
-    st[p.dc - 2] = xu;
-    if (p.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
-    return acc;
+        if (i < L.dc - 2) st[i] = hu[i + 1];
+    st[L.dc - 2] = xu;
+    return y;
 }
 
-template <int NV>
-__global__ void __launch_bounds__(NV * kTileThreads)
+__global__ void __launch_bounds__(kThreads)
 decode_kernel(const DecodeParams p) {
-    __shared__ __align__(16) float qk_raw[2][kD];   // post-conv q, k of src
-    __shared__ __align__(16) float v_raw[NV][kD];   // post-conv v of each tile's head
-    __shared__ float4 red[NV][4][2][kD / 4];        // per-wave column partials of S^T k, S^T q
-    __shared__ float scal[4];                       // q.q, k.k, q.k
-    __shared__ float gates[NV][2];                  // g, beta
+    __shared__ __align__(16) float q_s[kD], k_s[kD];
+    __shared__ __align__(16) float v_s[kMaxHeadsPerGroup][kD];
+    __shared__ float gate_s[kMaxHeadsPerGroup][2];
+    __shared__ float scal_s[3];
+    __shared__ v4f red_s[2][kThreads / kWave][kSlabCols / 4][2];   // [slab parity][wave][c4][u|q]
 
+    const Layer& L = p.L;
     const int src = blockIdx.x, bseq = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int t = tid / kTileThreads;               // tile (v head slot) of this thread
-    const int ltid = tid % kTileThreads;
-    const int w = ltid / kWave, lane = tid & (kWave - 1);
-    const int cgrp = lane & 31, rsub = lane >> 5;
-    const int count = mapped_count(p, src);
+    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int c4 = tid & 7, r0 = tid >> 3;
+    const int count = mapped_count(L, src);
+    const int nslab = count * kSlabsPerTile;
 
-    for (int base = 0; base == 0 || base < count; base += NV) {
-        const int slot = base + t;
-        const bool active = slot < count;
-        const int h = active ? mapped_head(p, src, slot) : 0;
-        float4* tile = reinterpret_cast<float4*>(p.state + ((size_t)bseq * p.h_v + h) * kD * kD);
-
-        // 1. State loads first: 16 x float4 per lane, all in flight during the conv.
-        float4 s[kRowsPerLane];
-        if (active) {
+    // Address of this thread's first element of slab n (rows r0 + 32 m follow at stride 32 rows).
+    auto slab_ptr = [&](int n) -> v4f* {
+        const int h = mapped_head(L, src, n / kSlabsPerTile);
+        float* tile = p.state + ((size_t)bseq * L.h_v + h) * kD * kD;
+        return reinterpret_cast<v4f*>(tile + (size_t)r0 * kD + (n % kSlabsPerTile) * kSlabCols) + c4;
+    };
+    auto load_slab = [&](v4f (&buf)[kRowsPerThread], int n) {
+        if (n < nslab) {
+            const v4f* ptr = slab_ptr(n);
 #pragma unroll
-            for (int m = 0; m < kRowsPerLane; ++m) {
-                const int i = w * 32 + 2 * m + rsub;
-                s[m] = tile[i * (kD / 4) + cgrp];
-            }
+            for (int m = 0; m < kRowsPerThread; ++m)
+                buf[m] = __builtin_nontemporal_load(ptr + (size_t)m * 32 * (kD / 4));
         }
+    };
 
-        // 2. Conv: the first pass also covers q and k of src (256 channels, the first
-        //    256 threads); each tile's 128 v channels go to the remaining threads.
-        const int nwork = (base == 0 ? 2 * kD : 0) + NV * kD;
-        for (int e = tid; e < nwork; e += NV * kTileThreads) {
-            int ee = e - (base == 0 ? 2 * kD : 0);
-            if (ee < 0) {
-                const int which = e / kD, i = e % kD;     // 0: q, 1: k
-                const int ch = which * p.h_k * kD + src * kD + i;
-                qk_raw[which][i] = conv_channel(p, bseq, ch);
-            } else {
-                const int vt = ee / kD, i = ee % kD;
-                if (base + vt < count) {
-                    const int hv = mapped_head(p, src, base + vt);
-                    v_raw[vt][i] = conv_channel(p, bseq, 2 * p.h_k * kD + hv * kD + i);
-                }
+    v4f s0[kRowsPerThread], s1[kRowsPerThread], s2[kRowsPerThread];
+    load_slab(s0, 0);
+    load_slab(s1, 1);
+    load_slab(s2, 2);
+
+    // Conv over q, k of src and v of every mapped head; gates of every mapped head.
+    const int nch = 2 * kD + count * kD;
+    for (int e = tid; e < nch; e += kThreads) {
+        if (e < kD) {
+            q_s[e] = conv_step_channel(p, bseq, q_channel(L, src, e));
+        } else if (e < 2 * kD) {
+            k_s[e - kD] = conv_step_channel(p, bseq, k_channel(L, src, e - kD));
+        } else {
+            const int t = (e - 2 * kD) / kD, j = (e - 2 * kD) % kD;
+            v_s[t][j] = conv_step_channel(p, bseq, v_channel(L, mapped_head(L, src, t), j));
+        }
+    }
+    if (tid < count) {
+        const int h = mapped_head(L, src, tid);
+        const size_t ab = (size_t)bseq * L.h_v + h;
+        gate_s[tid][0] = expf(log_gate(L, h, bf16_to_f32(p.a[ab])));
+        gate_s[tid][1] = sigmoid_f(bf16_to_f32(p.b[ab]));
+    }
+    __syncthreads();
+
+    // q.q, k.k, q.k over the 128 dims (one wave each).
+    if (w < 3) {
+        const float* x0 = (w == 1) ? k_s : q_s;
+        const float* x1 = (w == 0) ? q_s : k_s;
+        const float r = wave_sum(fmaf(x0[lane], x1[lane], x0[lane + kWave] * x1[lane + kWave]));
+        if (lane == 0) scal_s[w] = r;
+    }
+    __syncthreads();
+    const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
+    const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
+    const float kq = scal_s[2] * inv_q * inv_k;
+    float kr[kRowsPerThread], qr[kRowsPerThread];
+#pragma unroll
+    for (int m = 0; m < kRowsPerThread; ++m) {
+        kr[m] = k_s[r0 + 32 * m] * inv_k;
+        qr[m] = q_s[r0 + 32 * m] * inv_q;
+    }
+
+    // One slab: column sums, update, write back, output.
+    auto process = [&](v4f (&buf)[kRowsPerThread], int n) {
+        const int t = n / kSlabsPerTile, sc = n % kSlabsPerTile;
+        v4f ak = {0.f, 0.f, 0.f, 0.f}, aq = ak;
+#pragma unroll
+        for (int m = 0; m < kRowsPerThread; ++m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ak[e] = fmaf(buf[m][e], kr[m], ak[e]);
+                aq[e] = fmaf(buf[m][e], qr[m], aq[e]);
             }
         }
-        if (ltid == kWave && active) {              // one lane per tile computes its gates
-            const float al = p.A_log[h], dt = p.dt_bias[h];
-            const float av = bf16_to_f32(p.a[(size_t)bseq * p.h_v + h]);
-            const float bv = bf16_to_f32(p.b[(size_t)bseq * p.h_v + h]);
-            gates[t][0] = expf(-expf(al) * softplus_f(av + dt));
-            gates[t][1] = sigmoid_f(bv);
-        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { ak[e] = rowgroup_sum(ak[e]); aq[e] = rowgroup_sum(aq[e]); }
+        if (lane < 8) { red_s[n & 1][w][c4][0] = ak; red_s[n & 1][w][c4][1] = aq; }
         __syncthreads();
-
-        // 3. q.q, k.k, q.k over the 128 channels (wave 0 of the workgroup, first pass).
-        if (base == 0 && tid < kWave) {
-            const float q0 = qk_raw[0][tid], q1 = qk_raw[0][tid + kWave];
-            const float k0 = qk_raw[1][tid], k1 = qk_raw[1][tid + kWave];
-            const float qq = wave_sum(fmaf(q0, q0, q1 * q1));
-            const float kk = wave_sum(fmaf(k0, k0, k1 * k1));
-            const float qk = wave_sum(fmaf(q0, k0, q1 * k1));
-            if (tid == 0) { scal[0] = qq; scal[1] = kk; scal[2] = qk; }
+        v4f A = red_s[n & 1][0][c4][0], Q = red_s[n & 1][0][c4][1];
+#pragma unroll
+        for (int ww = 1; ww < kThreads / kWave; ++ww) { A += red_s[n & 1][ww][c4][0]; Q += red_s[n & 1][ww][c4][1]; }
+        const float g = gate_s[t][0], bt = gate_s[t][1];
+        const v4f vv = *reinterpret_cast<const v4f*>(&v_s[t][sc * kSlabCols + 4 * c4]);
+        v4f d;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = (vv[e] - g * A[e]) * bt;
+        v4f* ptr = slab_ptr(n);
+#pragma unroll
+        for (int m = 0; m < kRowsPerThread; ++m) {
+            v4f r;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[m], d[e], buf[m][e] * g);
+            __builtin_nontemporal_store(r, ptr + (size_t)m * 32 * (kD / 4));
         }
-        __syncthreads();
-
-        const float inv_q = p.q_scale / sqrtf(scal[0] + p.l2_eps);
-        const float inv_k = 1.0f / sqrtf(scal[1] + p.l2_eps);
-        const float kq = scal[2] * inv_q * inv_k;
-
-        // 4. Column partials over this lane's 16 rows.
-        float4 ak = make_float4(0.f, 0.f, 0.f, 0.f), aq = ak;
-        if (active) {
+        if (r0 == 0) {
+            v4f ov;
 #pragma unroll
-            for (int m = 0; m < kRowsPerLane; ++m) {
-                const int i = w * 32 + 2 * m + rsub;
-                const float ki = qk_raw[1][i] * inv_k, qi = qk_raw[0][i] * inv_q;
-                ak.x = fmaf(s[m].x, ki, ak.x); ak.y = fmaf(s[m].y, ki, ak.y);
-                ak.z = fmaf(s[m].z, ki, ak.z); ak.w = fmaf(s[m].w, ki, ak.w);
-                aq.x = fmaf(s[m].x, qi, aq.x); aq.y = fmaf(s[m].y, qi, aq.y);
-                aq.z = fmaf(s[m].z, qi, aq.z); aq.w = fmaf(s[m].w, qi, aq.w);
-            }
-        }
-        ak.x = pair_sum32(ak.x); ak.y = pair_sum32(ak.y); ak.z = pair_sum32(ak.z); ak.w = pair_sum32(ak.w);
-        aq.x = pair_sum32(aq.x); aq.y = pair_sum32(aq.y); aq.z = pair_sum32(aq.z); aq.w = pair_sum32(aq.w);
-        if (rsub == 0) { red[t][w][0][cgrp] = ak; red[t][w][1][cgrp] = aq; }
-        __syncthreads();
-
-        // 5. Finish the reductions for this lane's 4 columns, update and write back.
-        if (active) {
-            const float g = gates[t][0], bt = gates[t][1];
-            float4 A = red[t][0][0][cgrp], Q = red[t][0][1][cgrp];
-#pragma unroll
-            for (int ww = 1; ww < 4; ++ww) {
-                const float4 a2 = red[t][ww][0][cgrp], q2 = red[t][ww][1][cgrp];
-                A.x += a2.x; A.y += a2.y; A.z += a2.z; A.w += a2.w;
-                Q.x += q2.x; Q.y += q2.y; Q.z += q2.z; Q.w += q2.w;
-            }
-            const float4 vv = reinterpret_cast<const float4*>(v_raw[t])[cgrp];
-            float4 d;
-            d.x = (vv.x - g * A.x) * bt; d.y = (vv.y - g * A.y) * bt;
-            d.z = (vv.z - g * A.z) * bt; d.w = (vv.w - g * A.w) * bt;
-#pragma unroll
-            for (int m = 0; m < kRowsPerLane; ++m) {
-                const int i = w * 32 + 2 * m + rsub;
-                const float ki = qk_raw[1][i] * inv_k;
-                float4 r;
-                r.x = fmaf(ki, d.x, s[m].x * g); r.y = fmaf(ki, d.y, s[m].y * g);
-                r.z = fmaf(ki, d.z, s[m].z * g); r.w = fmaf(ki, d.w, s[m].w * g);
-                tile[i * (kD / 4) + cgrp] = r;
-            }
-            if (w == 0 && rsub == 0) {
-                float4 ov;
-                ov.x = fmaf(d.x, kq, g * Q.x); ov.y = fmaf(d.y, kq, g * Q.y);
-                ov.z = fmaf(d.z, kq, g * Q.z); ov.w = fmaf(d.w, kq, g * Q.w);
-                const size_t oo = ((size_t)bseq * p.h_v + h) * kD + 4 * cgrp;
-                if (p.o) *reinterpret_cast<float4*>(p.o + oo) = ov;
-                if (p.o_bf16) {
-                    uint2 pk;
-                    pk.x = pack_bf16x2(ov.x, ov.y);
-                    pk.y = pack_bf16x2(ov.z, ov.w);
-                    *reinterpret_cast<uint2*>(p.o_bf16 + oo) = pk;
-                }
+            for (int e = 0; e < 4; ++e) ov[e] = fmaf(d[e], kq, g * Q[e]);
+            const int h = mapped_head(L, src, t);
+            const size_t oo = ((size_t)bseq * L.h_v + h) * kD + sc * kSlabCols + 4 * c4;
+            if (p.o) *reinterpret_cast<v4f*>(p.o + oo) = ov;
+            if (p.o_bf16) {
+                uint2 pk;
+                pk.x = pack_bf16x2(ov[0], ov[1]);
+                pk.y = pack_bf16x2(ov[2], ov[3]);
+                *reinterpret_cast<uint2*>(p.o_bf16 + oo) = pk;
             }
         }
-        if (base + NV >= count) break;
-        __syncthreads();                              // LDS is reused by the next group
+    };
+
+    // Three rotating slab buffers: the loop body is unrolled so no register is copied
+    // while its load is still in flight.
+    for (int n = 0; n < nslab; n += 3) {
+        process(s0, n);
+        load_slab(s0, n + 3);
+        if (n + 1 < nslab) {
+            process(s1, n + 1);
+            load_slab(s1, n + 4);
+        }
+        if (n + 2 < nslab) {
+            process(s2, n + 2);
+            load_slab(s2, n + 5);
+        }
     }
 }
 
@@ -216,7 +216,7 @@ extern "C" int ix_gdn_channels(const ix_gdn_cfg* c) {
     return c ? 2 * c->h_k * c->d_k + c->h_v * c->d_v : 0;
 }
 
-extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.1.0 gfx950"; }
+extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.2.0 gfx950"; }
 
 // Shared validation of the fused layer description (also used by the prefill).
 extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
@@ -226,6 +226,8 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
     if (c->d_conv < 2 || c->d_conv > 4) return hipErrorInvalidValue;
     if (c->head_map != IX_GDN_HEAD_MOD && c->head_map != IX_GDN_HEAD_DIV) return hipErrorInvalidValue;
     if (c->head_map == IX_GDN_HEAD_DIV && c->h_v % c->h_k != 0) return hipErrorInvalidValue;
+    const int per_src = (c->h_v + c->h_k - 1) / c->h_k;     // most v heads on one q/k head
+    if (per_src > ixg::kMaxHeadsPerGroup) return hipErrorInvalidValue;
     if (c->conv_act != IX_GDN_ACT_NONE && c->conv_act != IX_GDN_ACT_SILU) return hipErrorInvalidValue;
     if (!(c->l2_eps >= 0.0f)) return hipErrorInvalidValue;
     return hipSuccess;
@@ -243,12 +245,9 @@ extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t
         (o_bf16 && (reinterpret_cast<uintptr_t>(o_bf16) & 7)))
         return hipErrorInvalidValue;                 // float4 / uint2 accesses
     ixg::DecodeParams p;
-    p.x = x; p.conv_state = conv_state; p.conv_w = conv_w; p.a = a; p.b = b;
-    p.A_log = A_log; p.dt_bias = dt_bias; p.state = state; p.o = o; p.o_bf16 = o_bf16;
-    p.h_k = cfg->h_k; p.h_v = cfg->h_v; p.C = ix_gdn_channels(cfg); p.dc = cfg->d_conv;
-    p.head_map = cfg->head_map; p.conv_act = cfg->conv_act;
-    p.per_src = cfg->head_map == IX_GDN_HEAD_DIV ? cfg->h_v / cfg->h_k : 0;
-    p.q_scale = cfg->q_scale; p.l2_eps = cfg->l2_eps;
-    hipLaunchKernelGGL(ixg::decode_kernel<2>, dim3((unsigned)cfg->h_k, (unsigned)B), dim3(2 * ixg::kTileThreads), 0, s, p);
+    p.L = ixg::make_layer(cfg, conv_w, A_log, dt_bias);
+    p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
+    p.state = state; p.o = o; p.o_bf16 = o_bf16;
+    hipLaunchKernelGGL(ixg::decode_kernel, dim3((unsigned)cfg->h_k, (unsigned)B), dim3(ixg::kThreads), 0, s, p);
     return hipGetLastError();
 }

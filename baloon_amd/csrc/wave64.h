@@ -17,6 +17,7 @@ constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]
 constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141; // lane i <- 7-i within each 8 lanes
 constexpr int kDppRowMirror = 0x140;     // lane i <- 15-i within each 16-lane row
+constexpr int kDppRowRor8 = 0x128;       // lane i <- lane (i + 8) mod 16 within each row (= i ^ 8)
 
 template <int Ctrl>
 __device__ __forceinline__ float dpp_f32(float v) {
