@@ -87,3 +87,36 @@ def test_fused_cfg_validation():
     assert L.ix_gdn_decode(ctypes.byref(good), 1, p, p, p, p, p, p, p, ctypes.c_void_p(260), NULL, NULL,
                            NULL) == INVALID           # state must be 16-byte aligned
     assert L.ix_gdn_decode(None, 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+
+
+def test_prefill_validation_without_launch():
+    L = bx.lib()
+    cfg = bx.make_cfg()
+    need = bx.ix_gdn_prefill_workspace_size(cfg, 2, 100)
+    assert need > 0 and need % 256 == 0
+    assert bx.ix_gdn_prefill_workspace_size(cfg, 0, 100) == 0
+    assert bx.ix_gdn_prefill_workspace_size(cfg, 2, -1) == 0
+    assert bx.ix_gdn_prefill_workspace_size(bx.make_cfg(d_k=64), 2, 100) == 0
+    assert bx.ix_gdn_prefill_workspace_size(cfg, 2, 200) > need       # grows with tokens
+    p = ctypes.c_void_p(1 << 20)
+
+    def call(n_seq, T, ws, nbytes, c=cfg):
+        return L.ix_gdn_prefill(ctypes.byref(c), n_seq, T, p, p, p, p, p, p, p, p, p, NULL, NULL, ws, nbytes, NULL)
+
+    assert call(2, 100, p, need - 1) == INVALID                      # workspace too small
+    assert call(2, 100, ctypes.c_void_p((1 << 20) + 64), need) == INVALID   # not 256-byte aligned
+    assert call(2, 100, NULL, need) == INVALID                       # no workspace
+    assert call(0, 100, p, need) == INVALID
+    assert call(2, -5, p, need) == INVALID
+    assert call(2, 100, p, need, bx.make_cfg(head_map=5)) == INVALID
+    assert call(2, 0, NULL, 0) == bx.HIP_SUCCESS                     # nothing to consume: no launch
+
+
+def test_head_group_limit():
+    # at most 16 v heads per q/k head in the fused kernels
+    L = bx.lib()
+    p = ctypes.c_void_p(256)
+    ok, bad = bx.make_cfg(h_k=2, h_v=32), bx.make_cfg(h_k=1, h_v=17)
+    assert L.ix_gdn_decode(ctypes.byref(bad), 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+    assert bx.ix_gdn_prefill_workspace_size(ok, 1, 64) > 0
+    assert bx.ix_gdn_prefill_workspace_size(bad, 1, 64) == 0

@@ -1,0 +1,184 @@
+"""GPU parity of the chunked prefill (ix_gdn_prefill) against the oracle's token-by-token
+recurrence (oracle.prefill, double precision).
+
+Tolerances, from the benchmark's acceptance rule: fp32 outputs within 1e-3 absolute of
+the oracle; bf16 outputs exactly RNE of the kernel's own fp32 outputs; fp32 state
+max|d|/max|ref| <= 1e-4 after the sequence (the reference's norm, tests/test_gdn.cu:10-13);
+conv state bit-exact. Inputs come from the portable generator (oracle/inputs.py).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import baloon_amd as bx
+import oracle
+from oracle import bf16, inputs
+from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host
+
+pytestmark = pytest.mark.gpu
+NT = min(16, os.cpu_count() or 1)
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def gpu_prefill(cfg, cu, tok, p, st, outputs=("o", "ob")):
+    """Runs ix_gdn_prefill on copies of the states; returns (conv_state, state, o, o_bf16)."""
+    torch = _torch()
+    cu = np.asarray(cu, np.int32)
+    n, T = cu.size - 1, int(tok["x"].shape[0])
+    d_cs, d_st = dev(st["conv_state"]), dev(st["state"])
+    o = torch.full((T, cfg.h_v, cfg.d_v), float("nan"), dtype=torch.float32, device="cuda") if "o" in outputs else None
+    ob = torch.zeros(T, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda") if "ob" in outputs else None
+    need = bx.ix_gdn_prefill_workspace_size(cfg, n, T)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    rc = bx.ix_gdn_prefill(cfg, n, T, dev(cu), dev(tok["x"]), d_cs, dev(p["w"]), dev(tok["a"]), dev(tok["b"]),
+                           dev(p["A_log"]), dev(p["dt_bias"]), d_st, o, ob, ws, need)
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return (host(d_cs), host(d_st), None if o is None else host(o), None if ob is None else host(ob))
+
+
+def oracle_prefill(cfg, cu, tok, p, st):
+    return oracle.prefill(cfg, cu, tok["x"], st["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
+                          p["dt_bias"], st["state"], nthreads=NT)
+
+
+def check(cfg, cu, seed, state_std=0.02, conv_std=1.0):
+    cu = np.asarray(cu, np.int32)
+    n, T = cu.size - 1, int(cu[-1])
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, max(T, 1))
+    tok = {k: v[:T] for k, v in tok.items()}
+    st = inputs.initial_states(cfg, seed, n, state_std=state_std, conv_std=conv_std)
+    cs, s, o, ob = gpu_prefill(cfg, cu, tok, p, st)
+    rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    rel = oracle.rel_err(s, rs)
+    assert rel <= TOL_STATE_REL, f"state rel err {rel}"
+    if T:
+        err = float(np.max(np.abs(o - ro)))
+        assert err <= TOL_O_ABS, f"o abs err {err}"
+        np.testing.assert_array_equal(ob, bf16.from_f32(o))
+    return rel
+
+
+@pytest.mark.parametrize("T", [1, 5, 63, 64, 65, 200])
+def test_single_sequence_lengths(T):
+    check(oracle.make_cfg(), [0, T], inputs.seed_for(3) + T)
+
+
+def test_varlen_with_empty_and_short_sequences():
+    check(oracle.make_cfg(), [0, 0, 1, 65, 195, 198, 198, 260], inputs.seed_for(4))
+
+
+@pytest.mark.parametrize("kw", [
+    dict(head_map=1),
+    dict(conv_act=1),
+    dict(q_scale=128 ** -0.5),
+    dict(d_conv=2),
+    dict(d_conv=3),
+    dict(h_k=3, h_v=8),
+    dict(h_k=4, h_v=2),
+    dict(h_k=2, h_v=6, head_map=1),
+    dict(h_k=1, h_v=1),
+])
+def test_variants(kw):
+    check(oracle.make_cfg(**kw), [0, 70, 71, 150], inputs.seed_for(3) + 11 * len(kw))
+
+
+def test_zero_initial_state_config3_shape_short():
+    check(oracle.make_cfg(), [0, 300], inputs.seed_for(3), state_std=0.0, conv_std=0.0)
+
+
+def test_config3_full_T4096():
+    # configuration 3: one sequence of 4096 tokens from a zero state.
+    rel = check(oracle.make_cfg(), [0, 4096], inputs.seed_for(3), state_std=0.0, conv_std=0.0)
+    print(f"T=4096 state rel err {rel:.2e}")
+
+
+def test_prefill_matches_gpu_decode_loop():
+    # The same tokens through T single-token decodes on the GPU give the same result.
+    torch = _torch()
+    cfg = bx.make_cfg()
+    seed, T = inputs.seed_for(3) + 99, 70
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, T)
+    st = inputs.initial_states(cfg, seed, 1)
+    cs, s, o, _ = gpu_prefill(cfg, [0, T], tok, p, st)
+    d_cs, d_st = dev(st["conv_state"]), dev(st["state"])
+    d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
+    od = torch.empty(1, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    outs = []
+    for t in range(T):
+        assert bx.ix_gdn_decode(cfg, 1, dev(tok["x"][t:t + 1]), d_cs, d_w, dev(tok["a"][t:t + 1]),
+                                dev(tok["b"][t:t + 1]), d_A, d_dt, d_st, od, None) == 0
+        outs.append(host(od)[0].copy())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(d_cs), cs)
+    assert float(np.max(np.abs(np.stack(outs) - o))) <= TOL_O_ABS
+    assert oracle.rel_err(s, host(d_st)) <= TOL_STATE_REL
+
+
+def test_config4_varlen_prefill_then_decode():
+    # configuration 4: 32 sequences, lengths ~ U[1, L], initial states N(0, 0.02), then 32
+    # decode steps per sequence from the carried conv and recurrent states. The full
+    # configuration draws lengths up to 2048; 512 keeps the double oracle to seconds.
+    torch = _torch()
+    cfg = bx.make_cfg()
+    seed, n, steps = inputs.seed_for(4), 32, 32
+    cu = inputs.varlen(seed, n, 1, 512)
+    T = int(cu[-1])
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, T)
+    st = inputs.initial_states(cfg, seed, n)
+    cs, s, o, _ = gpu_prefill(cfg, cu, tok, p, st)
+    rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    assert oracle.rel_err(s, rs) <= TOL_STATE_REL
+    assert float(np.max(np.abs(o - ro))) <= TOL_O_ABS
+    d_cs, d_st = dev(cs), dev(s)
+    d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
+    od = torch.empty(n, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    for k in range(steps):
+        t = inputs.token_inputs(cfg, seed, n, step=1000 + k)
+        assert bx.ix_gdn_decode(cfg, n, dev(t["x"]), d_cs, d_w, dev(t["a"]), dev(t["b"]), d_A, d_dt, d_st, od,
+                                None) == 0
+        rcs, rs, rod = oracle.decode(cfg, n, t["x"], rcs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], rs,
+                                     nthreads=NT)
+        torch.cuda.synchronize()
+        assert float(np.max(np.abs(host(od) - rod))) <= TOL_O_ABS, k
+    np.testing.assert_array_equal(host(d_cs), rcs)
+    assert oracle.rel_err(host(d_st), rs) <= TOL_STATE_REL
+
+
+def test_state_only_and_repeatable():
+    cfg = bx.make_cfg()
+    seed = inputs.seed_for(3) + 5
+    cu = [0, 100, 229]
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, 229)
+    st = inputs.initial_states(cfg, seed, 2)
+    a = gpu_prefill(cfg, cu, tok, p, st)
+    b = gpu_prefill(cfg, cu, tok, p, st, outputs=())
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])        # deterministic, outputs optional
+
+
+def test_non_monotone_cu_seqlens_is_clamped_in_bounds():
+    # A decreasing offset is clamped to a running maximum (an empty sequence); nothing is
+    # read or written outside the buffers and the other sequences are unaffected.
+    cfg = bx.make_cfg(h_k=2, h_v=4)
+    seed = inputs.seed_for(4) + 1
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, 90)
+    st = inputs.initial_states(cfg, seed, 3)
+    cs, s, o, _ = gpu_prefill(cfg, [0, 40, 30, 90], tok, p, st)
+    rcs, rs, ro = oracle_prefill(cfg, [0, 40, 40, 90], tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    assert oracle.rel_err(s, rs) <= TOL_STATE_REL
+    assert float(np.max(np.abs(o - ro))) <= TOL_O_ABS
