@@ -1,18 +1,20 @@
 #!/usr/bin/env python3
-"""Benchmark of the GDN decode hot path on one MI355X.
+"""Benchmark of the GDN path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--batch 64] [--layers 4]
+    python bench.py [--steps K] [--warmup W] [--batch 64] [--layers 4] [--no-cpu]
 
-Workload (configuration 2 of the benchmark set): batched GDN decode, B = 64 independent
-sequences, 16 q/k heads and 32 v heads, d_k = d_v = 128, fp32 state 128 MiB per layer,
-fused conv (4 taps over 8192 channels), one ix_gdn_decode launch per step. A "step" is one
-decode token for all B sequences of one layer; steps rotate over --layers independent layers
-(state, conv state, weights), so the working set (4 x 128 MiB) exceeds the 256 MB Infinity
-Cache and the state really streams from HBM. Inputs are synthetic, resident in HBM before the
-timed region. Every kernel launch is bracketed by HIP events on the launch stream.
+Headline workload (configuration 2 of the benchmark set): batched GDN decode, B = 64
+independent sequences, 16 q/k heads and 32 v heads, d_k = d_v = 128, fp32 state 128 MiB per
+layer, fused conv (4 taps over 8192 channels), one ix_gdn_decode launch per step. A "step" is
+one decode token for all B sequences of one layer; steps rotate over --layers independent
+layers (state, conv state, weights), so the working set (4 x 128 MiB) exceeds the 256 MB
+Infinity Cache and the state really streams from HBM. Inputs are synthetic and resident in
+HBM before the timed region, which is bracketed by HIP events on the launch stream.
 
-Prints one JSON line: decode tokens/s (value), the state-traffic roofline of the decode
-kernel, and the oracle (CPU port of the reference recurrence) timed on this host.
+Also reported on the same line: decode latency at B = 1 (configuration 1), chunked prefill
+of one 4096-token sequence (configuration 3) with its MFMA roofline fraction, the measured
+in-place HBM ceiling of the box, and the CPU oracle (a C port of the reference's recurrence)
+timed on this host over bounded samples of the same workloads.
 """
 from __future__ import annotations
 
@@ -108,6 +110,93 @@ def decode_bench(args):
     )
 
 
+def decode_latency(iters=200):
+    """Configuration 1: one decode token at B = 1 (2 MiB state), microseconds per call."""
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6D4E0001)
+    C, hv = cfg.channels, cfg.h_v
+    w = (torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    A_log = torch.rand(hv, generator=g, device=dev) * 2.77
+    dt = torch.randn(hv, generator=g, device=dev) * 0.1
+    st = torch.randn(1, hv, 128, 128, generator=g, device=dev) * 0.02
+    cs = torch.randn(1, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16)
+    x = torch.randn(1, C, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty(1, hv, 128, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(20):
+        bx.check("ix_gdn_decode", bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, stream))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    rcs = [bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, stream) for _ in range(iters)]
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for rc in rcs:
+        bx.check("ix_gdn_decode", rc)
+    return round(e0.elapsed_time(e1) * 1e3 / iters, 2)
+
+
+PREFILL_FLOP_PER_TOKEN = 5_767_168     # 2C^2(3d_k+2d_v) + 6 C d_k d_v per (v head, chunk of 64) / 64, x 32 heads
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_bench(T=4096, iters=10):
+    """Configuration 3: ix_gdn_prefill of one T-token sequence from a zero state."""
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6D4E0003)
+    C, hv = cfg.channels, cfg.h_v
+    w = (torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16)
+    A_log = torch.rand(hv, generator=g, device=dev) * 2.77
+    dt = torch.randn(hv, generator=g, device=dev) * 0.1
+    x = torch.randn(T, C, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    st = torch.zeros(1, hv, 128, 128, device=dev)
+    cs = torch.zeros(1, C, cfg.d_conv - 1, dtype=torch.bfloat16, device=dev)
+    o = torch.empty(T, hv, 128, dtype=torch.bfloat16, device=dev)
+    need = bx.ix_gdn_prefill_workspace_size(cfg, 1, T)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def run():
+        st.zero_()
+        cs.zero_()
+        return bx.ix_gdn_prefill(cfg, 1, T, cu, x, cs, w, a, b, A_log, dt, st, None, o, ws, need, stream)
+
+    for _ in range(2):
+        bx.check("ix_gdn_prefill", run())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the zero fills of the state and conv state (2.1 MB) are inside the region
+    e0.record(stream)
+    rcs = [run() for _ in range(iters)]
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for rc in rcs:
+        bx.check("ix_gdn_prefill", rc)
+    sec = e0.elapsed_time(e1) / 1e3 / iters
+    tflops = PREFILL_FLOP_PER_TOKEN * T / sec / 1e12
+    return dict(T=T, tokens_per_s=round(T / sec, 1), us_per_call=round(sec * 1e6, 1),
+                mfma=dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                          frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)),
+                workspace_mib=round(need / 2 ** 20, 1))
+
+
 def hbm_ceiling(nbuf=4, mib=128, iters=20):
     """Measured in-place read+write rate of the box: torch's x.mul_(1) over nbuf rotated
     128 MiB buffers (the decode state's traffic pattern, MALL defeated)."""
@@ -158,9 +247,21 @@ def cpu_baseline(args):
         out[cores] = (B * steps / el, steps, el)
     best = max(out)
     v, steps, el = out[best]
+    # prefill: token-by-token recurrence of one sequence (configuration 3's shape), bounded sample
+    Tp = 256
+    tok = inputs.token_inputs(cfg, inputs.seed_for(3), Tp)
+    st0 = inputs.initial_states(cfg, inputs.seed_for(3), 1, state_std=0.0, conv_std=0.0)
+    pre = {}
+    for cores in sorted({1, ncores}):
+        t0 = time.perf_counter()
+        oracle.prefill(cfg, [0, Tp], tok["x"], st0["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
+                       p["dt_bias"], st0["state"], nthreads=cores)
+        pre[cores] = Tp / (time.perf_counter() - t0)
     return dict(value=round(v, 1), unit="tokens/s", cores=best, kind="port",
                 sample=f"B={B} decode, {steps} steps in {el:.1f} s on {best} threads (oracle/gdn_oracle.c, double)",
-                value_1core=round(out[1][0], 1))
+                value_1core=round(out[1][0], 1),
+                prefill_tokens_per_s=round(pre[best], 1), prefill_tokens_per_s_1core=round(pre[1], 1),
+                prefill_sample=f"one sequence of {Tp} tokens, token-by-token recurrence")
 
 
 def main():
@@ -176,10 +277,12 @@ def main():
         sys.exit(1)
     torch.cuda.synchronize()
     d = decode_bench(args)
+    lat = decode_latency()
+    pf = prefill_bench()
     ceiling = hbm_ceiling()
     cpu = None if args.no_cpu else cpu_baseline(args)
     line = {
-        "metric": "GDN decode tokens/s at B=64 (32 v-heads, 128x128 fp32 state) + state HBM GB/s",
+        "metric": "GDN decode tokens/s + state HBM GB/s (%peak) at B=64; prefill tok/s T=4096",
         "value": round(d["tokens_per_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -195,7 +298,10 @@ def main():
                                f"{args.layers} layers rotated (state {args.layers}x128 MiB)",
                    "B": args.batch, "layers": args.layers, "parallelism": "single-gpu"},
         "avg_kernel_us": round(d["avg_kernel_us"], 2),
+        "state_gbs": d["roofline"]["achieved"],
         "hbm_inplace_ceiling_gbs": ceiling,
+        "decode_b1_us_per_token": lat,
+        "prefill": pf,
         "roofline": d["roofline"],
         "cpu_baseline": cpu,
     }
