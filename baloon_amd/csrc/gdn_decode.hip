@@ -51,27 +51,70 @@ __device__ __forceinline__ float rowgroup_sum(float v) {
     return pair_sum32(pair_sum16(v));
 }
 
-// Conv of one channel of sequence bseq: reads and shifts its bf16 history in place.
-__device__ __forceinline__ float conv_step_channel(const DecodeParams& p, int bseq, int ch) {
-    const Layer& L = p.L;
-    const size_t row = (size_t)bseq * L.C + ch;
-    uint16_t* st = p.conv_state + row * (L.dc - 1);
-    const uint16_t xu = p.x[row];
-    uint16_t hu[3];
-    float hist[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        hu[i] = (i < L.dc - 1) ? st[i] : (uint16_t)0;
-        hist[i] = bf16_to_f32(hu[i]);
-    }
-    const float y = conv_eval(L, hist, bf16_to_f32(xu), L.conv_w + (size_t)ch * L.dc);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-        if (i < L.dc - 2) st[i] = hu[i + 1];
-    st[L.dc - 2] = xu;
-    return y;
+// Conv inputs of two adjacent channels (ch even) of one sequence, as dwords: x of both,
+// the (DC-1)-entry bf16 histories of ch then ch+1, and their DC bf16 weights each. Every
+// access is 4-byte aligned because C, ch and the row offsets are even.
+template <int DC>
+struct ConvPair {
+    uint32_t x;
+    uint32_t h[DC - 1];
+    uint32_t w[DC];
+};
+
+__device__ __forceinline__ uint16_t u16_at(const uint32_t* a, int e) {
+    return (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
 }
 
+template <int DC>
+__device__ __forceinline__ void conv_pair_load(const DecodeParams& p, int bseq, int ch, ConvPair<DC>& c) {
+    const size_t row = (size_t)bseq * p.L.C + ch;
+    c.x = *reinterpret_cast<const uint32_t*>(p.x + row);
+    const uint32_t* hp = reinterpret_cast<const uint32_t*>(p.conv_state + row * (DC - 1));
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) c.h[i] = hp[i];
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(p.L.conv_w + (size_t)ch * DC);
+#pragma unroll
+    for (int i = 0; i < DC; ++i) c.w[i] = wp[i];
+}
+
+// Conv outputs of the pair (the same accumulation order as conv_eval) and the shifted
+// histories written back in place.
+template <int DC>
+__device__ __forceinline__ void conv_pair_apply(const DecodeParams& p, int bseq, int ch, const ConvPair<DC>& c,
+                                                float* y0, float* y1) {
+    const uint16_t xs[2] = {(uint16_t)(c.x & 0xffff), (uint16_t)(c.x >> 16)};
+    uint16_t nh[2 * (DC - 1)];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DC - 1; ++i)
+            acc = fmaf(bf16_to_f32(u16_at(c.h, q * (DC - 1) + i)), bf16_to_f32(u16_at(c.w, q * DC + i)), acc);
+        acc = fmaf(bf16_to_f32(xs[q]), bf16_to_f32(u16_at(c.w, q * DC + DC - 1)), acc);
+        if (p.L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
+        *(q == 0 ? y0 : y1) = acc;
+#pragma unroll
+        for (int i = 0; i < DC - 2; ++i) nh[q * (DC - 1) + i] = u16_at(c.h, q * (DC - 1) + i + 1);
+        nh[q * (DC - 1) + DC - 2] = xs[q];
+    }
+    const size_t row = (size_t)bseq * p.L.C + ch;
+    uint32_t* hp = reinterpret_cast<uint32_t*>(p.conv_state + row * (DC - 1));
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) hp[i] = (uint32_t)nh[2 * i] | ((uint32_t)nh[2 * i + 1] << 16);
+}
+
+// Channel pair e of group (bseq, src): pairs 0..63 are q, 64..127 k, then 64 per mapped v head.
+// Writes the conv outputs into q_s / k_s / v_s.
+__device__ __forceinline__ int pair_channel(const Layer& L, int src, int e, float*& dst,
+                                            float* q_s, float* k_s, float (*v_s)[kD]) {
+    if (e < 64) { dst = q_s + 2 * e; return q_channel(L, src, 2 * e); }
+    if (e < 128) { dst = k_s + 2 * (e - 64); return k_channel(L, src, 2 * (e - 64)); }
+    const int t = (e - 128) / 64, j = 2 * ((e - 128) % 64);
+    dst = v_s[t] + j;
+    return v_channel(L, mapped_head(L, src, t), j);
+}
+
+template <int DC>
 __global__ void __launch_bounds__(kThreads)
 decode_kernel(const DecodeParams p) {
     __shared__ __align__(16) float q_s[kD], k_s[kD];
@@ -102,22 +145,26 @@ decode_kernel(const DecodeParams p) {
         }
     };
 
+    // Conv over q, k of src and v of every mapped head, by channel pairs: the first pair of
+    // each thread is loaded before the state so its inputs return first.
+    const int npairs = 128 + count * 64;
+    float* dst0;
+    const int ch0 = tid < npairs ? pair_channel(L, src, tid, dst0, q_s, k_s, v_s) : 0;
+    ConvPair<DC> cp;
+    if (tid < npairs) conv_pair_load<DC>(p, bseq, ch0, cp);
+
     v4f s0[kRowsPerThread], s1[kRowsPerThread], s2[kRowsPerThread];
     load_slab(s0, 0);
     load_slab(s1, 1);
     load_slab(s2, 2);
 
-    // Conv over q, k of src and v of every mapped head; gates of every mapped head.
-    const int nch = 2 * kD + count * kD;
-    for (int e = tid; e < nch; e += kThreads) {
-        if (e < kD) {
-            q_s[e] = conv_step_channel(p, bseq, q_channel(L, src, e));
-        } else if (e < 2 * kD) {
-            k_s[e - kD] = conv_step_channel(p, bseq, k_channel(L, src, e - kD));
-        } else {
-            const int t = (e - 2 * kD) / kD, j = (e - 2 * kD) % kD;
-            v_s[t][j] = conv_step_channel(p, bseq, v_channel(L, mapped_head(L, src, t), j));
-        }
+    if (tid < npairs) conv_pair_apply<DC>(p, bseq, ch0, cp, dst0, dst0 + 1);
+    for (int e = tid + kThreads; e < npairs; e += kThreads) {      // more than 2 v heads per q/k head
+        float* dst;
+        const int ch = pair_channel(L, src, e, dst, q_s, k_s, v_s);
+        ConvPair<DC> c2;
+        conv_pair_load<DC>(p, bseq, ch, c2);
+        conv_pair_apply<DC>(p, bseq, ch, c2, dst, dst + 1);
     }
     if (tid < count) {
         const int h = mapped_head(L, src, tid);
@@ -244,10 +291,18 @@ extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t
     if ((reinterpret_cast<uintptr_t>(state) & 15) || (o && (reinterpret_cast<uintptr_t>(o) & 15)) ||
         (o_bf16 && (reinterpret_cast<uintptr_t>(o_bf16) & 7)))
         return hipErrorInvalidValue;                 // float4 / uint2 accesses
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(conv_state) |
+         reinterpret_cast<uintptr_t>(conv_w)) & 3)
+        return hipErrorInvalidValue;                 // conv inputs are read as dwords
     ixg::DecodeParams p;
     p.L = ixg::make_layer(cfg, conv_w, A_log, dt_bias);
     p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
-    hipLaunchKernelGGL(ixg::decode_kernel, dim3((unsigned)cfg->h_k, (unsigned)B), dim3(ixg::kThreads), 0, s, p);
+    const dim3 grid((unsigned)cfg->h_k, (unsigned)B), block(ixg::kThreads);
+    switch (cfg->d_conv) {
+        case 2: hipLaunchKernelGGL(ixg::decode_kernel<2>, grid, block, 0, s, p); break;
+        case 3: hipLaunchKernelGGL(ixg::decode_kernel<3>, grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL(ixg::decode_kernel<4>, grid, block, 0, s, p); break;
+    }
     return hipGetLastError();
 }
