@@ -30,7 +30,8 @@ ACT_SILU = 1
 # Every symbol include/ix_gdn.h declares.
 EXPORTS = (
     "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
-    "ix_gdn_channels", "ix_gdn_decode", "ix_gdn_prefill_workspace_size", "ix_gdn_prefill",
+    "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
+    "ix_gdn_prefill",
     "ix_gdn_version",
 )
 
@@ -81,7 +82,8 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_beta_gate": ([P, I, P], I),
         "ix_gdn_out_norm": ([P, P, P, P, I, I, F, P], I),
         "ix_gdn_channels": ([P], I),
-        "ix_gdn_decode": ([P, I, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_gdn_decode_workspace_size": ([P, I], Z),
+        "ix_gdn_decode": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_prefill_workspace_size": ([P, I, I], Z),
         "ix_gdn_prefill": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
@@ -142,11 +144,20 @@ def ix_gdn_out_norm(o, z, ssm_norm, y, h_v, S, eps, s=None) -> int:
 
 # ---- fused layer entry points ------------------------------------------------------------------
 
+def ix_gdn_decode_workspace_size(cfg: Cfg, B: int) -> int:
+    return lib().ix_gdn_decode_workspace_size(ctypes.byref(cfg), B)
+
+
 def ix_gdn_decode(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
-                  s=None) -> int:
-    """One decode token for B sequences. bf16 tensors may be torch.bfloat16 or int16/uint16 bits."""
+                  workspace=None, s=None) -> int:
+    """One decode token for B sequences. bf16 tensors may be torch.bfloat16 or int16/uint16 bits.
+
+    state is [B][h_v][d_v][d_k] fp32 (each head's state stored column by column). workspace,
+    if given, is a zero-filled device buffer of ix_gdn_decode_workspace_size(cfg, B) bytes
+    (left zeroed by every call); it selects the faster many-workgroup kernel."""
     return lib().ix_gdn_decode(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b),
-                               _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), _stream(s))
+                               _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), _ptr(workspace),
+                               _stream(s))
 
 
 def ix_gdn_prefill_workspace_size(cfg: Cfg, n_seq: int, total_T: int) -> int:

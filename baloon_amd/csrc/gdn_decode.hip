@@ -6,33 +6,37 @@
 // the delta-rule update of the fp32 state with output o = S'^T q. The reference does these
 // as separate launches (src/ix_gdn.cu:58-70, :73-84, :102-105, :25-56) and has no batch.
 //
-// Work decomposition: one 256-thread workgroup per (sequence b, q/k head src). It owns the
-// q and k channels of src and every v head mapped to src, so each conv-state channel and
-// each state element is read and written by exactly one workgroup: the in-place updates
-// are race free without any cross-workgroup synchronisation.
+// State layout: [B][h_v][d_v][d_k], i.e. each head's S (d_k x d_v) is stored column by
+// column, so column j (all 128 k indices) is one contiguous 512-byte run. A column is a
+// complete unit of the update:
+//   u_j = g S_j . k,  d_j = beta (v_j - u_j),  S_j' = g S_j + d_j k,  o_j = g S_j . q + d_j (k . q)
+// (the output identity lets one sweep produce both contractions, so every state element is
+// read once and written once; ~0.9 FLOP per byte, HBM-bound). Lane l of a wave holds k
+// indices 4 (l & 31) .. +3 of column (l >> 5) of a pair of adjacent columns: every wave
+// load/store instruction moves 1 KiB of contiguous state, and the column sums are
+// in-wave reductions over 32 lanes (DPP within rows, v_permlane16_swap across them).
 //
-// The state is the traffic (2 x 64 KiB per v head per token, ~0.9 FLOP/B): HBM-bound. A
-// workgroup streams its tiles as 16 KiB slabs of 128 rows x 32 columns. Columns are
-// independent in the update, so a slab is a complete unit of work:
-//   u = g S^T k,  d = beta (v - u),  S' = g S + k d^T,  o = g S^T q + d (k . q)
-// (the output identity lets one sweep produce both contractions, so every state element
-// is read once and written once). Thread (c4 = tid & 7, r0 = tid >> 3) holds float4 column
-// group c4 of rows r0 + 32 m, m = 0..3: each wave load/store instruction moves 8 full
-// 128-byte lines. Column sums are reduced in-thread over 4 rows, across the 8 row groups of
-// a wave with DPP row_ror and v_permlane16/32_swap, and across the 4 waves through LDS.
-// Slabs are loaded two ahead of the one being processed (the first ones before the conv,
-// so HBM latency overlaps it), with nontemporal loads and stores: the state is streamed
-// once per token and never reused from cache.
+// Two kernels, chosen by the launcher:
+//  * slab_kernel (a workspace of per-group counters is given): one workgroup per
+//    (sequence, v head, 64-column half tile), 4096 workgroups at B=64 for a short,
+//    well-balanced stream. Every workgroup evaluates the q/k conv of its q/k head
+//    read-only; the conv history of those channels is written back by the last workgroup
+//    of the (sequence, q/k head) group to finish reading it, found with one atomic counter
+//    per group. The counter is reset by that workgroup, so the workspace is all zeros
+//    again when the kernel ends. No workgroup ever waits for another.
+//  * group_kernel (no workspace): one workgroup per (sequence, q/k head) that owns every
+//    channel and tile of the group; race free by ownership.
+// State loads use nontemporal hints and are issued right after the conv inputs so that
+// HBM latency overlaps the conv; the state is streamed once per token.
 #include "gdn_common.h"
 
 namespace ixg {
 namespace {
 
 constexpr int kThreads = 256;                        // 4 waves
-constexpr int kSlabCols = 32;                        // state columns per slab
-constexpr int kSlabsPerTile = kD / kSlabCols;        // 4
-constexpr int kRowsPerThread = kD / (kThreads / 8);  // 4: rows r0 + 32 m
 constexpr int kMaxHeadsPerGroup = 16;                // v heads per q/k head
+constexpr int kHalfCols = 64;                        // columns per slab_kernel workgroup
+constexpr int kPairsPerWave = kHalfCols / 2 / (kThreads / kWave);   // 8 column pairs
 
 struct DecodeParams {
     Layer L;
@@ -40,16 +44,13 @@ struct DecodeParams {
     uint16_t* conv_state;       // [B][C][dc-1]
     const uint16_t* a;          // [B][h_v]
     const uint16_t* b;          // [B][h_v]
-    float* state;               // [B][h_v][128][128]
+    float* state;               // [B][h_v][d_v][d_k]
     float* o;                   // [B][h_v][128] or null
     uint16_t* o_bf16;           // [B][h_v][128] or null
 };
 
-// Sum over the 8 row groups of a wave (lanes that share lane & 7), result in every lane.
-__device__ __forceinline__ float rowgroup_sum(float v) {
-    v += dpp_f32<kDppRowRor8>(v);
-    return pair_sum32(pair_sum16(v));
-}
+// Sum over the 32 lanes of each half wave, result in all of them.
+__device__ __forceinline__ float half_sum(float v) { return pair_sum16(row_sum16(v)); }
 
 // Conv inputs of two adjacent channels (ch even) of one sequence, as dwords: x of both,
 // the (DC-1)-entry bf16 histories of ch then ch+1, and their DC bf16 weights each. Every
@@ -77,13 +78,13 @@ __device__ __forceinline__ void conv_pair_load(const DecodeParams& p, int bseq, 
     for (int i = 0; i < DC; ++i) c.w[i] = wp[i];
 }
 
-// Conv outputs of the pair (the same accumulation order as conv_eval) and the shifted
-// histories written back in place.
+// Conv outputs of the pair (the accumulation order of conv_eval) and the shifted histories
+// (each channel's history minus its oldest entry, then x), packed as dwords.
 template <int DC>
-__device__ __forceinline__ void conv_pair_apply(const DecodeParams& p, int bseq, int ch, const ConvPair<DC>& c,
-                                                float* y0, float* y1) {
+__device__ __forceinline__ void conv_pair_eval(const Layer& L, const ConvPair<DC>& c, float& y0, float& y1,
+                                               uint32_t (&nh)[DC - 1]) {
     const uint16_t xs[2] = {(uint16_t)(c.x & 0xffff), (uint16_t)(c.x >> 16)};
-    uint16_t nh[2 * (DC - 1)];
+    uint16_t n16[2 * (DC - 1)];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         float acc = 0.0f;
@@ -91,20 +92,134 @@ __device__ __forceinline__ void conv_pair_apply(const DecodeParams& p, int bseq,
         for (int i = 0; i < DC - 1; ++i)
             acc = fmaf(bf16_to_f32(u16_at(c.h, q * (DC - 1) + i)), bf16_to_f32(u16_at(c.w, q * DC + i)), acc);
         acc = fmaf(bf16_to_f32(xs[q]), bf16_to_f32(u16_at(c.w, q * DC + DC - 1)), acc);
-        if (p.L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
-        *(q == 0 ? y0 : y1) = acc;
+        if (L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
+        (q == 0 ? y0 : y1) = acc;
 #pragma unroll
-        for (int i = 0; i < DC - 2; ++i) nh[q * (DC - 1) + i] = u16_at(c.h, q * (DC - 1) + i + 1);
-        nh[q * (DC - 1) + DC - 2] = xs[q];
+        for (int i = 0; i < DC - 2; ++i) n16[q * (DC - 1) + i] = u16_at(c.h, q * (DC - 1) + i + 1);
+        n16[q * (DC - 1) + DC - 2] = xs[q];
     }
-    const size_t row = (size_t)bseq * p.L.C + ch;
-    uint32_t* hp = reinterpret_cast<uint32_t*>(p.conv_state + row * (DC - 1));
 #pragma unroll
-    for (int i = 0; i < DC - 1; ++i) hp[i] = (uint32_t)nh[2 * i] | ((uint32_t)nh[2 * i + 1] << 16);
+    for (int i = 0; i < DC - 1; ++i) nh[i] = (uint32_t)n16[2 * i] | ((uint32_t)n16[2 * i + 1] << 16);
 }
 
+template <int DC>
+__device__ __forceinline__ void hist_store(const DecodeParams& p, int bseq, int ch, const uint32_t (&nh)[DC - 1]) {
+    uint32_t* hp = reinterpret_cast<uint32_t*>(p.conv_state + ((size_t)bseq * p.L.C + ch) * (DC - 1));
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) hp[i] = nh[i];
+}
+
+// Gate and beta of head h of sequence bseq.
+__device__ __forceinline__ void gates(const DecodeParams& p, int bseq, int h, float* gb) {
+    const size_t ab = (size_t)bseq * p.L.h_v + h;
+    gb[0] = expf(log_gate(p.L, h, bf16_to_f32(p.a[ab])));
+    gb[1] = sigmoid_f(bf16_to_f32(p.b[ab]));
+}
+
+// The column update for one pair of columns held as one float4 per lane (see the header).
+// kr, qr: this lane's 4 entries of the normalised k and q; vj: v of this lane's column.
+__device__ __forceinline__ void column_update(const DecodeParams& p, v4f s, v4f* dst, const v4f& kr, const v4f& qr,
+                                              float vj, float g, float bt, float kq, size_t o_index, bool writer) {
+    float ak = s[0] * kr[0], aq = s[0] * qr[0];
+#pragma unroll
+    for (int e = 1; e < 4; ++e) { ak = fmaf(s[e], kr[e], ak); aq = fmaf(s[e], qr[e], aq); }
+    ak = half_sum(ak);
+    aq = half_sum(aq);
+    const float d = (vj - g * ak) * bt;
+    v4f r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[e], d, s[e] * g);
+    __builtin_nontemporal_store(r, dst);
+    if (writer) {
+        const float ov = fmaf(d, kq, g * aq);
+        if (p.o) p.o[o_index] = ov;
+        if (p.o_bf16) p.o_bf16[o_index] = f32_to_bf16(ov);
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// slab_kernel: grid (2 h_v, B); workgroup = (sequence bseq, v head h, half tile hf)
+// ---------------------------------------------------------------------------------------
+template <int DC>
+__global__ void __launch_bounds__(kThreads)
+slab_kernel(const DecodeParams p, int* __restrict__ counters) {
+    __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kHalfCols];
+    __shared__ float scal_s[2], gb_s[2];
+    __shared__ int last_s;
+
+    const Layer& L = p.L;
+    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int half = lane >> 5, i4 = lane & 31;
+    const int hf = blockIdx.x & 1, h = blockIdx.x >> 1, bseq = blockIdx.y;
+    const int src = src_of(L, h);
+
+    // Conv inputs: threads 0..63 q pairs, 64..127 k pairs, 128..159 the v pairs of this half tile.
+    int ch = 0;
+    float* dst = nullptr;
+    if (tid < 64) { ch = q_channel(L, src, 2 * tid); dst = q_s + 2 * tid; }
+    else if (tid < 128) { ch = k_channel(L, src, 2 * (tid - 64)); dst = k_s + 2 * (tid - 64); }
+    else if (tid < 128 + kHalfCols / 2) { ch = v_channel(L, h, hf * kHalfCols + 2 * (tid - 128)); dst = v_s + 2 * (tid - 128); }
+    const bool conv_thread = tid < 128 + kHalfCols / 2;
+    ConvPair<DC> cp;
+    if (conv_thread) conv_pair_load<DC>(p, bseq, ch, cp);
+
+    // State: wave w owns columns hf*64 + 16 w + 2 u + half, u = 0..7.
+    v4f* tile = reinterpret_cast<v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
+    const int j0 = hf * kHalfCols + 2 * kPairsPerWave * w + half;
+    v4f s[kPairsPerWave];
+#pragma unroll
+    for (int u = 0; u < kPairsPerWave; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
+
+    uint32_t nh[DC - 1];
+    float y0 = 0.0f, y1 = 0.0f;
+    if (conv_thread) {
+        conv_pair_eval<DC>(L, cp, y0, y1, nh);
+        dst[0] = y0;
+        dst[1] = y1;
+        if (tid >= 128) hist_store<DC>(p, bseq, ch, nh);          // v channels: owned by this workgroup
+    }
+    if (w < 2) {                                                  // wave 0: q.q, wave 1: k.k
+        const float r = wave_sum(fmaf(y0, y0, y1 * y1));
+        if (lane == 0) scal_s[w] = r;
+    }
+    if (tid == kThreads - 1) gates(p, bseq, h, gb_s);
+    __syncthreads();
+
+    // Every thread's reads of the q/k conv history are complete: count this workgroup in.
+    if (tid == 0) {
+        const int members = mapped_count(L, src) * 2;
+        last_s = atomicAdd(counters + (size_t)bseq * L.h_k + src, 1) == members - 1;
+    }
+    const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
+    const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
+    const float kq = wave_sum(fmaf(q_s[lane], k_s[lane], q_s[lane + kWave] * k_s[lane + kWave])) * inv_q * inv_k;
+    v4f kr, qr;
+    {
+        const v4f kk = *reinterpret_cast<const v4f*>(k_s + 4 * i4), qq = *reinterpret_cast<const v4f*>(q_s + 4 * i4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { kr[e] = kk[e] * inv_k; qr[e] = qq[e] * inv_q; }
+    }
+    const float g = gb_s[0], bt = gb_s[1];
+    const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
+#pragma unroll
+    for (int u = 0; u < kPairsPerWave; ++u) {
+        const int j = j0 + 2 * u;
+        column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0);
+    }
+
+    __syncthreads();
+    if (last_s) {
+        if (tid < 128) hist_store<DC>(p, bseq, ch, nh);
+        if (tid == 0) counters[(size_t)bseq * L.h_k + src] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// group_kernel: grid (h_k, B); workgroup = (sequence bseq, q/k head src), all mapped heads
+// ---------------------------------------------------------------------------------------
+constexpr int kGroupBatch = 4;                       // column pairs per load batch and wave
+
 // Channel pair e of group (bseq, src): pairs 0..63 are q, 64..127 k, then 64 per mapped v head.
-// Writes the conv outputs into q_s / k_s / v_s.
 __device__ __forceinline__ int pair_channel(const Layer& L, int src, int e, float*& dst,
                                             float* q_s, float* k_s, float (*v_s)[kD]) {
     if (e < 64) { dst = q_s + 2 * e; return q_channel(L, src, 2 * e); }
@@ -116,66 +231,57 @@ __device__ __forceinline__ int pair_channel(const Layer& L, int src, int e, floa
 
 template <int DC>
 __global__ void __launch_bounds__(kThreads)
-decode_kernel(const DecodeParams p) {
+group_kernel(const DecodeParams p) {
     __shared__ __align__(16) float q_s[kD], k_s[kD];
     __shared__ __align__(16) float v_s[kMaxHeadsPerGroup][kD];
     __shared__ float gate_s[kMaxHeadsPerGroup][2];
     __shared__ float scal_s[3];
-    __shared__ v4f red_s[2][kThreads / kWave][kSlabCols / 4][2];   // [slab parity][wave][c4][u|q]
 
     const Layer& L = p.L;
     const int src = blockIdx.x, bseq = blockIdx.y;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
-    const int c4 = tid & 7, r0 = tid >> 3;
+    const int half = lane >> 5, i4 = lane & 31;
     const int count = mapped_count(L, src);
-    const int nslab = count * kSlabsPerTile;
+    const int per_wave = count * (kD / 2) / (kThreads / kWave);     // column pairs of this wave
+    const int p0 = w * per_wave;
 
-    // Address of this thread's first element of slab n (rows r0 + 32 m follow at stride 32 rows).
-    auto slab_ptr = [&](int n) -> v4f* {
-        const int h = mapped_head(L, src, n / kSlabsPerTile);
-        float* tile = p.state + ((size_t)bseq * L.h_v + h) * kD * kD;
-        return reinterpret_cast<v4f*>(tile + (size_t)r0 * kD + (n % kSlabsPerTile) * kSlabCols) + c4;
+    // Column pair pr of the group (head slot pr / 64) -> this lane's float4 of it.
+    auto col_ptr = [&](int pr) -> v4f* {
+        const int col = 2 * pr + half, t = col / kD, j = col % kD;
+        return reinterpret_cast<v4f*>(p.state + (((size_t)bseq * L.h_v + mapped_head(L, src, t)) * kD + j) * kD) + i4;
     };
-    auto load_slab = [&](v4f (&buf)[kRowsPerThread], int n) {
-        if (n < nslab) {
-            const v4f* ptr = slab_ptr(n);
+    auto load = [&](v4f (&buf)[kGroupBatch], int base) {
 #pragma unroll
-            for (int m = 0; m < kRowsPerThread; ++m)
-                buf[m] = __builtin_nontemporal_load(ptr + (size_t)m * 32 * (kD / 4));
-        }
+        for (int u = 0; u < kGroupBatch; ++u)
+            if (base + u < per_wave) buf[u] = __builtin_nontemporal_load(col_ptr(p0 + base + u));
     };
 
-    // Conv over q, k of src and v of every mapped head, by channel pairs: the first pair of
-    // each thread is loaded before the state so its inputs return first.
     const int npairs = 128 + count * 64;
     float* dst0;
     const int ch0 = tid < npairs ? pair_channel(L, src, tid, dst0, q_s, k_s, v_s) : 0;
     ConvPair<DC> cp;
     if (tid < npairs) conv_pair_load<DC>(p, bseq, ch0, cp);
-
-    v4f s0[kRowsPerThread], s1[kRowsPerThread], s2[kRowsPerThread];
-    load_slab(s0, 0);
-    load_slab(s1, 1);
-    load_slab(s2, 2);
-
-    if (tid < npairs) conv_pair_apply<DC>(p, bseq, ch0, cp, dst0, dst0 + 1);
+    v4f b0[kGroupBatch], b1[kGroupBatch];
+    load(b0, 0);
+    load(b1, kGroupBatch);
+    if (tid < npairs) {
+        uint32_t nh[DC - 1];
+        conv_pair_eval<DC>(L, cp, dst0[0], dst0[1], nh);
+        hist_store<DC>(p, bseq, ch0, nh);
+    }
     for (int e = tid + kThreads; e < npairs; e += kThreads) {      // more than 2 v heads per q/k head
         float* dst;
         const int ch = pair_channel(L, src, e, dst, q_s, k_s, v_s);
         ConvPair<DC> c2;
+        uint32_t nh[DC - 1];
         conv_pair_load<DC>(p, bseq, ch, c2);
-        conv_pair_apply<DC>(p, bseq, ch, c2, dst, dst + 1);
+        conv_pair_eval<DC>(L, c2, dst[0], dst[1], nh);
+        hist_store<DC>(p, bseq, ch, nh);
     }
-    if (tid < count) {
-        const int h = mapped_head(L, src, tid);
-        const size_t ab = (size_t)bseq * L.h_v + h;
-        gate_s[tid][0] = expf(log_gate(L, h, bf16_to_f32(p.a[ab])));
-        gate_s[tid][1] = sigmoid_f(bf16_to_f32(p.b[ab]));
-    }
+    if (tid < count) gates(p, bseq, mapped_head(L, src, tid), gate_s[tid]);
     __syncthreads();
 
-    // q.q, k.k, q.k over the 128 dims (one wave each).
-    if (w < 3) {
+    if (w < 3) {                                                  // q.q, k.k, q.k
         const float* x0 = (w == 1) ? k_s : q_s;
         const float* x1 = (w == 0) ? q_s : k_s;
         const float r = wave_sum(fmaf(x0[lane], x1[lane], x0[lane + kWave] * x1[lane + kWave]));
@@ -185,74 +291,26 @@ decode_kernel(const DecodeParams p) {
     const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
     const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
     const float kq = scal_s[2] * inv_q * inv_k;
-    float kr[kRowsPerThread], qr[kRowsPerThread];
+    v4f kr, qr;
 #pragma unroll
-    for (int m = 0; m < kRowsPerThread; ++m) {
-        kr[m] = k_s[r0 + 32 * m] * inv_k;
-        qr[m] = q_s[r0 + 32 * m] * inv_q;
-    }
+    for (int e = 0; e < 4; ++e) { kr[e] = k_s[4 * i4 + e] * inv_k; qr[e] = q_s[4 * i4 + e] * inv_q; }
 
-    // One slab: column sums, update, write back, output.
-    auto process = [&](v4f (&buf)[kRowsPerThread], int n) {
-        const int t = n / kSlabsPerTile, sc = n % kSlabsPerTile;
-        v4f ak = {0.f, 0.f, 0.f, 0.f}, aq = ak;
+    auto process = [&](v4f (&buf)[kGroupBatch], int base) {
 #pragma unroll
-        for (int m = 0; m < kRowsPerThread; ++m) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                ak[e] = fmaf(buf[m][e], kr[m], ak[e]);
-                aq[e] = fmaf(buf[m][e], qr[m], aq[e]);
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { ak[e] = rowgroup_sum(ak[e]); aq[e] = rowgroup_sum(aq[e]); }
-        if (lane < 8) { red_s[n & 1][w][c4][0] = ak; red_s[n & 1][w][c4][1] = aq; }
-        __syncthreads();
-        v4f A = red_s[n & 1][0][c4][0], Q = red_s[n & 1][0][c4][1];
-#pragma unroll
-        for (int ww = 1; ww < kThreads / kWave; ++ww) { A += red_s[n & 1][ww][c4][0]; Q += red_s[n & 1][ww][c4][1]; }
-        const float g = gate_s[t][0], bt = gate_s[t][1];
-        const v4f vv = *reinterpret_cast<const v4f*>(&v_s[t][sc * kSlabCols + 4 * c4]);
-        v4f d;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = (vv[e] - g * A[e]) * bt;
-        v4f* ptr = slab_ptr(n);
-#pragma unroll
-        for (int m = 0; m < kRowsPerThread; ++m) {
-            v4f r;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[m], d[e], buf[m][e] * g);
-            __builtin_nontemporal_store(r, ptr + (size_t)m * 32 * (kD / 4));
-        }
-        if (r0 == 0) {
-            v4f ov;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ov[e] = fmaf(d[e], kq, g * Q[e]);
-            const int h = mapped_head(L, src, t);
-            const size_t oo = ((size_t)bseq * L.h_v + h) * kD + sc * kSlabCols + 4 * c4;
-            if (p.o) *reinterpret_cast<v4f*>(p.o + oo) = ov;
-            if (p.o_bf16) {
-                uint2 pk;
-                pk.x = pack_bf16x2(ov[0], ov[1]);
-                pk.y = pack_bf16x2(ov[2], ov[3]);
-                *reinterpret_cast<uint2*>(p.o_bf16 + oo) = pk;
-            }
+        for (int u = 0; u < kGroupBatch; ++u) {
+            if (base + u >= per_wave) break;
+            const int pr = p0 + base + u, col = 2 * pr + half, t = col / kD, j = col % kD;
+            const size_t oi = ((size_t)bseq * L.h_v + mapped_head(L, src, t)) * kD + j;
+            column_update(p, buf[u], col_ptr(pr), kr, qr, v_s[t][j], gate_s[t][0], gate_s[t][1], kq, oi, i4 == 0);
         }
     };
-
-    // Three rotating slab buffers: the loop body is unrolled so no register is copied
-    // while its load is still in flight.
-    for (int n = 0; n < nslab; n += 3) {
-        process(s0, n);
-        load_slab(s0, n + 3);
-        if (n + 1 < nslab) {
-            process(s1, n + 1);
-            load_slab(s1, n + 4);
-        }
-        if (n + 2 < nslab) {
-            process(s2, n + 2);
-            load_slab(s2, n + 5);
-        }
+    // Two batches in flight; the loop body is unrolled so no register is copied while its
+    // load is outstanding.
+    for (int base = 0; base < per_wave; base += 2 * kGroupBatch) {
+        process(b0, base);
+        load(b0, base + 2 * kGroupBatch);
+        process(b1, base + kGroupBatch);
+        load(b1, base + 3 * kGroupBatch);
     }
 }
 
@@ -263,7 +321,7 @@ extern "C" int ix_gdn_channels(const ix_gdn_cfg* c) {
     return c ? 2 * c->h_k * c->d_k + c->h_v * c->d_v : 0;
 }
 
-extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.2.0 gfx950"; }
+extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.3.0 gfx950"; }
 
 // Shared validation of the fused layer description (also used by the prefill).
 extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
@@ -280,29 +338,49 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
     return hipSuccess;
 }
 
+extern "C" size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B) {
+    if (ix_gdn_check_cfg_(cfg) != hipSuccess || B <= 0 || B > 65535) return 0;
+    return ((size_t)B * cfg->h_k * sizeof(int32_t) + 255) & ~(size_t)255;
+}
+
 extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
                                     const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
                                     const float* A_log, const float* dt_bias, float* state, float* o,
-                                    uint16_t* o_bf16, hipStream_t s) {
+                                    uint16_t* o_bf16, void* workspace, hipStream_t s) {
     const hipError_t e = ix_gdn_check_cfg_(cfg);
     if (e != hipSuccess) return e;
     if (B <= 0 || B > 65535) return hipErrorInvalidValue;
     if (!x || !conv_state || !conv_w || !a || !b || !A_log || !dt_bias || !state) return hipErrorInvalidValue;
-    if ((reinterpret_cast<uintptr_t>(state) & 15) || (o && (reinterpret_cast<uintptr_t>(o) & 15)) ||
-        (o_bf16 && (reinterpret_cast<uintptr_t>(o_bf16) & 7)))
-        return hipErrorInvalidValue;                 // float4 / uint2 accesses
+    if ((reinterpret_cast<uintptr_t>(state) & 15) || (o && (reinterpret_cast<uintptr_t>(o) & 3)) ||
+        (o_bf16 && (reinterpret_cast<uintptr_t>(o_bf16) & 1)))
+        return hipErrorInvalidValue;                 // float4 state accesses
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(conv_state) |
-         reinterpret_cast<uintptr_t>(conv_w)) & 3)
-        return hipErrorInvalidValue;                 // conv inputs are read as dwords
+         reinterpret_cast<uintptr_t>(conv_w) | reinterpret_cast<uintptr_t>(workspace)) & 3)
+        return hipErrorInvalidValue;                 // conv inputs and counters are dwords
     ixg::DecodeParams p;
     p.L = ixg::make_layer(cfg, conv_w, A_log, dt_bias);
     p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
-    const dim3 grid((unsigned)cfg->h_k, (unsigned)B), block(ixg::kThreads);
-    switch (cfg->d_conv) {
-        case 2: hipLaunchKernelGGL(ixg::decode_kernel<2>, grid, block, 0, s, p); break;
-        case 3: hipLaunchKernelGGL(ixg::decode_kernel<3>, grid, block, 0, s, p); break;
-        default: hipLaunchKernelGGL(ixg::decode_kernel<4>, grid, block, 0, s, p); break;
+    // The slab kernel needs every q/k head to feed at least one v head (its history is
+    // written by the group's last member); otherwise, and without a workspace, one
+    // workgroup owns each group.
+    const bool every_src_used = cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
+    const dim3 block(ixg::kThreads);
+    if (workspace && every_src_used) {
+        int* ctr = static_cast<int*>(workspace);
+        const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
+        switch (cfg->d_conv) {
+            case 2: hipLaunchKernelGGL(ixg::slab_kernel<2>, grid, block, 0, s, p, ctr); break;
+            case 3: hipLaunchKernelGGL(ixg::slab_kernel<3>, grid, block, 0, s, p, ctr); break;
+            default: hipLaunchKernelGGL(ixg::slab_kernel<4>, grid, block, 0, s, p, ctr); break;
+        }
+    } else {
+        const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
+        switch (cfg->d_conv) {
+            case 2: hipLaunchKernelGGL(ixg::group_kernel<2>, grid, block, 0, s, p); break;
+            case 3: hipLaunchKernelGGL(ixg::group_kernel<3>, grid, block, 0, s, p); break;
+            default: hipLaunchKernelGGL(ixg::group_kernel<4>, grid, block, 0, s, p); break;
+        }
     }
     return hipGetLastError();
 }

@@ -111,7 +111,7 @@ struct PrefillParams {
     uint16_t* conv_state;       // [n_seq][C][dc-1]
     const uint16_t* a;          // [T][h_v]
     const uint16_t* b;          // [T][h_v]
-    float* state;               // [n_seq][h_v][128][128]
+    float* state;               // [n_seq][h_v][d_v][d_k]
     float* o;                   // [T][h_v][128] or null
     uint16_t* o_bf16;           // [T][h_v][128] or null
     int n_seq, T, NC;
@@ -437,13 +437,12 @@ __global__ void __launch_bounds__(256) chain_kernel(const PrefillParams p) {
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int li = lane & 15, lg4 = lane >> 4;
 
-    // State slice: wave w owns rows 32 w + 16 tt + 4 lg4 + r, column j0 + li.
-    float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD + j0 + li;
+    // State slice: wave w owns rows 32 w + 16 tt + 4 lg4 + r (k index), column j0 + li (v
+    // index); the state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
+    float* st = p.state + (((size_t)s * L.h_v + h) * kD + j0 + li) * kD + 32 * w + 4 * lg4;
     v4 S[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) S[tt][r] = st[(size_t)(32 * w + 16 * tt + 4 * lg4 + r) * kD];
+    for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const v4*>(st + 16 * tt);
 
     const float* qbase = p.ws.qn + (size_t)src * p.T * kD;
     const float* kbase = p.ws.kn + (size_t)src * p.T * kD;
@@ -537,9 +536,7 @@ __global__ void __launch_bounds__(256) chain_kernel(const PrefillParams p) {
     }
 
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) st[(size_t)(32 * w + 16 * tt + 4 * lg4 + r) * kD] = S[tt][r];
+    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(st + 16 * tt) = S[tt];
 }
 
 }  // namespace
@@ -566,6 +563,7 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     if (total_T == 0) return hipSuccess;                       // nothing to consume
     if (!x || !a || !b || !workspace) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(workspace) & 255) return hipErrorInvalidValue;
+    if (reinterpret_cast<uintptr_t>(state) & 15) return hipErrorInvalidValue;      // float4 state accesses
     size_t off[13];
     const size_t need = ws_layout(cfg, n_seq, total_T, off);
     if (workspace_bytes < need) return hipErrorInvalidValue;

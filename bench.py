@@ -68,6 +68,7 @@ def decode_bench(args):
                 a=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16),
                 b=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16)) for _ in range(P)]
     o = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device=dev)   # stream-ordered: shared
     stream = torch.cuda.current_stream()
     lib = bx.lib()
     import ctypes
@@ -78,7 +79,7 @@ def decode_bench(args):
         Ly, In = layers[i % L], ins[i % P]
         return lib.ix_gdn_decode(cfg_ref, B, In["x"].data_ptr(), Ly["cs"].data_ptr(), Ly["w"].data_ptr(),
                                  In["a"].data_ptr(), In["b"].data_ptr(), Ly["A_log"].data_ptr(), Ly["dt"].data_ptr(),
-                                 Ly["state"].data_ptr(), None, o.data_ptr(), s_ptr)
+                                 Ly["state"].data_ptr(), None, o.data_ptr(), ws.data_ptr(), s_ptr)
 
     for i in range(args.warmup):
         bx.check("ix_gdn_decode", launch(i))
@@ -130,13 +131,14 @@ def decode_latency(iters=200):
     a = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
     b = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
     o = torch.empty(1, hv, 128, dtype=torch.bfloat16, device=dev)
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, 1), dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream()
     for _ in range(20):
-        bx.check("ix_gdn_decode", bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, stream))
+        bx.check("ix_gdn_decode", bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, ws, stream))
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    rcs = [bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, stream) for _ in range(iters)]
+    rcs = [bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, ws, stream) for _ in range(iters)]
     e1.record(stream)
     torch.cuda.synchronize()
     for rc in rcs:

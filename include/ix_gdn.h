@@ -84,6 +84,14 @@ typedef struct ix_gdn_cfg {
 /* Mixed-projection channel count C = 2*h_k*d_k + h_v*d_v (order q | k | v). */
 int ix_gdn_channels(const ix_gdn_cfg* cfg);
 
+/* Fused state layout (decode and prefill): [B][h_v][d_v][d_k] fp32 -- each head's state S
+ * (d_k x d_v, S[i][j] with i the k index and j the v index) is stored column by column, so
+ * element (b, h, i, j) is at ((b*h_v + h)*d_v + j)*d_k + i and every column is contiguous. */
+
+/* Bytes of the counter workspace ix_gdn_decode can use for B sequences (B*h_k int32, rounded
+ * up to 256), or 0 for an invalid description. */
+size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B);
+
 /* One decode token for B independent sequences of one GDN layer, in one launch:
  * causal conv over the mixed q|k|v channels with its rolling state, per-head L2 norm of q
  * and k, gates g = exp(-exp(A_log) * softplus(a + dt_bias)) and beta = sigmoid(b), head map
@@ -94,15 +102,18 @@ int ix_gdn_channels(const ix_gdn_cfg* cfg);
  *   conv_w     [C][d_conv] bf16
  *   a, b       [B][h_v] bf16 gate and beta logits
  *   A_log, dt_bias [h_v] fp32
- *   state      [B][h_v][d_k][d_v] fp32 (v index fastest), updated in place
+ *   state      [B][h_v][d_v][d_k] fp32 (layout above), updated in place, 16-byte aligned
  *   o          [B][h_v][d_v] fp32, or NULL
  *   o_bf16     [B][h_v][d_v] bf16 (round to nearest even of the fp32 output), or NULL
- * Each state, conv-state and output element is touched by exactly one workgroup, so the
- * in-place updates are race free. Calls on one stream are ordered; two streams must not
- * share a state or conv-state buffer. */
+ *   workspace  NULL, or ix_gdn_decode_workspace_size(cfg, B) bytes of device memory that are
+ *              all zero before the first call; every call leaves them all zero again. With a
+ *              workspace the state streams through more, shorter workgroups (faster); calls
+ *              that share one workspace must be ordered (same stream), since it holds
+ *              per-call counters. x, conv_state, conv_w and workspace must be 4-byte aligned.
+ * Calls on one stream are ordered; two streams must not share a state or conv-state buffer. */
 hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
                          const uint16_t* conv_w, const uint16_t* a, const uint16_t* b, const float* A_log,
-                         const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
+                         const float* dt_bias, float* state, float* o, uint16_t* o_bf16, void* workspace,
                          hipStream_t s IX_GDN_DEFAULT_STREAM);
 
 /* Bytes of device workspace ix_gdn_prefill needs for n_seq sequences and total_T tokens. */
@@ -112,7 +123,8 @@ size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total
  * total_T applications of ix_gdn_decode:
  *   cu_seqlens [n_seq+1] int32 device offsets (cu_seqlens[0] = 0, non-decreasing)
  *   x [total_T][C] bf16; a, b [total_T][h_v] bf16
- *   conv_state [n_seq][C][d_conv-1] bf16 in/out; state [n_seq][h_v][d_k][d_v] fp32 in/out
+ *   conv_state [n_seq][C][d_conv-1] bf16 in/out; state [n_seq][h_v][d_v][d_k] fp32 in/out
+ *   (16-byte aligned)
  *   o [total_T][h_v][d_v] fp32 or NULL; o_bf16 likewise
  *   workspace: device memory of ix_gdn_prefill_workspace_size() bytes, 256-byte aligned. */
 hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,

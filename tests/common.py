@@ -31,6 +31,16 @@ def host(t) -> np.ndarray:
     return t.numpy()
 
 
+def state_to_dev(st):
+    """Oracle state [..][h_v][d_k][d_v] -> device tensor in the library's [..][h_v][d_v][d_k] layout."""
+    return dev(np.ascontiguousarray(np.swapaxes(np.asarray(st, dtype=np.float32), -1, -2)))
+
+
+def state_from_dev(t) -> np.ndarray:
+    """Device state [..][h_v][d_v][d_k] -> numpy in the oracle's [..][h_v][d_k][d_v] layout."""
+    return np.ascontiguousarray(np.swapaxes(host(t), -1, -2))
+
+
 def bf16_excess_err(got_bits: np.ndarray, ref_f64: np.ndarray) -> float:
     """max(|bf16 - ref| - half a bf16 ulp of ref): the error beyond bf16's own rounding."""
     ref = np.asarray(ref_f64, dtype=np.float64)
@@ -52,4 +62,4 @@ def bf16_ulp_diff(got_bits: np.ndarray, ref_f64: np.ndarray) -> int:
     return int(np.max(np.abs(ordered(g) - ordered(ref_bits)))) if g.size else 0
 
 
-__all__ = ["oracle", "bf16", "inputs", "dev", "host", "bf16_ulp_diff", "bf16_excess_err", "TOL_O_ABS", "TOL_STATE_REL"]
+__all__ = ["oracle", "bf16", "inputs", "dev", "host", "state_to_dev", "state_from_dev", "bf16_ulp_diff", "bf16_excess_err", "TOL_O_ABS", "TOL_STATE_REL"]

@@ -79,14 +79,14 @@ def test_fused_cfg_validation():
     bad = [bx.make_cfg(d_k=64), bx.make_cfg(d_conv=1), bx.make_cfg(d_conv=5), bx.make_cfg(h_k=0),
            bx.make_cfg(head_map=2), bx.make_cfg(h_k=3, h_v=32, head_map=bx.HEAD_DIV), bx.make_cfg(conv_act=7)]
     for c in bad:
-        rc = L.ix_gdn_decode(ctypes.byref(c), 1, *([ctypes.c_void_p(256)] * 8), NULL, NULL, NULL)
+        rc = L.ix_gdn_decode(ctypes.byref(c), 1, *([ctypes.c_void_p(256)] * 8), NULL, NULL, NULL, NULL)
         assert rc == INVALID
     p = ctypes.c_void_p(256)
-    assert L.ix_gdn_decode(ctypes.byref(good), 0, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
-    assert L.ix_gdn_decode(ctypes.byref(good), 1, NULL, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+    assert L.ix_gdn_decode(ctypes.byref(good), 0, p, p, p, p, p, p, p, p, NULL, NULL, NULL, NULL) == INVALID
+    assert L.ix_gdn_decode(ctypes.byref(good), 1, NULL, p, p, p, p, p, p, p, NULL, NULL, NULL, NULL) == INVALID
     assert L.ix_gdn_decode(ctypes.byref(good), 1, p, p, p, p, p, p, p, ctypes.c_void_p(260), NULL, NULL,
-                           NULL) == INVALID           # state must be 16-byte aligned
-    assert L.ix_gdn_decode(None, 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+                           NULL, NULL) == INVALID           # state must be 16-byte aligned
+    assert L.ix_gdn_decode(None, 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL, NULL) == INVALID
 
 
 def test_prefill_validation_without_launch():
@@ -117,6 +117,6 @@ def test_head_group_limit():
     L = bx.lib()
     p = ctypes.c_void_p(256)
     ok, bad = bx.make_cfg(h_k=2, h_v=32), bx.make_cfg(h_k=1, h_v=17)
-    assert L.ix_gdn_decode(ctypes.byref(bad), 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL) == INVALID
+    assert L.ix_gdn_decode(ctypes.byref(bad), 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL, NULL) == INVALID
     assert bx.ix_gdn_prefill_workspace_size(ok, 1, 64) > 0
     assert bx.ix_gdn_prefill_workspace_size(bad, 1, 64) == 0

@@ -4,7 +4,8 @@ Tolerances (written here, from the benchmark's acceptance rule): fp32 outputs wi
 absolute of the double oracle; bf16 outputs bit-exact round-to-nearest-even of the kernel's
 own fp32 outputs, and within 1e-3 absolute of the oracle beyond bf16's own half-ulp
 rounding; fp32 state max|d|/max|ref| <= 1e-4 after the steps (the reference's norm,
-tests/test_gdn.cu:10-13); conv state bit-exact.
+tests/test_gdn.cu:10-13); conv state bit-exact. Both kernels are covered: with a counter workspace (many short
+workgroups, the q/k conv history written by the last member of each group) and without.
 """
 import os
 
@@ -14,7 +15,7 @@ import pytest
 import baloon_amd as bx
 import oracle
 from oracle import bf16, inputs
-from tests.common import TOL_O_ABS, TOL_STATE_REL, bf16_excess_err, dev, host
+from tests.common import TOL_O_ABS, TOL_STATE_REL, bf16_excess_err, dev, host, state_from_dev, state_to_dev
 
 pytestmark = pytest.mark.gpu
 NT = min(8, os.cpu_count() or 1)
@@ -28,13 +29,16 @@ def _torch():
 class Run:
     """Device copies of one layer's parameters and states, plus the oracle's copies."""
 
-    def __init__(self, cfg, B, seed, state_std=0.02, conv_std=1.0):
+    def __init__(self, cfg, B, seed, state_std=0.02, conv_std=1.0, ws=True):
+        torch = _torch()
         self.cfg, self.B, self.seed = cfg, B, seed
         self.p = inputs.layer_params(cfg, seed)
         s = inputs.initial_states(cfg, seed, B, state_std=state_std, conv_std=conv_std)
         self.cs, self.st = s["conv_state"], s["state"].astype(np.float64)
         self.d_w, self.d_A, self.d_dt = dev(self.p["w"]), dev(self.p["A_log"]), dev(self.p["dt_bias"])
-        self.d_cs, self.d_st = dev(s["conv_state"]), dev(s["state"])
+        self.d_cs, self.d_st = dev(s["conv_state"]), state_to_dev(s["state"])
+        self.ws = (torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device="cuda")
+                   if ws else None)
 
     def step(self, t, step_idx):
         torch = _torch()
@@ -42,7 +46,7 @@ class Run:
         o = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
         ob = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
         rc = bx.ix_gdn_decode(cfg, B, dev(t["x"]), self.d_cs, self.d_w, dev(t["a"]), dev(t["b"]), self.d_A,
-                              self.d_dt, self.d_st, o, ob)
+                              self.d_dt, self.d_st, o, ob, self.ws)
         assert rc == 0
         self.cs, self.st, ro = oracle.decode(cfg, B, t["x"], self.cs, self.p["w"], t["a"], t["b"], self.p["A_log"],
                                              self.p["dt_bias"], self.st, nthreads=NT)
@@ -57,9 +61,11 @@ class Run:
         assert ex <= TOL_O_ABS, f"{where} bf16 o err beyond rounding {ex}"
 
     def check_states(self, where=""):
-        rel = oracle.rel_err(host(self.d_st), self.st)
+        rel = oracle.rel_err(state_from_dev(self.d_st), self.st)
         assert rel <= TOL_STATE_REL, f"{where} state rel err {rel}"
         np.testing.assert_array_equal(host(self.d_cs), self.cs)
+        if self.ws is not None:
+            assert int(self.ws.count_nonzero()) == 0, "counter workspace not left zeroed"
 
 
 def run_steps(cfg, B, steps, seed, check_every=1, **kw):
@@ -73,18 +79,24 @@ def run_steps(cfg, B, steps, seed, check_every=1, **kw):
     return r
 
 
-def test_config1_single_token():
+WS = [pytest.param(True, id="workspace"), pytest.param(False, id="no_workspace")]
+
+
+@pytest.mark.parametrize("ws", WS)
+def test_config1_single_token(ws):
     # B=1, 16 q/k heads, 32 v heads, d=128, fused conv over 8192 channels.
-    run_steps(oracle.make_cfg(), 1, 1, inputs.seed_for(1))
+    run_steps(oracle.make_cfg(), 1, 1, inputs.seed_for(1), ws=ws)
 
 
-def test_config2_batch64_short():
+@pytest.mark.parametrize("ws", WS)
+def test_config2_batch64_short(ws):
     # B=64 with state carry-over (the full 256-step run is the benchmark; 16 steps here).
-    run_steps(oracle.make_cfg(), 64, 16, inputs.seed_for(2), check_every=4)
+    run_steps(oracle.make_cfg(), 64, 16, inputs.seed_for(2), check_every=4, ws=ws)
 
 
-def test_long_carry_256_steps_small_batch():
-    run_steps(oracle.make_cfg(), 2, 256, inputs.seed_for(2) + 100, check_every=32)
+@pytest.mark.parametrize("ws", WS)
+def test_long_carry_256_steps_small_batch(ws):
+    run_steps(oracle.make_cfg(), 2, 256, inputs.seed_for(2) + 100, check_every=32, ws=ws)
 
 
 @pytest.mark.parametrize("kw", [
@@ -99,9 +111,10 @@ def test_long_carry_256_steps_small_batch():
     dict(h_k=1, h_v=5),
     dict(l2_eps=1e-3),
 ])
-def test_variants(kw):
+@pytest.mark.parametrize("ws", WS)
+def test_variants(kw, ws):
     cfg = oracle.make_cfg(**kw)
-    run_steps(cfg, 3, 4, inputs.seed_for(1) + 7 * len(kw))
+    run_steps(cfg, 3, 4, inputs.seed_for(1) + 7 * len(kw), ws=ws)
 
 
 def test_config0_golden_identity_conv():
@@ -110,18 +123,19 @@ def test_config0_golden_identity_conv():
     cfg = bx.make_cfg(h_k=1, h_v=1, d_conv=2)
     C = cfg.channels
     d_w, d_A, d_dt = dev(g["w"]), dev(g["A_log"]), dev(g["dt_bias"])
-    d_st = dev(g["state0"])
+    d_st = state_to_dev(g["state0"])
     d_cs = torch.zeros(1, C, 1, dtype=torch.bfloat16, device="cuda")
     o = torch.empty(1, 1, 128, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, 1), dtype=torch.uint8, device="cuda")
     outs = []
     for t in range(g["x"].shape[0]):
         assert bx.ix_gdn_decode(cfg, 1, dev(g["x"][t:t + 1]), d_cs, d_w, dev(g["a"][t:t + 1]), dev(g["b"][t:t + 1]),
-                                d_A, d_dt, d_st, o, None) == 0
+                                d_A, d_dt, d_st, o, None, ws) == 0
         outs.append(host(o).copy())
     torch.cuda.synchronize()
     got = np.concatenate(outs)
     assert float(np.max(np.abs(got - g["o"]))) <= TOL_O_ABS
-    assert oracle.rel_err(host(d_st), g["state"]) <= TOL_STATE_REL
+    assert oracle.rel_err(state_from_dev(d_st), g["state"]) <= TOL_STATE_REL
 
 
 def test_deterministic_and_null_outputs():
@@ -134,7 +148,7 @@ def test_deterministic_and_null_outputs():
         t = inputs.token_inputs(cfg, seed, 8)
         o = torch.empty(8, 32, 128, dtype=torch.float32, device="cuda")
         assert bx.ix_gdn_decode(cfg, 8, dev(t["x"]), r.d_cs, r.d_w, dev(t["a"]), dev(t["b"]), r.d_A, r.d_dt,
-                                r.d_st, o, None) == 0
+                                r.d_st, o, None, r.ws) == 0
         torch.cuda.synchronize()
         res.append((host(o).copy(), host(r.d_st).copy()))
     np.testing.assert_array_equal(res[0][0], res[1][0])
@@ -143,7 +157,7 @@ def test_deterministic_and_null_outputs():
     r = Run(cfg, 8, seed)
     t = inputs.token_inputs(cfg, seed, 8)
     assert bx.ix_gdn_decode(cfg, 8, dev(t["x"]), r.d_cs, r.d_w, dev(t["a"]), dev(t["b"]), r.d_A, r.d_dt,
-                            r.d_st, None, None) == 0
+                            r.d_st, None, None, r.ws) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(r.d_st), res[0][1])
 
@@ -157,6 +171,21 @@ def test_bf16_output_is_rne_of_fp32_output():
     o = torch.empty(4, 32, 128, dtype=torch.float32, device="cuda")
     ob = torch.empty(4, 32, 128, dtype=torch.bfloat16, device="cuda")
     assert bx.ix_gdn_decode(cfg, 4, dev(t["x"]), r.d_cs, r.d_w, dev(t["a"]), dev(t["b"]), r.d_A, r.d_dt, r.d_st,
-                            o, ob) == 0
+                            o, ob, r.ws) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(ob), bf16.from_f32(host(o)))
+
+
+def test_workspace_and_group_kernels_agree():
+    # Same inputs through both kernels: conv states bit-identical, outputs and states within
+    # fp32 rounding of each other (their reductions are ordered differently).
+    cfg = bx.make_cfg()
+    seed = inputs.seed_for(2) + 17
+    ra, rb = Run(cfg, 16, seed, ws=True), Run(cfg, 16, seed, ws=False)
+    for k in range(3):
+        t = inputs.token_inputs(cfg, seed, 16, step=k)
+        oa, _, ro = ra.step(t, k)
+        ob, _, _ = rb.step(t, k)
+        assert float(np.max(np.abs(oa - ob))) <= 1e-5
+    np.testing.assert_array_equal(host(ra.d_cs), host(rb.d_cs))
+    assert oracle.rel_err(host(ra.d_st), host(rb.d_st)) <= 1e-5

@@ -14,7 +14,7 @@ import pytest
 import baloon_amd as bx
 import oracle
 from oracle import bf16, inputs
-from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host
+from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
 
 pytestmark = pytest.mark.gpu
 NT = min(16, os.cpu_count() or 1)
@@ -30,7 +30,7 @@ def gpu_prefill(cfg, cu, tok, p, st, outputs=("o", "ob")):
     torch = _torch()
     cu = np.asarray(cu, np.int32)
     n, T = cu.size - 1, int(tok["x"].shape[0])
-    d_cs, d_st = dev(st["conv_state"]), dev(st["state"])
+    d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
     o = torch.full((T, cfg.h_v, cfg.d_v), float("nan"), dtype=torch.float32, device="cuda") if "o" in outputs else None
     ob = torch.zeros(T, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda") if "ob" in outputs else None
     need = bx.ix_gdn_prefill_workspace_size(cfg, n, T)
@@ -40,7 +40,7 @@ def gpu_prefill(cfg, cu, tok, p, st, outputs=("o", "ob")):
                            dev(p["A_log"]), dev(p["dt_bias"]), d_st, o, ob, ws, need)
     assert rc == 0, rc
     torch.cuda.synchronize()
-    return (host(d_cs), host(d_st), None if o is None else host(o), None if ob is None else host(ob))
+    return (host(d_cs), state_from_dev(d_st), None if o is None else host(o), None if ob is None else host(ob))
 
 
 def oracle_prefill(cfg, cu, tok, p, st):
@@ -110,18 +110,19 @@ def test_prefill_matches_gpu_decode_loop():
     tok = inputs.token_inputs(cfg, seed, T)
     st = inputs.initial_states(cfg, seed, 1)
     cs, s, o, _ = gpu_prefill(cfg, [0, T], tok, p, st)
-    d_cs, d_st = dev(st["conv_state"]), dev(st["state"])
+    d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
     d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
     od = torch.empty(1, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, 1), dtype=torch.uint8, device="cuda")
     outs = []
     for t in range(T):
         assert bx.ix_gdn_decode(cfg, 1, dev(tok["x"][t:t + 1]), d_cs, d_w, dev(tok["a"][t:t + 1]),
-                                dev(tok["b"][t:t + 1]), d_A, d_dt, d_st, od, None) == 0
+                                dev(tok["b"][t:t + 1]), d_A, d_dt, d_st, od, None, ws) == 0
         outs.append(host(od)[0].copy())
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(d_cs), cs)
     assert float(np.max(np.abs(np.stack(outs) - o))) <= TOL_O_ABS
-    assert oracle.rel_err(s, host(d_st)) <= TOL_STATE_REL
+    assert oracle.rel_err(s, state_from_dev(d_st)) <= TOL_STATE_REL
 
 
 def test_config4_varlen_prefill_then_decode():
@@ -141,19 +142,20 @@ def test_config4_varlen_prefill_then_decode():
     np.testing.assert_array_equal(cs, rcs)
     assert oracle.rel_err(s, rs) <= TOL_STATE_REL
     assert float(np.max(np.abs(o - ro))) <= TOL_O_ABS
-    d_cs, d_st = dev(cs), dev(s)
+    d_cs, d_st = dev(cs), state_to_dev(s)
     d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
     od = torch.empty(n, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, n), dtype=torch.uint8, device="cuda")
     for k in range(steps):
         t = inputs.token_inputs(cfg, seed, n, step=1000 + k)
         assert bx.ix_gdn_decode(cfg, n, dev(t["x"]), d_cs, d_w, dev(t["a"]), dev(t["b"]), d_A, d_dt, d_st, od,
-                                None) == 0
+                                None, ws) == 0
         rcs, rs, rod = oracle.decode(cfg, n, t["x"], rcs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], rs,
                                      nthreads=NT)
         torch.cuda.synchronize()
         assert float(np.max(np.abs(host(od) - rod))) <= TOL_O_ABS, k
     np.testing.assert_array_equal(host(d_cs), rcs)
-    assert oracle.rel_err(host(d_st), rs) <= TOL_STATE_REL
+    assert oracle.rel_err(state_from_dev(d_st), rs) <= TOL_STATE_REL
 
 
 def test_state_only_and_repeatable():
