@@ -21,15 +21,15 @@
 // Kernels, in stream order:
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
 //                  the chunk table (sequence and first token of each chunk)
-//   prep_kernel    per chunk: conv (history from conv_state at sequence starts), L2 norm of
-//                  q and k, log decay and beta; fp32 q, k, v into the workspace
+//   prep_kernel    per (chunk, head): conv (history from conv_state at sequence starts), L2
+//                  norm of q and k, log decay and beta; fp32 q, k, v into the workspace
 //   commit_kernel  per sequence and channel: the new rolling conv history
-//   chunk_kernel   per (chunk, q/k head): K K^T and Q K^T on fp32 MFMA, then per mapped v
-//                  head A, M, and W | U by forward substitution (one column per thread)
+//   chunk_kernel   per (chunk, v head): K K^T and Q K^T on fp32 MFMA (lower block triangle),
+//                  A, M, and W | U by forward substitution (one column per thread)
 //   chain_kernel   per (sequence, v head, 16-column state slice): walks the chunks in
 //                  order carrying the state slice in MFMA accumulators; D, O and S' on fp32
-//                  MFMA. Columns of the state are independent, so 8 slices per head fill
-//                  the GPU even for a single sequence.
+//                  MFMA, state and output work on separate waves. Columns of the state are
+//                  independent, so 8 slices per head fill the GPU even for a single sequence.
 // The fp32 matrix cores (v_mfma_f32_16x16x4_f32) keep the chunked result within ~1e-6 of
 // the token-by-token recurrence in double.
 #include "gdn_common.h"
@@ -62,30 +62,33 @@ struct Ws {
     float* lg;           // [h_v][T] log decay
     float* bt;           // [h_v][T] beta
     float* W;            // [NC][h_v][64][128]
-    float* U;            // [NC][h_v][64][128]
+    float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
     float* M;            // [NC][h_v][64][64]
     float* G;            // [NC][h_v][64] cumulative log decay (padded rows repeat the last)
+    float* Kt;           // [NC][h_k][128][64]  K transposed, zero beyond the chunk length
 };
+constexpr int kWsSections = 14;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Byte offsets of every workspace section for (n_seq, T); returns the total size.
-inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[13]) {
+inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSections]) {
     const size_t NC = (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq;
-    const size_t sz[13] = {
+    const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * NC, sizeof(int32_t) * NC,
         sizeof(float) * c->h_k * (size_t)T * kD, sizeof(float) * c->h_k * (size_t)T * kD,
         sizeof(float) * c->h_v * (size_t)T * kD, sizeof(float) * c->h_v * (size_t)T,
         sizeof(float) * c->h_v * (size_t)T,
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk,
+        sizeof(float) * NC * c->h_k * kD * kChunk,
     };
     size_t pos = 0;
-    for (int i = 0; i < 13; ++i) { off[i] = pos; pos += align256(sz[i]); }
+    for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
     return pos;
 }
 
-inline Ws ws_bind(char* base, const size_t off[13]) {
+inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     Ws w;
     w.seq_lo = reinterpret_cast<int32_t*>(base + off[0]);
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
@@ -97,9 +100,10 @@ inline Ws ws_bind(char* base, const size_t off[13]) {
     w.lg = reinterpret_cast<float*>(base + off[7]);
     w.bt = reinterpret_cast<float*>(base + off[8]);
     w.W = reinterpret_cast<float*>(base + off[9]);
-    w.U = reinterpret_cast<float*>(base + off[10]);
+    w.Ut = reinterpret_cast<float*>(base + off[10]);
     w.M = reinterpret_cast<float*>(base + off[11]);
     w.G = reinterpret_cast<float*>(base + off[12]);
+    w.Kt = reinterpret_cast<float*>(base + off[13]);
     return w;
 }
 
@@ -183,66 +187,89 @@ __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGe
     return true;
 }
 
-// Conv output of channel ch at token position pos of sequence s (history from x, or from the
-// sequence's conv state for the first dc-1 positions).
-__device__ __forceinline__ float conv_at(const PrefillParams& p, int s, int lo, int pos, int ch) {
-    const Layer& L = p.L;
-    float hist[3];
-#pragma unroll
-    for (int i = 0; i < 3; ++i) {
-        hist[i] = 0.0f;
-        if (i < L.dc - 1) {
-            const int hp = pos - (L.dc - 1) + i;
-            const uint16_t u = hp >= 0 ? p.x[(size_t)(lo + hp) * L.C + ch]
-                                       : p.conv_state[((size_t)s * L.C + ch) * (L.dc - 1) + (L.dc - 1) + hp];
-            hist[i] = bf16_to_f32(u);
-        }
-    }
-    const float xv = bf16_to_f32(p.x[(size_t)(lo + pos) * L.C + ch]);
-    return conv_eval(L, hist, xv, L.conv_w + (size_t)ch * L.dc);
-}
+// ---------------------------------------------------------------------------------------
+// prep: grid (NC, 2 h_k + h_v), 256 threads; workgroup = (chunk, one q, k or v head).
+// Thread (c = tid & 127, th = tid >> 7) owns channel c of the head for tokens 32 th .. 32 th
+// + 31 of the chunk: its history and all its inputs are loaded up front, then the conv runs
+// along the tokens. q and k rows are L2-normalised (one wave sum per token and wave, two
+// waves per token half).
+// ---------------------------------------------------------------------------------------
+constexpr int kPrepTok = kChunk / 2;
 
-// ---------------------------------------------------------------------------------------
-// prep: grid (NC, h_k + h_v), 256 threads
-// ---------------------------------------------------------------------------------------
+template <int DC>
 __global__ void __launch_bounds__(256) prep_kernel(const PrefillParams p) {
+    __shared__ float part[2][2][kPrepTok];          // [token half][wave of the half][token]
     ChunkGeo g;
     if (!chunk_geo(p, blockIdx.x, g)) return;
     const Layer& L = p.L;
     const int lo = p.ws.seq_lo[g.s];
-    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int c = tid & (kD - 1), th = tid >> 7, wh = (tid >> 6) & 1;
     const int y = blockIdx.y;
-    if (y < L.h_k) {
-        // q and k of head src: one wave per token, lanes own dims lane and lane + 64.
-        const int src = y;
-        for (int t = w; t < g.len; t += 4) {
-            const int pos = g.pos0 + t;
-            const float q0 = conv_at(p, g.s, lo, pos, q_channel(L, src, lane));
-            const float q1 = conv_at(p, g.s, lo, pos, q_channel(L, src, lane + kWave));
-            const float k0 = conv_at(p, g.s, lo, pos, k_channel(L, src, lane));
-            const float k1 = conv_at(p, g.s, lo, pos, k_channel(L, src, lane + kWave));
-            const float qq = wave_sum(fmaf(q0, q0, q1 * q1));
-            const float kk = wave_sum(fmaf(k0, k0, k1 * k1));
-            const float inv_q = L.q_scale / sqrtf(qq + L.l2_eps);
-            const float inv_k = 1.0f / sqrtf(kk + L.l2_eps);
-            const size_t row = ((size_t)src * p.T + g.t0 + t) * kD;
-            p.ws.qn[row + lane] = q0 * inv_q;
-            p.ws.qn[row + lane + kWave] = q1 * inv_q;
-            p.ws.kn[row + lane] = k0 * inv_k;
-            p.ws.kn[row + lane + kWave] = k1 * inv_k;
-        }
-    } else {
-        const int h = y - L.h_k;
-        for (int e = tid; e < g.len * kD; e += 256) {
-            const int t = e / kD, j = e % kD;
-            p.ws.vv[((size_t)h * p.T + g.t0 + t) * kD + j] = conv_at(p, g.s, lo, g.pos0 + t, v_channel(L, h, j));
-        }
-        if (tid < g.len) {
-            const size_t ab = (size_t)(g.t0 + tid) * L.h_v + h;
-            p.ws.lg[(size_t)h * p.T + g.t0 + tid] = log_gate(L, h, bf16_to_f32(p.a[ab]));
-            p.ws.bt[(size_t)h * p.T + g.t0 + tid] = sigmoid_f(bf16_to_f32(p.b[ab]));
-        }
+    const int kind = y < L.h_k ? 0 : (y < 2 * L.h_k ? 1 : 2);           // q, k, v
+    const int head = kind == 0 ? y : (kind == 1 ? y - L.h_k : y - 2 * L.h_k);
+    const int ch = kind == 0 ? q_channel(L, head, c) : (kind == 1 ? k_channel(L, head, c) : v_channel(L, head, c));
+    const int tb = kPrepTok * th;                                          // first token of this thread
+    const int n = min(max(g.len - tb, 0), kPrepTok);
+
+    // History of the first token (only threads that own tokens read it: positions before
+    // the sequence start come from its conv state, the others lie inside the sequence).
+    float hist[DC - 1];
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) {
+        const int pos = g.pos0 + tb - (DC - 1) + i;
+        uint16_t u = 0;
+        if (n > 0)
+            u = pos >= 0 ? p.x[(size_t)(lo + pos) * L.C + ch]
+                         : p.conv_state[((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + pos];
+        hist[i] = bf16_to_f32(u);
     }
+    uint16_t xs[kPrepTok];
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t) xs[t] = t < n ? p.x[(size_t)(g.t0 + tb + t) * L.C + ch] : (uint16_t)0;
+    const uint16_t* wr = L.conv_w + (size_t)ch * DC;
+    float wv[DC];
+#pragma unroll
+    for (int i = 0; i < DC; ++i) wv[i] = bf16_to_f32(wr[i]);
+
+    float yv[kPrepTok];
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t) {
+        const float xv = bf16_to_f32(xs[t]);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DC - 1; ++i) acc = fmaf(hist[i], wv[i], acc);
+        acc = fmaf(xv, wv[DC - 1], acc);
+        if (L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
+        yv[t] = acc;
+#pragma unroll
+        for (int i = 0; i < DC - 2; ++i) hist[i] = hist[i + 1];
+        hist[DC - 2] = xv;
+    }
+
+    if (kind == 2) {
+        float* dst = p.ws.vv + ((size_t)head * p.T + g.t0 + tb) * kD + c;
+#pragma unroll
+        for (int t = 0; t < kPrepTok; ++t)
+            if (t < n) dst[(size_t)t * kD] = yv[t];
+        if (tid < g.len) {
+            const size_t ab = (size_t)(g.t0 + tid) * L.h_v + head;
+            p.ws.lg[(size_t)head * p.T + g.t0 + tid] = log_gate(L, head, bf16_to_f32(p.a[ab]));
+            p.ws.bt[(size_t)head * p.T + g.t0 + tid] = sigmoid_f(bf16_to_f32(p.b[ab]));
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t) {
+        const float r = wave_sum(yv[t] * yv[t]);
+        if (lane == 0) part[th][wh][t] = r;
+    }
+    __syncthreads();
+    const float scale = kind == 0 ? L.q_scale : 1.0f;
+    float* dst = (kind == 0 ? p.ws.qn : p.ws.kn) + ((size_t)head * p.T + g.t0 + tb) * kD + c;
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t)
+        if (t < n) dst[(size_t)t * kD] = yv[t] * (scale / sqrtf(part[th][0][t] + part[th][1][t] + L.l2_eps));
 }
 
 // ---------------------------------------------------------------------------------------
@@ -272,156 +299,298 @@ __global__ void __launch_bounds__(256) commit_kernel(const PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
-// chunk-local: grid (NC, h_k), 256 threads
+// chunk-local: grid (NC, h_v), 256 threads; workgroup = (chunk, v head)
 // ---------------------------------------------------------------------------------------
-constexpr int kKS = kD + 4;          // padded LDS row stride of K and Q tiles
+constexpr int kKS = kD + 4;          // padded LDS row stride of the K tile
+
+// The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
+__device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
+    br = i < 1 ? 0 : i < 3 ? 1 : i < 6 ? 2 : 3;
+    bc = i - br * (br + 1) / 2;
+}
 
 __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
     __shared__ __align__(16) float K_s[kChunk][kKS];
-    __shared__ __align__(16) float Q_s[kChunk][kKS];
     __shared__ __align__(16) float A_s[kChunk][kChunk];
     __shared__ float G_s[kChunk], B_s[kChunk];
-    float (*KK_s)[kChunk] = reinterpret_cast<float (*)[kChunk]>(&Q_s[0][0]);              // after Q K^T
-    float (*QK_s)[kChunk] = reinterpret_cast<float (*)[kChunk]>(&Q_s[0][0] + kChunk * kChunk);
 
     ChunkGeo g;
     const int c = blockIdx.x;
     if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
-    const int src = blockIdx.y;
+    const int h = blockIdx.y, src = src_of(L, h);
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int li = lane & 15, lg4 = lane >> 4;
+    const size_t ch = (size_t)c * L.h_v + h;
+    const float* kbase = p.ws.kn + ((size_t)src * p.T + g.t0) * kD;
+    const float* qbase = p.ws.qn + ((size_t)src * p.T + g.t0) * kD;
 
-    // Stage K and Q rows of the chunk (zero beyond its length).
+    // Stage the K rows of the chunk (zero beyond its length); wave 0 also scans the decay.
     for (int e = tid; e < kChunk * (kD / 4); e += 256) {
         const int t = e / (kD / 4), c4 = e % (kD / 4);
-        v4 kv = {0.f, 0.f, 0.f, 0.f}, qv = kv;
-        if (t < g.len) {
-            const size_t row = ((size_t)src * p.T + g.t0 + t) * kD;
-            kv = *reinterpret_cast<const v4*>(p.ws.kn + row + 4 * c4);
-            qv = *reinterpret_cast<const v4*>(p.ws.qn + row + 4 * c4);
-        }
+        v4 kv = {0.f, 0.f, 0.f, 0.f};
+        if (t < g.len) kv = *reinterpret_cast<const v4*>(kbase + (size_t)t * kD + 4 * c4);
         *reinterpret_cast<v4*>(&K_s[t][4 * c4]) = kv;
-        *reinterpret_cast<v4*>(&Q_s[t][4 * c4]) = qv;
+    }
+    if (w == 0) {
+        float lgt = lane < g.len ? p.ws.lg[(size_t)h * p.T + g.t0 + lane] : 0.0f;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {          // inclusive scan over the 64 lanes
+            const float o = __shfl_up(lgt, off, kWave);
+            if (lane >= off) lgt += o;
+        }
+        G_s[lane] = lgt;
+        B_s[lane] = lane < g.len ? p.ws.bt[(size_t)h * p.T + g.t0 + lane] : 0.0f;
+        p.ws.G[ch * kChunk + lane] = lgt;
     }
     __syncthreads();
 
-    // K K^T and Q K^T, lower block triangle: wave w owns block row w, blocks c <= w.
-    // MFMA k index of (block 4m + e, lane group g) is 16 m + 4 g + e (same for A and B).
-    v4 kk[4], qk[4];
+    // K K^T and Q K^T on the lower block triangle, then A (into LDS) and M (to the workspace).
+    // MFMA k index of (block 4m + e, lane group g) is 16 m + 4 g + e for both operands.
+    float* Mg = p.ws.M + ch * kChunk * kChunk;
+    for (int i = w; i < 10; i += 4) {
+        int br, bc;
+        tri_block(i, br, bc);
+        const int arow = 16 * br + li;
+        const bool qok = arow < g.len;
+        v4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) { kk[cb] = v4{0.f, 0.f, 0.f, 0.f}; qk[cb] = kk[cb]; }
+        for (int m = 0; m < kD / 16; ++m) {
+            const v4 ak = *reinterpret_cast<const v4*>(&K_s[arow][16 * m + 4 * lg4]);
+            const v4 aq = qok ? *reinterpret_cast<const v4*>(qbase + (size_t)arow * kD + 16 * m + 4 * lg4)
+                              : v4{0.f, 0.f, 0.f, 0.f};
+            const v4 bk = *reinterpret_cast<const v4*>(&K_s[16 * bc + li][16 * m + 4 * lg4]);
 #pragma unroll
-    for (int m = 0; m < kD / 16; ++m) {
-        const v4 ak = *reinterpret_cast<const v4*>(&K_s[16 * w + li][16 * m + 4 * lg4]);
-        const v4 aq = *reinterpret_cast<const v4*>(&Q_s[16 * w + li][16 * m + 4 * lg4]);
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
-            if (cb <= w) {
-                const v4 bk = *reinterpret_cast<const v4*>(&K_s[16 * cb + li][16 * m + 4 * lg4]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kk[cb] = mfma4(ak[e], bk[e], kk[cb]);
-                    qk[cb] = mfma4(aq[e], bk[e], qk[cb]);
-                }
+            for (int e = 0; e < 4; ++e) {
+                kk = mfma4(ak[e], bk[e], kk);
+                qk = mfma4(aq[e], bk[e], qk);
             }
         }
-    }
-
-    // Park both products in LDS (over Q_s, which is no longer read) to free the accumulators.
-    __syncthreads();
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            KK_s[16 * w + 4 * lg4 + r][16 * cb + li] = kk[cb][r];
-            QK_s[16 * w + 4 * lg4 + r][16 * cb + li] = qk[cb][r];
+            const int t = 16 * br + 4 * lg4 + r, s = 16 * bc + li;
+            float av = 0.0f, mv = 0.0f;
+            if (s <= t) {
+                const float e = expf(G_s[t] - G_s[s]);
+                mv = e * qk[r];
+                if (s < t) av = B_s[t] * e * kk[r];
+            }
+            A_s[t][s] = av;
+            Mg[t * kChunk + s] = mv;
         }
+    }
+    // the upper blocks of M are zero
+    for (int e = tid; e < 6 * 256; e += 256) {
+        const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
+        const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
+        Mg[(16 * br + r) * kChunk + 16 * bc + col] = 0.0f;
+    }
     __syncthreads();
 
-    const int count = mapped_count(L, src);
-    for (int m = 0; m < count; ++m) {
-        const int h = mapped_head(L, src, m);
-        const size_t ch = (size_t)c * L.h_v + h;
-        if (w == 0) {
-            float lgt = lane < g.len ? p.ws.lg[(size_t)h * p.T + g.t0 + lane] : 0.0f;
-            // inclusive scan over the 64 lanes
+    // Forward substitution (I + A) X = R for the 256 columns of R = [diag(beta Gam) K | diag(beta) V]:
+    // waves 0-1 own the W columns, waves 2-3 the U columns (a wave-uniform split).
+    {
+        const int j = tid & (kD - 1);
+        const bool is_w = tid < kD;
+        float xr[kChunk];
+        if (is_w) {
 #pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                const float o = __shfl_up(lgt, off, kWave);
-                if (lane >= off) lgt += o;
-            }
-            G_s[lane] = lgt;
-            B_s[lane] = lane < g.len ? p.ws.bt[(size_t)h * p.T + g.t0 + lane] : 0.0f;
-            p.ws.G[ch * kChunk + lane] = lgt;
+            for (int t = 0; t < kChunk; ++t) xr[t] = B_s[t] * expf(G_s[t]) * K_s[t][j];
+        } else {
+            const float* vsrc = p.ws.vv + ((size_t)h * p.T + g.t0) * kD + j;
+#pragma unroll
+            for (int t = 0; t < kChunk; ++t) xr[t] = t < g.len ? B_s[t] * vsrc[(size_t)t * kD] : 0.0f;
         }
-        __syncthreads();
-
-        // A into LDS, M into the workspace (C layout: row 16w + 4 lg4 + r, column 16 cb + li).
-        float* Mg = p.ws.M + ch * kChunk * kChunk;
+        // Four partial sums per row keep the dependent FMA chain short.
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) {
+        for (int t = 1; t < kChunk; ++t) {
+            float r[4] = {xr[t], 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * w + 4 * lg4 + r, s = 16 * cb + li;
-                float av = 0.0f, mv = 0.0f;
-                if (s <= t) {
-                    const float e = expf(G_s[t] - G_s[s]);
-                    mv = e * QK_s[t][s];
-                    if (s < t) av = B_s[t] * e * KK_s[t][s];
-                }
-                A_s[t][s] = av;
-                Mg[t * kChunk + s] = mv;
+            for (int q4 = 0; q4 < t; q4 += 4) {
+                const v4 av = *reinterpret_cast<const v4*>(&A_s[t][q4]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (q4 + e < t) r[e] = fmaf(-av[e], xr[q4 + e], r[e]);
             }
+            xr[t] = (r[0] + r[1]) + (r[2] + r[3]);
         }
-        __syncthreads();
-
-        // Forward substitution (I + A) X = R for the 256 columns of R = [diag(beta Gam) K | diag(beta) V]:
-        // waves 0-1 own the W columns, waves 2-3 the U columns (a wave-uniform split).
-        {
-            const int j = tid & (kD - 1);
-            const bool is_w = tid < kD;
-            float xr[kChunk];
-            if (is_w) {
-#pragma unroll
-                for (int t = 0; t < kChunk; ++t) xr[t] = B_s[t] * expf(G_s[t]) * K_s[t][j];
-            } else {
-                const float* vsrc = p.ws.vv + ((size_t)h * p.T + g.t0) * kD + j;
-#pragma unroll
-                for (int t = 0; t < kChunk; ++t) xr[t] = t < g.len ? B_s[t] * vsrc[(size_t)t * kD] : 0.0f;
-            }
-#pragma unroll
-            for (int t = 1; t < kChunk; ++t) {
-                float r = xr[t];
-#pragma unroll
-                for (int q4 = 0; q4 < t; q4 += 4) {
-                    const v4 av = *reinterpret_cast<const v4*>(&A_s[t][q4]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (q4 + e < t) r = fmaf(-av[e], xr[q4 + e], r);
-                }
-                xr[t] = r;
-            }
-            float* dst = (is_w ? p.ws.W : p.ws.U) + ch * kChunk * kD + j;
+        if (is_w) {
+            float* dst = p.ws.W + ch * kChunk * kD + j;
 #pragma unroll
             for (int t = 0; t < kChunk; ++t) dst[(size_t)t * kD] = xr[t];
+        } else {
+            v4* dst = reinterpret_cast<v4*>(p.ws.Ut + (ch * kD + j) * kChunk);     // column j of U, contiguous
+#pragma unroll
+            for (int t4 = 0; t4 < kChunk / 4; ++t4) dst[t4] = v4{xr[4 * t4], xr[4 * t4 + 1], xr[4 * t4 + 2], xr[4 * t4 + 3]};
         }
-        __syncthreads();
+    }
+    // K^T of the chunk for the chain's state update, written once per (chunk, q/k head) by the
+    // workgroup of its first mapped v head: thread (i = tid / 2, half = tid % 2) writes
+    // tokens 32 half .. +31 of row i.
+    if (mapped_head(L, src, 0) == h) {
+        const int i = tid >> 1, t0h = 32 * (tid & 1);
+        v4* dst = reinterpret_cast<v4*>(p.ws.Kt + (((size_t)c * L.h_k + src) * kD + i) * kChunk + t0h);
+#pragma unroll
+        for (int t4 = 0; t4 < 8; ++t4)
+            dst[t4] = v4{K_s[t0h + 4 * t4][i], K_s[t0h + 4 * t4 + 1][i], K_s[t0h + 4 * t4 + 2][i], K_s[t0h + 4 * t4 + 3][i]};
     }
 }
 
 // ---------------------------------------------------------------------------------------
 // chain: one workgroup per (sequence, v head, 16-column slice), 256 threads
 // ---------------------------------------------------------------------------------------
-// Rows r and r + 32 (state) or r and r + 16 (chunk rows) are read by the two lane groups
-// of a half wave together; 16 padding words after every such block put them 16 banks apart.
-__device__ __forceinline__ int s_idx(int row, int col) { return row * kSlice + col + 16 * (row >> 5); }
-__device__ __forceinline__ int d_idx(int row, int col) { return row * kSlice + col + 16 * (row >> 4); }
+// LDS tiles of the chain are stored column by column (4 padding words per column), so the
+// 4 consecutive rows of one column that a lane needs are one 16-byte access.
+constexpr int kSCol = kD + 4;          // state slice column stride
+constexpr int kDCol = kChunk + 4;      // D tile column stride
 
-__global__ void __launch_bounds__(256) chain_kernel(const PrefillParams p) {
-    __shared__ float S_l[kD * kSlice + 16 * (kD / 32)];
-    __shared__ float D_l[kChunk * kSlice + 16 * (kChunk / 16)];
-    __shared__ float Dg_l[kChunk * kSlice + 16 * (kChunk / 16)];
+// The chain workgroup has 8 waves in two roles that meet at two barriers per chunk:
+//   state waves (0-3): S -> LDS | W S, D = U - W S -> LDS | S' = Gam_last S + K^T (exp(G_last - G) D)
+//   output waves (4-7):          | Q S                   | O = diag(Gam) Q S + M D
+// Each role loads the next chunk's operands (double buffer) while it computes the current one.
+// Lane (li = lane & 15, lg4 = lane >> 4) of role wave r uses rows 16 r + li of the 64-row
+// chunk tiles as MFMA A operands and rows 16 r + 4 lg4 + i in C layout; state wave r owns
+// state rows (k index) 32 r .. 32 r + 31.
+struct StateOps {
+    v4 aw[8];             // W row 16r+li, k = 32 lg4 + 4 m + e
+    v4 kt[2][4];          // K^T row 32 r + 16 tt + li, token 16 lg4 + 4 q + e
+    v4 u;                 // U rows 16r + 4 lg4 + i, column j0 + li
+    v4 gv;                // G at those rows
+    float glast;          // G of the chunk's last row
+};
+struct OutOps {
+    v4 aq[8];             // Q row 16r+li (the last row again past the chunk end)
+    v4 am[4];             // M row 16r+li, s = 16 lg4 + 4 m + e
+    v4 gv;
+    int t0, len;
+};
+
+struct ChainCtx {
+    const PrefillParams* p;
+    const float* qbase;   // q rows of the head's q/k head
+    int h, src, seq_lo, seq_hi, c_begin, j0, r, li, lg4;
+};
+
+__device__ __forceinline__ size_t chain_ch(const ChainCtx& x, int c) { return (size_t)c * x.p->L.h_v + x.h; }
+
+__device__ __forceinline__ void load_state_ops(const ChainCtx& x, int c, StateOps& o) {
+    const PrefillParams& p = *x.p;
+    const size_t ch = chain_ch(x, c);
+    const float* Wc = p.ws.W + ch * kChunk * kD;
+    const float* Gc = p.ws.G + ch * kChunk;
+    const float* Kc = p.ws.Kt + ((size_t)c * p.L.h_k + x.src) * kD * kChunk;
+    const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) o.aw[m] = *reinterpret_cast<const v4*>(Wc + (size_t)arow * kD + 32 * x.lg4 + 4 * m);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            o.kt[tt][q] = *reinterpret_cast<const v4*>(Kc + (size_t)(32 * x.r + 16 * tt + x.li) * kChunk + 16 * x.lg4 + 4 * q);
+    o.u = *reinterpret_cast<const v4*>(p.ws.Ut + (ch * kD + x.j0 + x.li) * kChunk + crow);
+    o.gv = *reinterpret_cast<const v4*>(Gc + crow);
+    o.glast = Gc[kChunk - 1];
+}
+
+__device__ __forceinline__ void load_out_ops(const ChainCtx& x, int c, OutOps& o) {
+    const PrefillParams& p = *x.p;
+    const size_t ch = chain_ch(x, c);
+    o.t0 = x.seq_lo + (c - x.c_begin) * kChunk;            // chunk c of the sequence (no table lookup)
+    o.len = min(kChunk, x.seq_hi - o.t0);
+    const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
+    // Q rows past the chunk end re-read its last row: an MFMA output row depends only on its
+    // own A row, so those rows only produce output rows that are never stored.
+    const float* qr = x.qbase + (size_t)(o.t0 + min(arow, o.len - 1)) * kD + 32 * x.lg4;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) o.aq[m] = *reinterpret_cast<const v4*>(qr + 4 * m);
+    const float* Mc = p.ws.M + ch * kChunk * kChunk;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) o.am[m] = *reinterpret_cast<const v4*>(Mc + (size_t)arow * kChunk + 16 * x.lg4 + 4 * m);
+    o.gv = *reinterpret_cast<const v4*>(p.ws.G + ch * kChunk + crow);
+}
+
+// State waves, one chunk: D = U - W S, S' = Gam_last S + K^T (exp(G_last - G) D).
+__device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o, v4 (&S)[2], float* S_l,
+                                           float* D_l, float* Dg_l) {
+    const int r = x.r, li = x.li, lg4 = x.lg4, crow = 16 * r + 4 * lg4;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(S_l + li * kSCol + 32 * r + 16 * tt + 4 * lg4) = S[tt];
+    lds_barrier();                                                    // (A) state slice visible
+
+    // W S for rows 16r..16r+15; k index of block (m, e), lane group g: 32 g + 4 m + e.
+    v4 ws[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 32 * lg4 + 4 * m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ws[m & 1] = mfma4(o.aw[m][e], bv[e], ws[m & 1]);
+    }
+    v4 d, dg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        d[i] = o.u[i] - (ws[0][i] + ws[1][i]);
+        dg[i] = expf(o.glast - o.gv[i]) * d[i];
+    }
+    *reinterpret_cast<v4*>(D_l + li * kDCol + crow) = d;
+    *reinterpret_cast<v4*>(Dg_l + li * kDCol + crow) = dg;
+    lds_barrier();                                                    // (B) D visible
+
+    // S' = Gam_last S + K^T Dg; k index 16 g + b over the chunk rows.
+    const float gl = expf(o.glast);
+    v4 dgv[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) dgv[m] = *reinterpret_cast<const v4*>(Dg_l + li * kDCol + 16 * lg4 + 4 * m);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        v4 acc = {0.f, 0.f, 0.f, 0.f};
+        S[tt] *= gl;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            if (b & 1) acc = mfma4(o.kt[tt][b >> 2][b & 3], dgv[b >> 2][b & 3], acc);
+            else S[tt] = mfma4(o.kt[tt][b >> 2][b & 3], dgv[b >> 2][b & 3], S[tt]);
+        }
+        S[tt] += acc;
+    }
+}
+
+// Output waves, one chunk: O = diag(Gam) Q S + M D for rows 16r..16r+15.
+__device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, const float* S_l, const float* D_l) {
+    const PrefillParams& p = *x.p;
+    const int r = x.r, li = x.li, lg4 = x.lg4, crow = 16 * r + 4 * lg4;
+    lds_barrier();                                                    // (A)
+    v4 qs[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 32 * lg4 + 4 * m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qs[m & 1] = mfma4(o.aq[m][e], bv[e], qs[m & 1]);
+    }
+    lds_barrier();                                                    // (B)
+    v4 ov[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { ov[0][i] = expf(o.gv[i]) * (qs[0][i] + qs[1][i]); ov[1][i] = 0.0f; }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const v4 bv = *reinterpret_cast<const v4*>(D_l + li * kDCol + 16 * lg4 + 4 * m);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[m & 1] = mfma4(o.am[m][e], bv[e], ov[m & 1]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = crow + i;
+        if (t < o.len) {
+            const size_t oo = ((size_t)(o.t0 + t) * p.L.h_v + x.h) * kD + x.j0 + li;
+            const float ovr = ov[0][i] + ov[1][i];
+            if (p.o) p.o[oo] = ovr;
+            if (p.o_bf16) p.o_bf16[oo] = f32_to_bf16(ovr);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
+    __shared__ __align__(16) float S_l[kSlice * kSCol];
+    __shared__ __align__(16) float D_l[kSlice * kDCol];
+    __shared__ __align__(16) float Dg_l[kSlice * kDCol];
 
     const Layer& L = p.L;
     // XCD-aware mapping: the 8 slices of one (sequence, head) pair share an XCD (and its L2).
@@ -432,111 +601,59 @@ __global__ void __launch_bounds__(256) chain_kernel(const PrefillParams p) {
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
     const int c_begin = p.ws.chunk_off[s], c_end = p.ws.chunk_off[s + 1];
     if (c_begin >= c_end) return;
-    const int seq_hi = p.ws.seq_lo[s + 1];
-    const int j0 = slice * kSlice;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
-    const int li = lane & 15, lg4 = lane >> 4;
 
-    // State slice: wave w owns rows 32 w + 16 tt + 4 lg4 + r (k index), column j0 + li (v
-    // index); the state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
-    float* st = p.state + (((size_t)s * L.h_v + h) * kD + j0 + li) * kD + 32 * w + 4 * lg4;
-    v4 S[2];
+    ChainCtx x;
+    x.p = &p;
+    x.qbase = p.ws.qn + (size_t)src * p.T * kD;
+    x.h = h;
+    x.src = src;
+    x.seq_lo = p.ws.seq_lo[s];
+    x.seq_hi = p.ws.seq_lo[s + 1];
+    x.c_begin = c_begin;
+    x.j0 = slice * kSlice;
+    x.r = w & 3;
+    x.li = lane & 15;
+    x.lg4 = lane >> 4;
+
+    if (w < 4) {
+        // State slice: rows 32 r + 16 tt + 4 lg4 + i (k index), column j0 + li (v index); the
+        // state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
+        float* st = p.state + (((size_t)s * L.h_v + h) * kD + x.j0 + x.li) * kD + 32 * x.r + 4 * x.lg4;
+        v4 S[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const v4*>(st + 16 * tt);
-
-    const float* qbase = p.ws.qn + (size_t)src * p.T * kD;
-    const float* kbase = p.ws.kn + (size_t)src * p.T * kD;
-
-    for (int c = c_begin; c < c_end; ++c) {
-        const int t0 = p.ws.chunk_t0[c];
-        const int len = min(kChunk, seq_hi - t0);
-        const size_t ch = (size_t)c * L.h_v + h;
-        const float* Wc = p.ws.W + ch * kChunk * kD;
-        const float* Uc = p.ws.U + ch * kChunk * kD;
-        const float* Mc = p.ws.M + ch * kChunk * kChunk;
-        const float* Gc = p.ws.G + ch * kChunk;
-
-        // Operands of this chunk (issued before the state exchange).
-        const int arow = 16 * w + li;                          // A-operand row of this lane
-        v4 aw[8], aq[8], am[4];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) {
-            aw[m] = *reinterpret_cast<const v4*>(Wc + (size_t)arow * kD + 32 * lg4 + 4 * m);
-            aq[m] = arow < len ? *reinterpret_cast<const v4*>(qbase + (size_t)(t0 + arow) * kD + 32 * lg4 + 4 * m)
-                               : v4{0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const v4*>(st + 16 * tt);
+        __builtin_amdgcn_s_waitcnt(0);             // the state is in registers before the loop
+        // Prefetches are unconditional (past the last chunk they re-read it): a load that is
+        // skipped on one path forces the compiler to wait for every load in flight.
+        StateOps A, B;
+        load_state_ops(x, c_begin, A);
+        int c = c_begin;
+        for (; c + 1 < c_end; c += 2) {
+            load_state_ops(x, c + 1, B);
+            state_step(x, A, S, S_l, D_l, Dg_l);
+            __builtin_amdgcn_sched_barrier(0);     // keep A's reload after A's last use
+            load_state_ops(x, min(c + 2, c_end - 1), A);
+            state_step(x, B, S, S_l, D_l, Dg_l);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        if (c < c_end) state_step(x, A, S, S_l, D_l, Dg_l);
 #pragma unroll
-        for (int m = 0; m < 4; ++m) am[m] = *reinterpret_cast<const v4*>(Mc + (size_t)arow * kChunk + 16 * lg4 + 4 * m);
-        const int crow = 16 * w + 4 * lg4;                     // C-layout rows crow + r
-        float u[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) u[r] = Uc[(size_t)(crow + r) * kD + j0 + li];
-        const v4 gv = *reinterpret_cast<const v4*>(Gc + crow);
-        const float glast = Gc[kChunk - 1];
-
-        // 1. state slice -> LDS
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) S_l[s_idx(32 * w + 16 * tt + 4 * lg4 + r, li)] = S[tt][r];
-        __syncthreads();
-
-        // 2. W S and Q S for rows 16w..16w+15 (k index of block b, lane group g: 32 g + b).
-        v4 ws = {0.f, 0.f, 0.f, 0.f}, qs = ws;
-#pragma unroll
-        for (int m = 0; m < 8; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float bv = S_l[s_idx(32 * lg4 + 4 * m + e, li)];
-                ws = mfma4(aw[m][e], bv, ws);
-                qs = mfma4(aq[m][e], bv, qs);
-            }
-
-        // 3. D = U - W S; D and exp(G_last - G_t) D to LDS.
-        v4 d;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            d[r] = u[r] - ws[r];
-            D_l[d_idx(crow + r, li)] = d[r];
-            Dg_l[d_idx(crow + r, li)] = expf(glast - gv[r]) * d[r];
+        for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(st + 16 * tt) = S[tt];
+    } else {
+        OutOps A, B;                               // same schedule as the state waves
+        load_out_ops(x, c_begin, A);
+        int c = c_begin;
+        for (; c + 1 < c_end; c += 2) {
+            load_out_ops(x, c + 1, B);
+            out_step(x, A, S_l, D_l);
+            __builtin_amdgcn_sched_barrier(0);
+            load_out_ops(x, min(c + 2, c_end - 1), A);
+            out_step(x, B, S_l, D_l);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
-
-        // 4. O = diag(Gam) Q S + M D (k index 16 g + b).
-        v4 ov;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) ov[r] = expf(gv[r]) * qs[r];
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ov = mfma4(am[m][e], D_l[d_idx(16 * lg4 + 4 * m + e, li)], ov);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = crow + r;
-            if (t < len) {
-                const size_t oo = ((size_t)(t0 + t) * L.h_v + h) * kD + j0 + li;
-                if (p.o) p.o[oo] = ov[r];
-                if (p.o_bf16) p.o_bf16[oo] = f32_to_bf16(ov[r]);
-            }
-        }
-
-        // 5. S' = Gam_last S + K^T (exp(G_last - G) D), k index 16 g + b over the chunk rows.
-        const float gl = expf(glast);
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            S[tt] *= gl;
-            const int col = 32 * w + 16 * tt + li;            // A-operand row of K^T = k dim
-#pragma unroll
-            for (int b = 0; b < 16; ++b) {
-                const int t = 16 * lg4 + b;
-                const float kv = t < len ? kbase[(size_t)(t0 + t) * kD + col] : 0.0f;
-                S[tt] = mfma4(kv, Dg_l[d_idx(t, li)], S[tt]);
-            }
-        }
+        if (c < c_end) out_step(x, A, S_l, D_l);
     }
-
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(st + 16 * tt) = S[tt];
 }
 
 }  // namespace
@@ -546,7 +663,7 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c);
 
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    size_t off[13];
+    size_t off[ixg::kWsSections];
     return ixg::ws_layout(cfg, n_seq, total_T, off);
 }
 
@@ -564,7 +681,7 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     if (!x || !a || !b || !workspace) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(workspace) & 255) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(state) & 15) return hipErrorInvalidValue;      // float4 state accesses
-    size_t off[13];
+    size_t off[kWsSections];
     const size_t need = ws_layout(cfg, n_seq, total_T, off);
     if (workspace_bytes < need) return hipErrorInvalidValue;
     const long long NC = (total_T + kChunk - 1) / kChunk + (long long)n_seq;
@@ -579,11 +696,16 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     p.n_seq = n_seq; p.T = total_T; p.NC = (int)NC;
 
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    hipLaunchKernelGGL(prep_kernel, dim3((unsigned)NC, (unsigned)(cfg->h_k + cfg->h_v)), dim3(256), 0, s, p);
+    const dim3 pgrid((unsigned)NC, (unsigned)(2 * cfg->h_k + cfg->h_v));
+    switch (cfg->d_conv) {
+        case 2: hipLaunchKernelGGL(prep_kernel<2>, pgrid, dim3(256), 0, s, p); break;
+        case 3: hipLaunchKernelGGL(prep_kernel<3>, pgrid, dim3(256), 0, s, p); break;
+        default: hipLaunchKernelGGL(prep_kernel<4>, pgrid, dim3(256), 0, s, p); break;
+    }
     const size_t nch = (size_t)n_seq * p.L.C;
     hipLaunchKernelGGL(commit_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, s, p);
-    hipLaunchKernelGGL(chunk_kernel, dim3((unsigned)NC, (unsigned)cfg->h_k), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(chunk_kernel, dim3((unsigned)NC, (unsigned)cfg->h_v), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
-    hipLaunchKernelGGL(chain_kernel, dim3((unsigned)(groups * 64)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(chain_kernel, dim3((unsigned)(groups * 64)), dim3(512), 0, s, p);
     return hipGetLastError();
 }

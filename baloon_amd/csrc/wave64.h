@@ -51,6 +51,15 @@ __device__ __forceinline__ float wave_sum(float v) {
     return pair_sum32(pair_sum16(row_sum16(v)));
 }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() also orders global
+// memory, which makes every wave wait for all of its outstanding global loads (vmcnt(0))
+// before the barrier -- including loads issued early on purpose to prefetch later work.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Double-precision 64-lane sum, result in every lane (xor butterfly on ds_swizzle/bpermute).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
