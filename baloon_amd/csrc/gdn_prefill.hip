@@ -452,15 +452,15 @@ constexpr int kDCol = kChunk + 4;      // D tile column stride
 // chunk tiles as MFMA A operands and rows 16 r + 4 lg4 + i in C layout; state wave r owns
 // state rows (k index) 32 r .. 32 r + 31.
 struct StateOps {
-    v4 aw[8];             // W row 16r+li, k = 32 lg4 + 4 m + e
-    v4 kt[2][4];          // K^T row 32 r + 16 tt + li, token 16 lg4 + 4 q + e
+    v4 aw[8];             // W row 16r+li, k = 16 m + 4 lg4 + e
+    v4 kt[2][4];          // K^T row 32 r + 16 tt + li, token 16 q + 4 lg4 + e
     v4 u;                 // U rows 16r + 4 lg4 + i, column j0 + li
     v4 gv;                // G at those rows
     float glast;          // G of the chunk's last row
 };
 struct OutOps {
     v4 aq[8];             // Q row 16r+li (the last row again past the chunk end)
-    v4 am[4];             // M row 16r+li, s = 16 lg4 + 4 m + e
+    v4 am[4];             // M row 16r+li, s = 16 m + 4 lg4 + e
     v4 gv;
     int t0, len;
 };
@@ -481,12 +481,12 @@ __device__ __forceinline__ void load_state_ops(const ChainCtx& x, int c, StateOp
     const float* Kc = p.ws.Kt + ((size_t)c * p.L.h_k + x.src) * kD * kChunk;
     const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) o.aw[m] = *reinterpret_cast<const v4*>(Wc + (size_t)arow * kD + 32 * x.lg4 + 4 * m);
+    for (int m = 0; m < 8; ++m) o.aw[m] = *reinterpret_cast<const v4*>(Wc + (size_t)arow * kD + 16 * m + 4 * x.lg4);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            o.kt[tt][q] = *reinterpret_cast<const v4*>(Kc + (size_t)(32 * x.r + 16 * tt + x.li) * kChunk + 16 * x.lg4 + 4 * q);
+            o.kt[tt][q] = *reinterpret_cast<const v4*>(Kc + (size_t)(32 * x.r + 16 * tt + x.li) * kChunk + 16 * q + 4 * x.lg4);
     o.u = *reinterpret_cast<const v4*>(p.ws.Ut + (ch * kD + x.j0 + x.li) * kChunk + crow);
     o.gv = *reinterpret_cast<const v4*>(Gc + crow);
     o.glast = Gc[kChunk - 1];
@@ -500,12 +500,12 @@ __device__ __forceinline__ void load_out_ops(const ChainCtx& x, int c, OutOps& o
     const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
     // Q rows past the chunk end re-read its last row: an MFMA output row depends only on its
     // own A row, so those rows only produce output rows that are never stored.
-    const float* qr = x.qbase + (size_t)(o.t0 + min(arow, o.len - 1)) * kD + 32 * x.lg4;
+    const float* qr = x.qbase + (size_t)(o.t0 + min(arow, o.len - 1)) * kD + 4 * x.lg4;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) o.aq[m] = *reinterpret_cast<const v4*>(qr + 4 * m);
+    for (int m = 0; m < 8; ++m) o.aq[m] = *reinterpret_cast<const v4*>(qr + 16 * m);
     const float* Mc = p.ws.M + ch * kChunk * kChunk;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) o.am[m] = *reinterpret_cast<const v4*>(Mc + (size_t)arow * kChunk + 16 * x.lg4 + 4 * m);
+    for (int m = 0; m < 4; ++m) o.am[m] = *reinterpret_cast<const v4*>(Mc + (size_t)arow * kChunk + 16 * m + 4 * x.lg4);
     o.gv = *reinterpret_cast<const v4*>(p.ws.G + ch * kChunk + crow);
 }
 
@@ -517,11 +517,12 @@ __device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o,
     for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(S_l + li * kSCol + 32 * r + 16 * tt + 4 * lg4) = S[tt];
     lds_barrier();                                                    // (A) state slice visible
 
-    // W S for rows 16r..16r+15; k index of block (m, e), lane group g: 32 g + 4 m + e.
+    // W S for rows 16r..16r+15; k index of block (m, e), lane group g: 16 m + 4 g + e (each
+    // load instruction of a wave then reads 64 contiguous bytes of 16 operand rows).
     v4 ws[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 32 * lg4 + 4 * m);
+        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 16 * m + 4 * lg4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) ws[m & 1] = mfma4(o.aw[m][e], bv[e], ws[m & 1]);
     }
@@ -535,11 +536,11 @@ __device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o,
     *reinterpret_cast<v4*>(Dg_l + li * kDCol + crow) = dg;
     lds_barrier();                                                    // (B) D visible
 
-    // S' = Gam_last S + K^T Dg; k index 16 g + b over the chunk rows.
+    // S' = Gam_last S + K^T Dg; token index of block (q, e): 16 q + 4 g + e.
     const float gl = expf(o.glast);
     v4 dgv[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) dgv[m] = *reinterpret_cast<const v4*>(Dg_l + li * kDCol + 16 * lg4 + 4 * m);
+    for (int m = 0; m < 4; ++m) dgv[m] = *reinterpret_cast<const v4*>(Dg_l + li * kDCol + 16 * m + 4 * lg4);
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
         v4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -561,7 +562,7 @@ __device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, con
     v4 qs[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
     for (int m = 0; m < 8; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 32 * lg4 + 4 * m);
+        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 16 * m + 4 * lg4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) qs[m & 1] = mfma4(o.aq[m][e], bv[e], qs[m & 1]);
     }
@@ -571,7 +572,7 @@ __device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, con
     for (int i = 0; i < 4; ++i) { ov[0][i] = expf(o.gv[i]) * (qs[0][i] + qs[1][i]); ov[1][i] = 0.0f; }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(D_l + li * kDCol + 16 * lg4 + 4 * m);
+        const v4 bv = *reinterpret_cast<const v4*>(D_l + li * kDCol + 16 * m + 4 * lg4);
 #pragma unroll
         for (int e = 0; e < 4; ++e) ov[m & 1] = mfma4(o.am[m][e], bv[e], ov[m & 1]);
     }
