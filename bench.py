@@ -101,13 +101,17 @@ def decode_bench(args):
     avg_launch_s = total_ms / K / 1e3          # average launch duration seen by the stream
     state_bytes = 2 * B * hv * STATE_TILE
     achieved = state_bytes / avg_launch_s / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(tf) and B == 64 and L == 4:
+        traffic = json.load(open(tf))["bytes_per_launch"]      # PMC-measured HBM bytes per launch
     return dict(
         tokens_per_s=B * K / (total_ms / 1e3),
         ms_per_step=total_ms / K,
         avg_kernel_us=avg_launch_s * 1e6,
         state_bytes_per_launch=state_bytes,
         roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None),
+                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic),
     )
 
 
