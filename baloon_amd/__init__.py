@@ -31,7 +31,7 @@ ACT_SILU = 1
 EXPORTS = (
     "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
     "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
-    "ix_gdn_prefill",
+    "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
     "ix_gdn_version",
 )
 
@@ -55,6 +55,15 @@ class Cfg(ctypes.Structure):
     @property
     def channels(self) -> int:
         return 2 * self.h_k * self.d_k + self.h_v * self.d_v
+
+
+class OutGate(ctypes.Structure):
+    """``ix_gdn_out_gate`` (include/ix_gdn.h): y = o / sqrt(mean(o^2) + eps) * ssm_norm * sigmoid(z)."""
+
+    _fields_ = [
+        ("z", ctypes.c_void_p), ("ssm_norm", ctypes.c_void_p), ("eps", ctypes.c_float),
+        ("y", ctypes.c_void_p), ("y_bf16", ctypes.c_void_p),
+    ]
 
 
 def make_cfg(h_k=16, h_v=32, d_k=128, d_v=128, d_conv=4, head_map=HEAD_MOD, conv_act=ACT_NONE,
@@ -86,6 +95,9 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_decode": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_prefill_workspace_size": ([P, I, I], Z),
         "ix_gdn_prefill": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
+        "ix_gdn_decode_gated": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_gdn_prefill_gated_workspace_size": ([P, I, I], Z),
+        "ix_gdn_prefill_gated": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
     }
     for name, (args, res) in sig.items():
@@ -153,8 +165,8 @@ def ix_gdn_decode(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, stat
     """One decode token for B sequences. bf16 tensors may be torch.bfloat16 or int16/uint16 bits.
 
     state is [B][h_v][d_v][d_k] fp32 (each head's state stored column by column). workspace,
-    if given, is a zero-filled device buffer of ix_gdn_decode_workspace_size(cfg, B) bytes
-    (left zeroed by every call); it selects the faster many-workgroup kernel."""
+    if given, is a device buffer of ix_gdn_decode_workspace_size(cfg, B) bytes, zero-filled
+    once (the calls keep its counters at zero); it selects the faster many-workgroup kernel."""
     return lib().ix_gdn_decode(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b),
                                _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), _ptr(workspace),
                                _stream(s))
@@ -169,6 +181,35 @@ def ix_gdn_prefill(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, 
     return lib().ix_gdn_prefill(ctypes.byref(cfg), n_seq, total_T, _ptr(cu_seqlens), _ptr(x), _ptr(conv_state),
                                 _ptr(conv_w), _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o),
                                 _ptr(o_bf16), _ptr(workspace), workspace_bytes, _stream(s))
+
+
+def out_gate(z, ssm_norm, eps, y=None, y_bf16=None) -> OutGate:
+    """The gate description of the gated calls, from device tensors (z bf16, ssm_norm fp32)."""
+    return OutGate(_ptr(z), _ptr(ssm_norm), eps, _ptr(y), _ptr(y_bf16))
+
+
+def ix_gdn_decode_gated(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
+                        gate: OutGate | None = None, workspace=None, s=None) -> int:
+    """ix_gdn_decode plus the gated RMS output norm of each (sequence, v head) in the same launch."""
+    g = ctypes.byref(gate) if gate is not None else None
+    return lib().ix_gdn_decode_gated(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a),
+                                     _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), g,
+                                     _ptr(workspace), _stream(s))
+
+
+def ix_gdn_prefill_gated_workspace_size(cfg: Cfg, n_seq: int, total_T: int) -> int:
+    return lib().ix_gdn_prefill_gated_workspace_size(ctypes.byref(cfg), n_seq, total_T)
+
+
+def ix_gdn_prefill_gated(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, a, b, A_log, dt_bias, state,
+                         o=None, o_bf16=None, gate: OutGate | None = None, workspace=None, workspace_bytes=0,
+                         s=None) -> int:
+    """ix_gdn_prefill plus the gated RMS output norm of every (token, v head) row."""
+    g = ctypes.byref(gate) if gate is not None else None
+    return lib().ix_gdn_prefill_gated(ctypes.byref(cfg), n_seq, total_T, _ptr(cu_seqlens), _ptr(x),
+                                      _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias),
+                                      _ptr(state), _ptr(o), _ptr(o_bf16), g, _ptr(workspace), workspace_bytes,
+                                      _stream(s))
 
 
 def version() -> str:

@@ -70,4 +70,49 @@ __device__ __forceinline__ float log_gate(const Layer& L, int h, float a) {
     return -expf(L.A_log[h]) * softplus_f(a + L.dt_bias[h]);
 }
 
+// Device copy of ix_gdn_out_gate.
+struct OutGate {
+    const uint16_t* z;
+    const float* nrm;
+    float eps;
+    float* y;
+    uint16_t* y_bf16;
+};
+
+inline OutGate make_out_gate(const ix_gdn_out_gate* g) {
+    OutGate o{};
+    if (g) { o.z = g->z; o.nrm = g->ssm_norm; o.eps = g->eps; o.y = g->y; o.y_bf16 = g->y_bf16; }
+    return o;
+}
+
+// Sum of v^2 over the wave, the same bits in every lane and in every kernel that calls it:
+// each square is rounded before the sums (left to itself the compiler fuses it into the
+// first DPP add, whose result then differs between lanes), and lane 0's total is broadcast.
+__device__ __forceinline__ float wave_sum_sq(float v) {
+    float sq = v * v;
+    __asm__("" : "+v"(sq));
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(wave_sum(sq))));
+}
+
+// Gated RMS norm of one head's 128 outputs, called by a whole wave: lane l holds o of
+// columns l (lo) and 64 + l (hi); row is the offset of the head's first element in z and y.
+// The sum of squares is (sum over columns 0..63) + (sum over 64..127), each a wave_sum_sq,
+// so every kernel that holds the head in this form gets the same bits.
+// out_gate_apply takes the two partial sums already reduced.
+__device__ __forceinline__ void out_gate_apply(const OutGate& g, size_t row, float lo, float hi, float ss_lo,
+                                               float ss_hi, int lane) {
+    const float ss = ss_lo + ss_hi;
+    const float inv = 1.0f / sqrtf(ss * (1.0f / kD) + g.eps);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int j = lane + q * (kD / 2);
+        const float y = (q ? hi : lo) * inv * g.nrm[j] * sigmoid_f(bf16_to_f32(g.z[row + j]));
+        if (g.y) g.y[row + j] = y;
+        if (g.y_bf16) g.y_bf16[row + j] = f32_to_bf16(y);
+    }
+}
+__device__ __forceinline__ void out_gate_head(const OutGate& g, size_t row, float lo, float hi, int lane) {
+    out_gate_apply(g, row, lo, hi, wave_sum_sq(lo), wave_sum_sq(hi), lane);
+}
+
 }  // namespace ixg

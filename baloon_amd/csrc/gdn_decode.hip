@@ -26,6 +26,11 @@
 //    again when the kernel ends. No workgroup ever waits for another.
 //  * group_kernel (no workspace): one workgroup per (sequence, q/k head) that owns every
 //    channel and tile of the group; race free by ownership.
+// Both have a gated variant (ix_gdn_decode_gated) that ends with the gated RMS output norm
+// of each head (the semantics of ix_gdn_out_norm, src/ix_gdn.cu:87-100). The group kernel
+// holds whole heads; in the slab kernel the two half-tile workgroups of a head publish their
+// 64 outputs and partial sum of squares to the workspace before their state stores, and
+// the second to count in on the head's counter finishes the head (again without waiting).
 // State loads use nontemporal hints and are issued right after the conv inputs so that
 // HBM latency overlaps the conv; the state is streamed once per token.
 #include "gdn_common.h"
@@ -47,7 +52,26 @@ struct DecodeParams {
     float* state;               // [B][h_v][d_v][d_k]
     float* o;                   // [B][h_v][128] or null
     uint16_t* o_bf16;           // [B][h_v][128] or null
+    OutGate og;                 // gated variant only
 };
+
+// Workspace sections (each 256-byte aligned): group counters [B][h_k], head counters
+// [B][h_v], exchanged half-head outputs [B][h_v][2][64] and their sums of squares
+// [B][h_v][2]. The counters are zero between calls; the rest is scratch.
+struct DecodeWs {
+    int* group;
+    int* head;
+    float* xo;
+    float* xs;
+};
+
+inline size_t decode_ws_layout(int B, int h_k, int h_v, size_t (&off)[4]) {
+    const size_t sz[4] = {(size_t)B * h_k * 4, (size_t)B * h_v * 4, (size_t)B * h_v * 2 * kHalfCols * 4,
+                          (size_t)B * h_v * 2 * 4};
+    size_t at = 0;
+    for (int i = 0; i < 4; ++i) { off[i] = at; at += (sz[i] + 255) & ~(size_t)255; }
+    return at;
+}
 
 // Sum over the 32 lanes of each half wave, result in all of them.
 __device__ __forceinline__ float half_sum(float v) { return pair_sum16(row_sum16(v)); }
@@ -118,7 +142,8 @@ __device__ __forceinline__ void gates(const DecodeParams& p, int bseq, int h, fl
 
 // The column update for one pair of columns held as one float4 per lane (see the header).
 // kr, qr: this lane's 4 entries of the normalised k and q; vj: v of this lane's column.
-__device__ __forceinline__ void column_update(const DecodeParams& p, v4f s, v4f* dst, const v4f& kr, const v4f& qr,
+// Returns the column's output (valid in every lane).
+__device__ __forceinline__ float column_update(const DecodeParams& p, v4f s, v4f* dst, const v4f& kr, const v4f& qr,
                                               float vj, float g, float bt, float kq, size_t o_index, bool writer) {
     float ak = s[0] * kr[0], aq = s[0] * qr[0];
 #pragma unroll
@@ -130,20 +155,80 @@ __device__ __forceinline__ void column_update(const DecodeParams& p, v4f s, v4f*
 #pragma unroll
     for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[e], d, s[e] * g);
     __builtin_nontemporal_store(r, dst);
+    const float ov = fmaf(d, kq, g * aq);
     if (writer) {
-        const float ov = fmaf(d, kq, g * aq);
         if (p.o) p.o[o_index] = ov;
         if (p.o_bf16) p.o_bf16[o_index] = f32_to_bf16(ov);
     }
+    return ov;
+}
+
+// The same column math split in two: the sums and the output first, the state store later.
+__device__ __forceinline__ float column_reduce(const DecodeParams& p, const v4f& s, const v4f& kr, const v4f& qr,
+                                               float vj, float g, float bt, float kq, size_t o_index, bool writer,
+                                               float& d) {
+    float ak = s[0] * kr[0], aq = s[0] * qr[0];
+#pragma unroll
+    for (int e = 1; e < 4; ++e) { ak = fmaf(s[e], kr[e], ak); aq = fmaf(s[e], qr[e], aq); }
+    ak = half_sum(ak);
+    aq = half_sum(aq);
+    d = (vj - g * ak) * bt;
+    const float ov = fmaf(d, kq, g * aq);
+    if (writer) {
+        if (p.o) p.o[o_index] = ov;
+        if (p.o_bf16) p.o_bf16[o_index] = f32_to_bf16(ov);
+    }
+    return ov;
+}
+__device__ __forceinline__ void column_store(const v4f& s, v4f* dst, const v4f& kr, float d, float g) {
+    v4f r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[e], d, s[e] * g);
+    __builtin_nontemporal_store(r, dst);
+}
+
+// Gated norm of head (bseq, h) split over two workgroups, run by one whole wave of each:
+// lane l holds the output of column hf*64 + l. Each publishes its half and partial sum of
+// squares, then counts in; the second to count in reads the other half and writes y for the
+// head, then resets the counter.
+// The published values go through agent-scope atomic stores and loads, which are coherent
+// across the XCDs' L2 caches without cache maintenance (an agent-scope fence would write
+// back and invalidate the whole L2, full of this kernel's state lines, per workgroup). The
+// stores are complete (vmcnt 0) before the counting atomic is issued, and the reads are
+// issued only after it has returned the partner's count.
+__device__ __forceinline__ void head_gate_exchange(const DecodeParams& p, const DecodeWs& ws, int bseq, int h,
+                                                   int hf, float v, int lane) {
+    const size_t hd = (size_t)bseq * p.L.h_v + h;
+    const float part = wave_sum_sq(v);
+    __hip_atomic_store(ws.xo + (hd * 2 + hf) * kHalfCols + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(ws.xs + hd * 2 + hf, part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    int last = 0;
+    if (lane == 0) {
+        last = __hip_atomic_fetch_add(ws.head + hd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
+        if (last) __hip_atomic_store(ws.head + hd, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    last = __builtin_amdgcn_readfirstlane(last);
+    if (!last) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const int oh = hf ^ 1;
+    const float vo =
+        __hip_atomic_load(ws.xo + (hd * 2 + oh) * kHalfCols + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float po = __hip_atomic_load(ws.xs + hd * 2 + oh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out_gate_apply(p.og, hd * kD, hf ? vo : v, hf ? v : vo, hf ? po : part, hf ? part : po, lane);
 }
 
 // ---------------------------------------------------------------------------------------
 // slab_kernel: grid (2 h_v, B); workgroup = (sequence bseq, v head h, half tile hf)
 // ---------------------------------------------------------------------------------------
-template <int DC>
+template <int DC, bool GATED>
 __global__ void __launch_bounds__(kThreads)
-slab_kernel(const DecodeParams p, int* __restrict__ counters) {
+slab_kernel(const DecodeParams p, const DecodeWs ws) {
     __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kHalfCols];
+    __shared__ float o_s[GATED ? kHalfCols : 1];
+    int* __restrict__ counters = ws.group;
     __shared__ float scal_s[2], gb_s[2];
     __shared__ int last_s;
 
@@ -201,10 +286,25 @@ slab_kernel(const DecodeParams p, int* __restrict__ counters) {
     }
     const float g = gb_s[0], bt = gb_s[1];
     const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
+    if constexpr (!GATED) {
 #pragma unroll
-    for (int u = 0; u < kPairsPerWave; ++u) {
-        const int j = j0 + 2 * u;
-        column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0);
+        for (int u = 0; u < kPairsPerWave; ++u) {
+            const int j = j0 + 2 * u;
+            column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j,
+                          i4 == 0);
+        }
+    } else {
+        float dv[kPairsPerWave];
+#pragma unroll
+        for (int u = 0; u < kPairsPerWave; ++u) {
+            const int j = j0 + 2 * u;
+            const float ov = column_reduce(p, s[u], kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0, dv[u]);
+            if (i4 == 0) o_s[j - hf * kHalfCols] = ov;
+        }
+        __syncthreads();
+        if (w == 0) head_gate_exchange(p, ws, bseq, h, hf, o_s[lane], lane);
+#pragma unroll
+        for (int u = 0; u < kPairsPerWave; ++u) column_store(s[u], tile + (size_t)(j0 + 2 * u) * (kD / 4), kr, dv[u], g);
     }
 
     __syncthreads();
@@ -229,11 +329,12 @@ __device__ __forceinline__ int pair_channel(const Layer& L, int src, int e, floa
     return v_channel(L, mapped_head(L, src, t), j);
 }
 
-template <int DC>
+template <int DC, bool GATED>
 __global__ void __launch_bounds__(kThreads)
 group_kernel(const DecodeParams p) {
     __shared__ __align__(16) float q_s[kD], k_s[kD];
     __shared__ __align__(16) float v_s[kMaxHeadsPerGroup][kD];
+    __shared__ float o_s[GATED ? kMaxHeadsPerGroup : 1][kD];
     __shared__ float gate_s[kMaxHeadsPerGroup][2];
     __shared__ float scal_s[3];
 
@@ -301,7 +402,9 @@ group_kernel(const DecodeParams p) {
             if (base + u >= per_wave) break;
             const int pr = p0 + base + u, col = 2 * pr + half, t = col / kD, j = col % kD;
             const size_t oi = ((size_t)bseq * L.h_v + mapped_head(L, src, t)) * kD + j;
-            column_update(p, buf[u], col_ptr(pr), kr, qr, v_s[t][j], gate_s[t][0], gate_s[t][1], kq, oi, i4 == 0);
+            const float ov =
+                column_update(p, buf[u], col_ptr(pr), kr, qr, v_s[t][j], gate_s[t][0], gate_s[t][1], kq, oi, i4 == 0);
+            if (GATED && i4 == 0) o_s[t][j] = ov;
         }
     };
     // Two batches in flight; the loop body is unrolled so no register is copied while its
@@ -312,6 +415,41 @@ group_kernel(const DecodeParams p) {
         process(b1, base + kGroupBatch);
         load(b1, base + 3 * kGroupBatch);
     }
+    if constexpr (GATED) {
+        __syncthreads();
+        for (int t = w; t < count; t += kThreads / kWave)
+            out_gate_head(p.og, ((size_t)bseq * L.h_v + mapped_head(L, src, t)) * kD, o_s[t][lane],
+                          o_s[t][lane + kWave], lane);
+    }
+}
+
+template <bool GATED>
+void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, void* workspace, hipStream_t s) {
+    // The slab kernel needs every q/k head to feed at least one v head (its history is
+    // written by the group's last member); otherwise, and without a workspace, one
+    // workgroup owns each group.
+    const bool every_src_used = cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
+    const dim3 block(kThreads);
+    if (workspace && every_src_used) {
+        size_t off[4];
+        decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
+        char* base = static_cast<char*>(workspace);
+        const DecodeWs ws{reinterpret_cast<int*>(base + off[0]), reinterpret_cast<int*>(base + off[1]),
+                          reinterpret_cast<float*>(base + off[2]), reinterpret_cast<float*>(base + off[3])};
+        const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
+        switch (cfg->d_conv) {
+            case 2: hipLaunchKernelGGL((slab_kernel<2, GATED>), grid, block, 0, s, p, ws); break;
+            case 3: hipLaunchKernelGGL((slab_kernel<3, GATED>), grid, block, 0, s, p, ws); break;
+            default: hipLaunchKernelGGL((slab_kernel<4, GATED>), grid, block, 0, s, p, ws); break;
+        }
+    } else {
+        const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
+        switch (cfg->d_conv) {
+            case 2: hipLaunchKernelGGL((group_kernel<2, GATED>), grid, block, 0, s, p); break;
+            case 3: hipLaunchKernelGGL((group_kernel<3, GATED>), grid, block, 0, s, p); break;
+            default: hipLaunchKernelGGL((group_kernel<4, GATED>), grid, block, 0, s, p); break;
+        }
+    }
 }
 
 }  // namespace
@@ -321,7 +459,7 @@ extern "C" int ix_gdn_channels(const ix_gdn_cfg* c) {
     return c ? 2 * c->h_k * c->d_k + c->h_v * c->d_v : 0;
 }
 
-extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.3.0 gfx950"; }
+extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.4.0 gfx950"; }
 
 // Shared validation of the fused layer description (also used by the prefill).
 extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
@@ -340,13 +478,15 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
 
 extern "C" size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || B <= 0 || B > 65535) return 0;
-    return ((size_t)B * cfg->h_k * sizeof(int32_t) + 255) & ~(size_t)255;
+    size_t off[4];
+    return ixg::decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
 }
 
-extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
-                                    const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
-                                    const float* A_log, const float* dt_bias, float* state, float* o,
-                                    uint16_t* o_bf16, void* workspace, hipStream_t s) {
+// Validation and parameter set-up shared by the plain and gated decode.
+static hipError_t decode_params(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                                const uint16_t* conv_w, const uint16_t* a, const uint16_t* b, const float* A_log,
+                                const float* dt_bias, float* state, float* o, uint16_t* o_bf16, void* workspace,
+                                ixg::DecodeParams& p) {
     const hipError_t e = ix_gdn_check_cfg_(cfg);
     if (e != hipSuccess) return e;
     if (B <= 0 || B > 65535) return hipErrorInvalidValue;
@@ -357,30 +497,45 @@ extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t
     if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(conv_state) |
          reinterpret_cast<uintptr_t>(conv_w) | reinterpret_cast<uintptr_t>(workspace)) & 3)
         return hipErrorInvalidValue;                 // conv inputs and counters are dwords
-    ixg::DecodeParams p;
     p.L = ixg::make_layer(cfg, conv_w, A_log, dt_bias);
     p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
-    // The slab kernel needs every q/k head to feed at least one v head (its history is
-    // written by the group's last member); otherwise, and without a workspace, one
-    // workgroup owns each group.
-    const bool every_src_used = cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
-    const dim3 block(ixg::kThreads);
-    if (workspace && every_src_used) {
-        int* ctr = static_cast<int*>(workspace);
-        const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
-        switch (cfg->d_conv) {
-            case 2: hipLaunchKernelGGL(ixg::slab_kernel<2>, grid, block, 0, s, p, ctr); break;
-            case 3: hipLaunchKernelGGL(ixg::slab_kernel<3>, grid, block, 0, s, p, ctr); break;
-            default: hipLaunchKernelGGL(ixg::slab_kernel<4>, grid, block, 0, s, p, ctr); break;
-        }
-    } else {
-        const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
-        switch (cfg->d_conv) {
-            case 2: hipLaunchKernelGGL(ixg::group_kernel<2>, grid, block, 0, s, p); break;
-            case 3: hipLaunchKernelGGL(ixg::group_kernel<3>, grid, block, 0, s, p); break;
-            default: hipLaunchKernelGGL(ixg::group_kernel<4>, grid, block, 0, s, p); break;
-        }
-    }
+    p.og = ixg::OutGate{};
+    return hipSuccess;
+}
+
+// The gate description of the gated calls: z and ssm_norm, at least one output, aligned.
+extern "C" hipError_t ix_gdn_check_gate_(const ix_gdn_out_gate* g) {
+    if (!g || !g->z || !g->ssm_norm || (!g->y && !g->y_bf16)) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(g->z) & 1) || (reinterpret_cast<uintptr_t>(g->ssm_norm) & 3) ||
+        (reinterpret_cast<uintptr_t>(g->y) & 3) || (reinterpret_cast<uintptr_t>(g->y_bf16) & 1))
+        return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                                    const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
+                                    const float* A_log, const float* dt_bias, float* state, float* o,
+                                    uint16_t* o_bf16, void* workspace, hipStream_t s) {
+    ixg::DecodeParams p;
+    const hipError_t e = decode_params(cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16,
+                                       workspace, p);
+    if (e != hipSuccess) return e;
+    ixg::launch_decode<false>(cfg, B, p, workspace, s);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                                          const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
+                                          const float* A_log, const float* dt_bias, float* state, float* o,
+                                          uint16_t* o_bf16, const ix_gdn_out_gate* gate, void* workspace,
+                                          hipStream_t s) {
+    ixg::DecodeParams p;
+    hipError_t e = decode_params(cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16,
+                                 workspace, p);
+    if (e != hipSuccess) return e;
+    if ((e = ix_gdn_check_gate_(gate)) != hipSuccess) return e;
+    p.og = ixg::make_out_gate(gate);
+    ixg::launch_decode<true>(cfg, B, p, workspace, s);
     return hipGetLastError();
 }

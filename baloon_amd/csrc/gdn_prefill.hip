@@ -657,10 +657,24 @@ __global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// out_gate_kernel: gated RMS output norm of every (token, v head) row, one wave per row,
+// reading the fp32 outputs the chain wrote (ix_gdn_prefill_gated only).
+// ---------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) out_gate_kernel(const float* __restrict__ o, const OutGate g, long long rows) {
+    const long long r = (long long)blockIdx.x * 4 + threadIdx.x / kWave;
+    if (r >= rows) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t row = (size_t)r * kD;
+    out_gate_head(g, row, o[row + lane], o[row + lane + kWave], lane);
+}
+
 }  // namespace
 }  // namespace ixg
 
 extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c);
+
+extern "C" hipError_t ix_gdn_check_gate_(const ix_gdn_out_gate* g);
 
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
@@ -668,14 +682,22 @@ extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq
     return ixg::ws_layout(cfg, n_seq, total_T, off);
 }
 
-extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
-                                     const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
-                                     const uint16_t* a, const uint16_t* b, const float* A_log,
-                                     const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
-                                     void* workspace, size_t workspace_bytes, hipStream_t s) {
+// The gated prefill's workspace: the prefill's, then [total_T][h_v][d_v] fp32 outputs.
+extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
+    const size_t base = ix_gdn_prefill_workspace_size(cfg, n_seq, total_T);
+    if (!base) return 0;
+    return base + (((size_t)total_T * cfg->h_v * ixg::kD * sizeof(float) + 255) & ~(size_t)255);
+}
+
+static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
+                               const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                               const uint16_t* b, const float* A_log, const float* dt_bias, float* state, float* o,
+                               uint16_t* o_bf16, const ix_gdn_out_gate* gate, void* workspace,
+                               size_t workspace_bytes, hipStream_t s) {
     using namespace ixg;
-    const hipError_t e = ix_gdn_check_cfg_(cfg);
+    hipError_t e = ix_gdn_check_cfg_(cfg);
     if (e != hipSuccess) return e;
+    if (gate && (e = ix_gdn_check_gate_(gate)) != hipSuccess) return e;
     if (n_seq <= 0 || total_T < 0) return hipErrorInvalidValue;
     if (!cu_seqlens || !conv_state || !conv_w || !A_log || !dt_bias || !state) return hipErrorInvalidValue;
     if (total_T == 0) return hipSuccess;                       // nothing to consume
@@ -684,10 +706,13 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     if (reinterpret_cast<uintptr_t>(state) & 15) return hipErrorInvalidValue;      // float4 state accesses
     size_t off[kWsSections];
     const size_t need = ws_layout(cfg, n_seq, total_T, off);
-    if (workspace_bytes < need) return hipErrorInvalidValue;
+    if (workspace_bytes < (gate ? ix_gdn_prefill_gated_workspace_size(cfg, n_seq, total_T) : need))
+        return hipErrorInvalidValue;
     const long long NC = (total_T + kChunk - 1) / kChunk + (long long)n_seq;
     const long long pairs = (long long)n_seq * cfg->h_v;
     if (NC > 0x7fffffffLL || pairs * kSlices > 0x7fffffffLL) return hipErrorInvalidValue;
+    const long long rows = (long long)total_T * cfg->h_v;
+    if (gate && (rows + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidValue;
 
     PrefillParams p;
     p.L = make_layer(cfg, conv_w, A_log, dt_bias);
@@ -695,6 +720,7 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     p.cu = cu_seqlens; p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
     p.n_seq = n_seq; p.T = total_T; p.NC = (int)NC;
+    if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
     const dim3 pgrid((unsigned)NC, (unsigned)(2 * cfg->h_k + cfg->h_v));
@@ -708,5 +734,28 @@ extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total
     hipLaunchKernelGGL(chunk_kernel, dim3((unsigned)NC, (unsigned)cfg->h_v), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
     hipLaunchKernelGGL(chain_kernel, dim3((unsigned)(groups * 64)), dim3(512), 0, s, p);
+    if (gate)
+        hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o,
+                           make_out_gate(gate), rows);
     return hipGetLastError();
+}
+
+extern "C" hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
+                                     const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
+                                     const uint16_t* a, const uint16_t* b, const float* A_log,
+                                     const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
+                                     void* workspace, size_t workspace_bytes, hipStream_t s) {
+    return prefill_impl(cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o,
+                        o_bf16, nullptr, workspace, workspace_bytes, s);
+}
+
+extern "C" hipError_t ix_gdn_prefill_gated(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
+                                           const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
+                                           const uint16_t* a, const uint16_t* b, const float* A_log,
+                                           const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
+                                           const ix_gdn_out_gate* gate, void* workspace, size_t workspace_bytes,
+                                           hipStream_t s) {
+    if (!gate) return hipErrorInvalidValue;
+    return prefill_impl(cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o,
+                        o_bf16, gate, workspace, workspace_bytes, s);
 }

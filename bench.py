@@ -44,7 +44,9 @@ def parse():
     return ap.parse_args()
 
 
-def decode_bench(args):
+def decode_bench(args, gated=False):
+    """B-sequence decode over rotated layers; gated=True times ix_gdn_decode_gated (the same
+    step with the gated output norm fused in, y written as bf16)."""
     import torch
 
     import baloon_amd as bx
@@ -69,14 +71,25 @@ def decode_bench(args):
                 b=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16)) for _ in range(P)]
     o = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
     ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device=dev)   # stream-ordered: shared
+    z = torch.randn(B, hv, 128, generator=g, device=dev).to(torch.bfloat16)
+    nrm = 1.0 + 0.1 * torch.randn(128, generator=g, device=dev)
+    y = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
+    gate = bx.out_gate(z, nrm, 1e-6, None, y)
     stream = torch.cuda.current_stream()
     lib = bx.lib()
     import ctypes
     cfg_ref = ctypes.byref(cfg)
     s_ptr = stream.cuda_stream
 
+    gate_ref = ctypes.byref(gate)
+
     def launch(i):
         Ly, In = layers[i % L], ins[i % P]
+        if gated:
+            return lib.ix_gdn_decode_gated(cfg_ref, B, In["x"].data_ptr(), Ly["cs"].data_ptr(), Ly["w"].data_ptr(),
+                                           In["a"].data_ptr(), In["b"].data_ptr(), Ly["A_log"].data_ptr(),
+                                           Ly["dt"].data_ptr(), Ly["state"].data_ptr(), None, None, gate_ref,
+                                           ws.data_ptr(), s_ptr)
         return lib.ix_gdn_decode(cfg_ref, B, In["x"].data_ptr(), Ly["cs"].data_ptr(), Ly["w"].data_ptr(),
                                  In["a"].data_ptr(), In["b"].data_ptr(), Ly["A_log"].data_ptr(), Ly["dt"].data_ptr(),
                                  Ly["state"].data_ptr(), None, o.data_ptr(), ws.data_ptr(), s_ptr)
@@ -263,7 +276,16 @@ def cpu_baseline(args):
         oracle.prefill(cfg, [0, Tp], tok["x"], st0["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
                        p["dt_bias"], st0["state"], nthreads=cores)
         pre[cores] = Tp / (time.perf_counter() - t0)
-    return dict(value=round(v, 1), unit="tokens/s", cores=best, kind="port",
+    cpu_model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu_model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(value=round(v, 1), unit="tokens/s", cores=best, kind="port", nproc=os.cpu_count(),
+                cpu_model=cpu_model,
                 sample=f"B={B} decode, {steps} steps in {el:.1f} s on {best} threads (oracle/gdn_oracle.c, double)",
                 value_1core=round(out[1][0], 1),
                 prefill_tokens_per_s=round(pre[best], 1), prefill_tokens_per_s_1core=round(pre[1], 1),
@@ -283,6 +305,7 @@ def main():
         sys.exit(1)
     torch.cuda.synchronize()
     d = decode_bench(args)
+    dg = decode_bench(args, gated=True)
     lat = decode_latency()
     pf = prefill_bench()
     ceiling = hbm_ceiling()
@@ -307,6 +330,8 @@ def main():
         "state_gbs": d["roofline"]["achieved"],
         "hbm_inplace_ceiling_gbs": ceiling,
         "decode_b1_us_per_token": lat,
+        "decode_gated": {"avg_kernel_us": round(dg["avg_kernel_us"], 2), "state_gbs": dg["roofline"]["achieved"],
+                         "note": "same step with the gated RMS output norm fused in (bf16 y instead of bf16 o)"},
         "prefill": pf,
         "roofline": d["roofline"],
         "cpu_baseline": cpu,

@@ -88,9 +88,24 @@ int ix_gdn_channels(const ix_gdn_cfg* cfg);
  * (d_k x d_v, S[i][j] with i the k index and j the v index) is stored column by column, so
  * element (b, h, i, j) is at ((b*h_v + h)*d_v + j)*d_k + i and every column is contiguous. */
 
-/* Bytes of the counter workspace ix_gdn_decode can use for B sequences (B*h_k int32, rounded
- * up to 256), or 0 for an invalid description. */
+/* Bytes of the workspace ix_gdn_decode and ix_gdn_decode_gated can use for B sequences, or 0
+ * for an invalid description. It holds per-group counters (which the calls keep at zero) and
+ * per-head exchange slots for the gated output norm (scratch, never needs clearing). */
 size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B);
+
+/* Gated RMS output norm fused into a layer call's epilogue: for every token row and v head,
+ *   y = o / sqrt(mean(o^2) + eps) * ssm_norm * sigmoid(z)
+ * over the head's d_v outputs -- the semantics of ix_gdn_out_norm (src/ix_gdn.cu:87-100:
+ * products in that order, sigmoid(x) = 1/(1+exp(-x))) with fp32 accumulation of the sum of
+ * squares, taken as (sum of columns 0..63) + (sum of columns 64..127). Read on the host at
+ * call time. */
+typedef struct ix_gdn_out_gate {
+    const uint16_t* z;        /* [rows][h_v][d_v] bf16 gate logits (from the in-projection) */
+    const float* ssm_norm;    /* [d_v] fp32 norm weight shared by all heads */
+    float eps;
+    float* y;                 /* [rows][h_v][d_v] fp32, or NULL */
+    uint16_t* y_bf16;         /* [rows][h_v][d_v] bf16 (RNE of the fp32 value), or NULL */
+} ix_gdn_out_gate;
 
 /* One decode token for B independent sequences of one GDN layer, in one launch:
  * causal conv over the mixed q|k|v channels with its rolling state, per-head L2 norm of q
@@ -116,6 +131,17 @@ hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16
                          const float* dt_bias, float* state, float* o, uint16_t* o_bf16, void* workspace,
                          hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* ix_gdn_decode followed by the gated output norm of each (sequence, v head), in the same
+ * launch: gate->z, gate->y, gate->y_bf16 are [B][h_v][d_v]. o and o_bf16 may both be NULL.
+ * gate must be non-NULL with z, ssm_norm and at least one of y, y_bf16 set. With a workspace
+ * the two workgroups of a head pass their outputs through its exchange slots, and the second
+ * to finish writes y for the whole head. */
+hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                               const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
+                               const float* A_log, const float* dt_bias, float* state, float* o,
+                               uint16_t* o_bf16, const ix_gdn_out_gate* gate, void* workspace,
+                               hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* Bytes of device workspace ix_gdn_prefill needs for n_seq sequences and total_T tokens. */
 size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
 
@@ -132,6 +158,19 @@ hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const i
                           const uint16_t* b, const float* A_log, const float* dt_bias, float* state, float* o,
                           uint16_t* o_bf16, void* workspace, size_t workspace_bytes,
                           hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Bytes of device workspace ix_gdn_prefill_gated needs (the prefill's, plus room for the
+ * fp32 outputs the norm reads when the caller passes no o). */
+size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
+
+/* ix_gdn_prefill followed by the gated output norm of every (token, v head) row:
+ * gate->z, gate->y, gate->y_bf16 are [total_T][h_v][d_v]; workspace_bytes must be at least
+ * ix_gdn_prefill_gated_workspace_size(). */
+hipError_t ix_gdn_prefill_gated(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
+                                const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
+                                const uint16_t* a, const uint16_t* b, const float* A_log, const float* dt_bias,
+                                float* state, float* o, uint16_t* o_bf16, const ix_gdn_out_gate* gate,
+                                void* workspace, size_t workspace_bytes, hipStream_t s IX_GDN_DEFAULT_STREAM);
 
 /* Library version string. */
 const char* ix_gdn_version(void);

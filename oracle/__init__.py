@@ -132,6 +132,17 @@ def out_norm(o, z, nrm, h_v, S, eps):
     return r
 
 
+def gated_out(o, z_bits, nrm, eps):
+    """The gated output norm of every (row, head) of o [..][h_v][d_v]: ixo_out_norm
+    (tests/test_gdn.cu:49-50) over the rows, with o taken to fp32 and z from bf16 bits.
+    Returns float64 of o's shape."""
+    o = np.asarray(o)
+    S = o.shape[-1]
+    rows = o.size // S
+    z = bf16.to_f32(np.asarray(z_bits, dtype=np.uint16)).reshape(-1)
+    return out_norm(o.astype(np.float32).reshape(-1), z, nrm, rows, S, eps).reshape(o.shape)
+
+
 def beta_gate(b):
     """tests/test_gdn.cu:54."""
     b = _f32(b)

@@ -64,7 +64,7 @@ class Gen:
 
 
 # Tensor ids (stable; step-dependent tensors add step * 0x100).
-T_X, T_CS, T_W, T_A, T_B, T_ALOG, T_DT, T_STATE, T_LEN = range(1, 10)
+T_X, T_CS, T_W, T_A, T_B, T_ALOG, T_DT, T_STATE, T_LEN, T_Z, T_NRM = range(1, 12)
 
 
 def layer_params(cfg, seed: int) -> dict:
@@ -86,6 +86,16 @@ def token_inputs(cfg, seed: int, rows: int, step: int = 0) -> dict:
         "x": g.normal_bf16(T_X + 0x100 * step, (rows, C)),
         "a": g.normal_bf16(T_A + 0x100 * step, (rows, cfg.h_v)),
         "b": g.normal_bf16(T_B + 0x100 * step, (rows, cfg.h_v)),
+    }
+
+
+def out_gate_inputs(cfg, seed: int, rows: int, step: int = 0) -> dict:
+    """Gated output norm inputs: z [rows][h_v][d_v] ~ N(0,1) bf16 and the norm weight
+    ssm_norm [d_v] = 1 + 0.1 N(0,1) fp32 (the distribution of tests/test_gdn.cu:48)."""
+    g = Gen(seed)
+    return {
+        "z": g.normal_bf16(T_Z + 0x100 * step, (rows, cfg.h_v, cfg.d_v)),
+        "nrm": (1.0 + g.normal(T_NRM, (cfg.d_v,), 0.1)).astype(np.float32),
     }
 
 

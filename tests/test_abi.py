@@ -120,3 +120,46 @@ def test_head_group_limit():
     assert L.ix_gdn_decode(ctypes.byref(bad), 1, p, p, p, p, p, p, p, p, NULL, NULL, NULL, NULL) == INVALID
     assert bx.ix_gdn_prefill_workspace_size(ok, 1, 64) > 0
     assert bx.ix_gdn_prefill_workspace_size(bad, 1, 64) == 0
+
+
+def test_gated_validation_without_launch():
+    L = bx.lib()
+    cfg = bx.make_cfg()
+    p = ctypes.c_void_p(1 << 20)
+    ok = bx.OutGate(1 << 20, 1 << 20, 1e-6, 1 << 20, None)
+
+    def dec(gate, c=cfg):
+        g = ctypes.byref(gate) if gate is not None else None
+        return L.ix_gdn_decode_gated(ctypes.byref(c), 1, p, p, p, p, p, p, p, p, NULL, NULL, g, NULL, NULL)
+
+    assert dec(None) == INVALID                                                  # gate required
+    assert dec(bx.OutGate(None, 1 << 20, 1e-6, 1 << 20, None)) == INVALID      # no z
+    assert dec(bx.OutGate(1 << 20, None, 1e-6, 1 << 20, None)) == INVALID      # no ssm_norm
+    assert dec(bx.OutGate(1 << 20, 1 << 20, 1e-6, None, None)) == INVALID      # no output
+    assert dec(bx.OutGate(1 << 20, (1 << 20) + 2, 1e-6, 1 << 20, None)) == INVALID   # ssm_norm alignment
+    assert dec(bx.OutGate((1 << 20) + 1, 1 << 20, 1e-6, None, 1 << 20)) == INVALID   # z alignment
+    assert dec(ok, bx.make_cfg(d_conv=7)) == INVALID
+
+    need = bx.ix_gdn_prefill_workspace_size(cfg, 2, 100)
+    gneed = bx.ix_gdn_prefill_gated_workspace_size(cfg, 2, 100)
+    assert gneed >= need + 100 * 32 * 128 * 4 and gneed % 256 == 0
+    assert bx.ix_gdn_prefill_gated_workspace_size(cfg, 0, 100) == 0
+
+    def pre(gate, nbytes):
+        g = ctypes.byref(gate) if gate is not None else None
+        return L.ix_gdn_prefill_gated(ctypes.byref(cfg), 2, 100, p, p, p, p, p, p, p, p, p, NULL, NULL, g, p,
+                                      nbytes, NULL)
+
+    assert pre(None, gneed) == INVALID
+    assert pre(ok, gneed - 1) == INVALID                   # needs room for the norm's fp32 input
+    assert pre(bx.OutGate(1 << 20, 1 << 20, 1e-6, None, None), gneed) == INVALID
+
+
+def test_decode_workspace_sections():
+    # group counters [B][h_k], head counters [B][h_v], exchange [B][h_v][2][64] fp32 and
+    # [B][h_v][2] fp32, each section 256-byte aligned
+    cfg = bx.make_cfg()
+    r = lambda n: (n + 255) // 256 * 256
+    for B in (1, 3, 64):
+        assert bx.ix_gdn_decode_workspace_size(cfg, B) == (r(B * 16 * 4) + r(B * 32 * 4) + r(B * 32 * 2 * 64 * 4)
+                                                          + r(B * 32 * 2 * 4))

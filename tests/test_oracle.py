@@ -201,6 +201,35 @@ def test_out_norm_constant_row():
         np.testing.assert_allclose(y[h], c[h] / math.sqrt(c[h] ** 2 + eps) * nrm * 0.5, rtol=2e-7)
 
 
+def test_out_norm_mean_of_squares_and_gate_sign():
+    # Half the row at a, half at b: mean(o^2) = (a^2 + b^2) / 2 (a sum or a wrong divisor fails);
+    # z = +-ln 3 gives sigmoid 3/4 and 1/4 (a sign error in the gate swaps them).
+    S, eps = 8, 0.0
+    a, b = 3.0, 4.0
+    o = np.array([a] * 4 + [b] * 4, np.float32)
+    z = np.array([math.log(3.0), -math.log(3.0)] * 4, np.float32)
+    nrm = np.full(S, 2.0, np.float32)
+    y = oracle.out_norm(o, z, nrm, 1, S, eps)
+    rms = math.sqrt((a * a + b * b) / 2)
+    want = o / rms * 2.0 * np.array([0.75, 0.25] * 4)
+    np.testing.assert_allclose(y, want, rtol=1e-6)
+
+
+def test_gated_out_rows_and_bf16_gate():
+    # gated_out normalises each (row, head) of [rows][h_v][d_v] on its own, with z given as
+    # bf16 bits: constant rows c give sign(c) * nrm * sigmoid(z) (eps = 0).
+    rows, hv, S = 2, 3, 16
+    c = np.array([[1.0, -2.0, 0.5], [4.0, -0.25, 8.0]])
+    o = np.repeat(c[..., None], S, axis=-1)
+    zf = np.array([0.0, 1.0, -1.0], np.float32)
+    z_bits = np.broadcast_to(bf16.from_f32(zf)[None, :, None], (rows, hv, S)).copy()
+    nrm = np.linspace(0.5, 1.5, S).astype(np.float32)
+    y = oracle.gated_out(o, z_bits, nrm, 0.0)
+    sig = 1.0 / (1.0 + np.exp(-zf.astype(np.float64)))
+    want = np.sign(c)[..., None] * nrm[None, None, :] * sig[None, :, None]
+    np.testing.assert_allclose(y, want, rtol=1e-6)
+
+
 # ------------------------------------------------------------------------------------------
 # fused decode and prefill (extensions)
 # ------------------------------------------------------------------------------------------
