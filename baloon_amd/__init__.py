@@ -32,6 +32,7 @@ EXPORTS = (
     "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
     "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
+    "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_commit_window",
     "ix_gdn_version",
 )
 
@@ -98,6 +99,9 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_decode_gated": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_prefill_gated_workspace_size": ([P, I, I], Z),
         "ix_gdn_prefill_gated": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
+        "ix_gdn_window_record_size": ([P, I, I], Z),
+        "ix_gdn_decode_window": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_gdn_commit_window": ([P, I, I, P, P, P, P, P, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
     }
     for name, (args, res) in sig.items():
@@ -210,6 +214,24 @@ def ix_gdn_prefill_gated(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, co
                                       _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias),
                                       _ptr(state), _ptr(o), _ptr(o_bf16), g, _ptr(workspace), workspace_bytes,
                                       _stream(s))
+
+
+def ix_gdn_window_record_size(cfg: Cfg, B: int, K: int) -> int:
+    return lib().ix_gdn_window_record_size(ctypes.byref(cfg), B, K)
+
+
+def ix_gdn_decode_window(cfg: Cfg, B, K, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
+                         record=None, s=None) -> int:
+    """Verify K draft tokens per sequence (x [B][K][C]); the states are read, not written."""
+    return lib().ix_gdn_decode_window(ctypes.byref(cfg), B, K, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a),
+                                      _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16),
+                                      _ptr(record), _stream(s))
+
+
+def ix_gdn_commit_window(cfg: Cfg, B, K, accepted, x, record, conv_state, state, s=None) -> int:
+    """Advance each sequence's states by its accepted prefix of the verified window."""
+    return lib().ix_gdn_commit_window(ctypes.byref(cfg), B, K, _ptr(accepted), _ptr(x), _ptr(record),
+                                      _ptr(conv_state), _ptr(state), _stream(s))
 
 
 def version() -> str:

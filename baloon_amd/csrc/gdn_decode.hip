@@ -73,23 +73,6 @@ inline size_t decode_ws_layout(int B, int h_k, int h_v, size_t (&off)[4]) {
     return at;
 }
 
-// Sum over the 32 lanes of each half wave, result in all of them.
-__device__ __forceinline__ float half_sum(float v) { return pair_sum16(row_sum16(v)); }
-
-// Conv inputs of two adjacent channels (ch even) of one sequence, as dwords: x of both,
-// the (DC-1)-entry bf16 histories of ch then ch+1, and their DC bf16 weights each. Every
-// access is 4-byte aligned because C, ch and the row offsets are even.
-template <int DC>
-struct ConvPair {
-    uint32_t x;
-    uint32_t h[DC - 1];
-    uint32_t w[DC];
-};
-
-__device__ __forceinline__ uint16_t u16_at(const uint32_t* a, int e) {
-    return (uint16_t)(a[e >> 1] >> (16 * (e & 1)));
-}
-
 template <int DC>
 __device__ __forceinline__ void conv_pair_load(const DecodeParams& p, int bseq, int ch, ConvPair<DC>& c) {
     const size_t row = (size_t)bseq * p.L.C + ch;
@@ -100,30 +83,6 @@ __device__ __forceinline__ void conv_pair_load(const DecodeParams& p, int bseq, 
     const uint32_t* wp = reinterpret_cast<const uint32_t*>(p.L.conv_w + (size_t)ch * DC);
 #pragma unroll
     for (int i = 0; i < DC; ++i) c.w[i] = wp[i];
-}
-
-// Conv outputs of the pair (the accumulation order of conv_eval) and the shifted histories
-// (each channel's history minus its oldest entry, then x), packed as dwords.
-template <int DC>
-__device__ __forceinline__ void conv_pair_eval(const Layer& L, const ConvPair<DC>& c, float& y0, float& y1,
-                                               uint32_t (&nh)[DC - 1]) {
-    const uint16_t xs[2] = {(uint16_t)(c.x & 0xffff), (uint16_t)(c.x >> 16)};
-    uint16_t n16[2 * (DC - 1)];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < DC - 1; ++i)
-            acc = fmaf(bf16_to_f32(u16_at(c.h, q * (DC - 1) + i)), bf16_to_f32(u16_at(c.w, q * DC + i)), acc);
-        acc = fmaf(bf16_to_f32(xs[q]), bf16_to_f32(u16_at(c.w, q * DC + DC - 1)), acc);
-        if (L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
-        (q == 0 ? y0 : y1) = acc;
-#pragma unroll
-        for (int i = 0; i < DC - 2; ++i) n16[q * (DC - 1) + i] = u16_at(c.h, q * (DC - 1) + i + 1);
-        n16[q * (DC - 1) + DC - 2] = xs[q];
-    }
-#pragma unroll
-    for (int i = 0; i < DC - 1; ++i) nh[i] = (uint32_t)n16[2 * i] | ((uint32_t)n16[2 * i + 1] << 16);
 }
 
 template <int DC>

@@ -128,6 +128,64 @@ def decode_bench(args, gated=False):
     )
 
 
+def window_bench(args, K=4, iters=64):
+    """Speculative window at B = 64: ix_gdn_decode_window over K draft tokens, then
+    ix_gdn_commit_window with all K accepted (the most state work), layers rotated as in the
+    decode leg. Reports microseconds per call and the state GB/s of each (verify reads the
+    state once, commit reads and writes it once)."""
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    B, L = args.batch, args.layers
+    C, hv = cfg.channels, cfg.h_v
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6D4E0005)
+    layers = [dict(w=(torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16),
+                   A_log=torch.rand(hv, generator=g, device=dev) * 2.77,
+                   dt=torch.randn(hv, generator=g, device=dev) * 0.1,
+                   state=torch.randn(B, hv, 128, 128, generator=g, device=dev) * 0.02,
+                   cs=torch.randn(B, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16))
+              for _ in range(L)]
+    x = torch.randn(B, K, C, generator=g, device=dev).to(torch.bfloat16)
+    a = torch.randn(B, K, hv, generator=g, device=dev).to(torch.bfloat16)
+    b = torch.randn(B, K, hv, generator=g, device=dev).to(torch.bfloat16)
+    o = torch.empty(B, K, hv, 128, dtype=torch.bfloat16, device=dev)
+    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device=dev)
+    acc = torch.full((B,), K, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def verify(i):
+        Ly = layers[i % L]
+        return bx.ix_gdn_decode_window(cfg, B, K, x, Ly["cs"], Ly["w"], a, b, Ly["A_log"], Ly["dt"], Ly["state"],
+                                       None, o, rec, stream)
+
+    def commit(i):
+        Ly = layers[i % L]
+        return bx.ix_gdn_commit_window(cfg, B, K, acc, x, rec, Ly["cs"], Ly["state"], stream)
+
+    out = {}
+    for name, fn in (("verify", verify), ("commit", commit)):
+        for i in range(8):
+            bx.check(name, fn(i))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rcs = [fn(i) for i in range(iters)]
+        e1.record(stream)
+        torch.cuda.synchronize()
+        for rc in rcs:
+            bx.check(name, rc)
+        out[name] = e0.elapsed_time(e1) * 1e3 / iters
+    sb = B * hv * STATE_TILE
+    return dict(K=K, B=B, verify_us=round(out["verify"], 2), commit_us=round(out["commit"], 2),
+                verify_state_gbs=round(sb / out["verify"] / 1e3, 1),
+                commit_state_gbs=round(2 * sb / out["commit"] / 1e3, 1),
+                us_per_token_window=round((out["verify"] + out["commit"]) / K, 2))
+
+
 def decode_latency(iters=200):
     """Configuration 1: one decode token at B = 1 (2 MiB state), microseconds per call."""
     import torch
@@ -306,6 +364,7 @@ def main():
     torch.cuda.synchronize()
     d = decode_bench(args)
     dg = decode_bench(args, gated=True)
+    win = window_bench(args)
     lat = decode_latency()
     pf = prefill_bench()
     ceiling = hbm_ceiling()
@@ -332,6 +391,7 @@ def main():
         "decode_b1_us_per_token": lat,
         "decode_gated": {"avg_kernel_us": round(dg["avg_kernel_us"], 2), "state_gbs": dg["roofline"]["achieved"],
                          "note": "same step with the gated RMS output norm fused in (bf16 y instead of bf16 o)"},
+        "spec_window": win,
         "prefill": pf,
         "roofline": d["roofline"],
         "cpu_baseline": cpu,

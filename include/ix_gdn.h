@@ -172,6 +172,42 @@ hipError_t ix_gdn_prefill_gated(const ix_gdn_cfg* cfg, int n_seq, int total_T, c
                                 float* state, float* o, uint16_t* o_bf16, const ix_gdn_out_gate* gate,
                                 void* workspace, size_t workspace_bytes, hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* ---------------------------------------------------------------------------------------
+ * Speculative windows (additions; no reference counterpart)
+ *
+ * A window is K draft tokens per sequence (1 <= K <= 16). ix_gdn_decode_window runs them
+ * from the committed states and writes their outputs plus a window record, without
+ * changing either state; ix_gdn_commit_window then advances the committed states by each
+ * sequence's accepted prefix. Outputs are bit-identical to K ix_gdn_decode calls, and the
+ * committed states to n calls for n accepted tokens.
+ *
+ * Window record (fp32, row = b*K + t; sections in this order, each 256-byte aligned):
+ *   k_hat [B*K][h_k][d_k]  normalised key of each q/k head
+ *   v     [B*K][h_v][d_v]  conv output of each v head's channels
+ *   g     [B*K][h_v]       decay exp(-exp(A_log) * softplus(a + dt_bias))
+ *   beta  [B*K][h_v]       sigmoid(b)
+ * Both calls require every q/k head to feed at least one v head (IX_GDN_HEAD_DIV, or
+ * h_v >= h_k with IX_GDN_HEAD_MOD).
+ * --------------------------------------------------------------------------------------- */
+
+/* Bytes of the window record for B sequences and K tokens, or 0 for an invalid request. */
+size_t ix_gdn_window_record_size(const ix_gdn_cfg* cfg, int B, int K);
+
+/* Verify a window: x [B][K][C] bf16, a, b [B][K][h_v] bf16; conv_state and state as in
+ * ix_gdn_decode (read only here); o, o_bf16 [B][K][h_v][d_v] (either may be NULL); record:
+ * ix_gdn_window_record_size() bytes, 256-byte aligned, written. */
+hipError_t ix_gdn_decode_window(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x,
+                                const uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                                const uint16_t* b, const float* A_log, const float* dt_bias, const float* state,
+                                float* o, uint16_t* o_bf16, void* record, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Commit a window: accepted [B] int32 device array, each clamped to [0, K]; x and record as
+ * given to ix_gdn_decode_window. Sequence b's conv_state and state advance by accepted[b]
+ * tokens; a sequence with accepted[b] = 0 is not touched. */
+hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, const int32_t* accepted, const uint16_t* x,
+                                const void* record, uint16_t* conv_state, float* state,
+                                hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* Library version string. */
 const char* ix_gdn_version(void);
 

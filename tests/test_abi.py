@@ -163,3 +163,29 @@ def test_decode_workspace_sections():
     for B in (1, 3, 64):
         assert bx.ix_gdn_decode_workspace_size(cfg, B) == (r(B * 16 * 4) + r(B * 32 * 4) + r(B * 32 * 2 * 64 * 4)
                                                           + r(B * 32 * 2 * 4))
+
+
+def test_window_validation_without_launch():
+    L = bx.lib()
+    cfg = bx.make_cfg()
+    p = ctypes.c_void_p(1 << 20)
+    r = bx.ix_gdn_window_record_size(cfg, 2, 4)
+    rows = 8
+    rr = lambda n: (n + 255) // 256 * 256
+    assert r == rr(rows * 16 * 128 * 4) + rr(rows * 32 * 128 * 4) + 2 * rr(rows * 32 * 4)
+    for B, K in [(0, 4), (2, 0), (2, 17), (-1, 1)]:
+        assert bx.ix_gdn_window_record_size(cfg, B, K) == 0
+
+    def verify(K, c=cfg, rec=p, state=p):
+        return L.ix_gdn_decode_window(ctypes.byref(c), 2, K, p, p, p, p, p, p, p, state, NULL, NULL, rec, NULL)
+
+    def commit(K, c=cfg, acc=p, rec=p):
+        return L.ix_gdn_commit_window(ctypes.byref(c), 2, K, acc, p, rec, p, p, NULL)
+
+    for f in (verify, commit):
+        assert f(0) == INVALID and f(17) == INVALID
+        assert f(4, c=bx.make_cfg(h_k=4, h_v=2)) == INVALID            # a q/k head feeds no v head
+        assert f(4, rec=ctypes.c_void_p((1 << 20) + 16)) == INVALID     # record not 256-byte aligned
+        assert f(4, rec=NULL) == INVALID
+    assert verify(4, state=ctypes.c_void_p((1 << 20) + 8)) == INVALID  # state not 16-byte aligned
+    assert commit(4, acc=NULL) == INVALID

@@ -1,0 +1,132 @@
+"""GPU parity of the speculative-window calls (ix_gdn_decode_window, ix_gdn_commit_window).
+
+The window's outputs must be bit-identical to K ix_gdn_decode calls on the same states (the
+kernels share the column math), the verify call must leave both states untouched, and commit
+with n accepted tokens must leave the states bit-identical to n decode calls; against the
+double oracle the decode tolerances hold (fp32 outputs 1e-3 absolute, state max|d|/max|ref|
+<= 1e-4, conv state bit-exact). Accepted counts are clamped to [0, K].
+"""
+import numpy as np
+import pytest
+
+import baloon_amd as bx
+import oracle
+from oracle import inputs
+from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def window_case(cfg, B, K, accepted, seed):
+    torch = _torch()
+    p = inputs.layer_params(cfg, seed)
+    st = inputs.initial_states(cfg, seed, B)
+    tok = inputs.token_inputs(cfg, seed, B * K)                      # row b*K + t
+    x = tok["x"].reshape(B, K, -1)
+    a = tok["a"].reshape(B, K, -1)
+    b = tok["b"].reshape(B, K, -1)
+    d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
+    d_x, d_a, d_b = dev(x), dev(a), dev(b)
+
+    # verify
+    d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
+    cs0, st0 = host(d_cs).copy(), host(d_st).copy()
+    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
+    o_win = torch.full((B, K, cfg.h_v, cfg.d_v), float("nan"), dtype=torch.float32, device="cuda")
+    assert bx.ix_gdn_decode_window(cfg, B, K, d_x, d_cs, d_w, d_a, d_b, d_A, d_dt, d_st, o_win, None, rec) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(d_st), st0)                    # verify changes no state
+    np.testing.assert_array_equal(host(d_cs), cs0)
+    o_win = host(o_win)
+
+    # the same tokens through K decode calls, keeping the states after each
+    l_cs, l_st = dev(st["conv_state"]), state_to_dev(st["state"])
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device="cuda")
+    od = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    after = [(cs0, st0)]
+    for t in range(K):
+        assert bx.ix_gdn_decode(cfg, B, dev(x[:, t]), l_cs, d_w, dev(a[:, t]), dev(b[:, t]), d_A, d_dt, l_st, od,
+                                None, ws) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(o_win[:, t], host(od), err_msg=f"window output t={t}")
+        after.append((host(l_cs).copy(), host(l_st).copy()))
+
+    # commit
+    acc = np.asarray(accepted, np.int32)
+    assert bx.ix_gdn_commit_window(cfg, B, K, dev(acc), d_x, rec, d_cs, d_st) == 0
+    torch.cuda.synchronize()
+    cs1, st1 = host(d_cs), host(d_st)
+    for bi in range(B):
+        n = int(min(max(acc[bi], 0), K))
+        np.testing.assert_array_equal(cs1[bi], after[n][0][bi], err_msg=f"conv state b={bi} n={n}")
+        np.testing.assert_array_equal(st1[bi], after[n][1][bi], err_msg=f"state b={bi} n={n}")
+
+    # against the double oracle: outputs of the whole window, states after each prefix
+    rcs, rst = st["conv_state"], st["state"].astype(np.float64)
+    ref = [(rcs, rst)]
+    for t in range(K):
+        rcs, rst, ro = oracle.decode(cfg, B, x[:, t], rcs, p["w"], a[:, t], b[:, t], p["A_log"], p["dt_bias"], rst,
+                                     nthreads=8)
+        assert float(np.max(np.abs(o_win[:, t] - ro))) <= TOL_O_ABS
+        ref.append((rcs, rst))
+    for bi in range(B):
+        n = int(min(max(acc[bi], 0), K))
+        np.testing.assert_array_equal(cs1[bi], ref[n][0][bi])
+        got = np.swapaxes(st1[bi], -1, -2)
+        assert oracle.rel_err(got, ref[n][1][bi]) <= TOL_STATE_REL
+
+
+@pytest.mark.parametrize("K,accepted", [
+    (4, [0, 1, 2, 3, 4, 4]),
+    (1, [1, 0, -2, 7, 1, 1]),
+    (8, [8, 5, 0, 13, 3, -1]),
+])
+def test_window_verify_and_commit(K, accepted):
+    window_case(bx.make_cfg(), 6, K, accepted, inputs.seed_for(2) + 50 + K)
+
+
+@pytest.mark.parametrize("kw", [dict(head_map=1, h_k=4, h_v=12), dict(d_conv=2), dict(d_conv=3, conv_act=1),
+                                dict(h_k=3, h_v=8, q_scale=0.125)])
+def test_window_variants(kw):
+    window_case(bx.make_cfg(**kw), 3, 3, [3, 1, 2], inputs.seed_for(2) + 60 + len(kw))
+
+
+def test_window_then_decode_continues():
+    # After a commit the states continue under ix_gdn_decode like any others.
+    torch = _torch()
+    cfg = bx.make_cfg()
+    B, K, seed = 4, 3, inputs.seed_for(2) + 71
+    p = inputs.layer_params(cfg, seed)
+    st = inputs.initial_states(cfg, seed, B)
+    tok = inputs.token_inputs(cfg, seed, B * K)
+    x, a, b = (tok[n].reshape(B, K, -1) for n in ("x", "a", "b"))
+    d_w, d_A, d_dt = dev(p["w"]), dev(p["A_log"]), dev(p["dt_bias"])
+    d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
+    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
+    assert bx.ix_gdn_decode_window(cfg, B, K, dev(x), d_cs, d_w, dev(a), dev(b), d_A, d_dt, d_st, None, None,
+                                   rec) == 0
+    acc = np.array([2, 0, 3, 1], np.int32)
+    assert bx.ix_gdn_commit_window(cfg, B, K, dev(acc), dev(x), rec, d_cs, d_st) == 0
+    rcs, rst = st["conv_state"].copy(), st["state"].astype(np.float64)
+    for bi in range(B):
+        for t in range(int(acc[bi])):
+            c1, s1, _ = oracle.decode(cfg, 1, x[bi:bi + 1, t], rcs[bi:bi + 1], p["w"], a[bi:bi + 1, t],
+                                      b[bi:bi + 1, t], p["A_log"], p["dt_bias"], rst[bi:bi + 1])
+            rcs[bi], rst[bi] = c1[0], s1[0]
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device="cuda")
+    od = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    for k in range(4):
+        t = inputs.token_inputs(cfg, seed, B, step=100 + k)
+        assert bx.ix_gdn_decode(cfg, B, dev(t["x"]), d_cs, d_w, dev(t["a"]), dev(t["b"]), d_A, d_dt, d_st, od, None,
+                                ws) == 0
+        rcs, rst, ro = oracle.decode(cfg, B, t["x"], rcs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], rst,
+                                     nthreads=8)
+        torch.cuda.synchronize()
+        assert float(np.max(np.abs(host(od) - ro))) <= TOL_O_ABS
+    np.testing.assert_array_equal(host(d_cs), rcs)
+    assert oracle.rel_err(state_from_dev(d_st), rst) <= TOL_STATE_REL
