@@ -33,6 +33,7 @@ EXPORTS = (
     "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
     "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_commit_window",
+    "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
     "ix_gdn_version",
 )
 
@@ -84,7 +85,7 @@ def lib() -> ctypes.CDLL:
     if not os.path.exists(LIB_PATH):
         raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m baloon_amd.build`")
     L = ctypes.CDLL(LIB_PATH)
-    P, I, F, Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+    P, I, F, Z, LL = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t, ctypes.c_longlong
     sig = {
         "ix_gdn_step": ([P, P, P, P, P, P, P, I, I, I, P], I),
         "ix_gdn_conv_step": ([P, P, P, P, I, I, P], I),
@@ -102,6 +103,12 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_window_record_size": ([P, I, I], Z),
         "ix_gdn_decode_window": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_commit_window": ([P, I, I, P, P, P, P, P, P], I),
+        "ix_bf16_gemv": ([P, P, P, LL, LL, P], I),
+        "ix_bf16_gemv_pair": ([P, P, P, LL, P, P, LL, LL, P], I),
+        "ix_bf16_gemv_split": ([P, P, P, LL, LL, I, P], I),
+        "ix_mmvq_q8_0": ([P, P, P, I, I, I, P], I),
+        "ix_gdn_in_proj_width": ([P], I),
+        "ix_gdn_in_proj": ([P, I, I, P, P, P, P, P, P, P, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
     }
     for name, (args, res) in sig.items():
@@ -232,6 +239,34 @@ def ix_gdn_commit_window(cfg: Cfg, B, K, accepted, x, record, conv_state, state,
     """Advance each sequence's states by its accepted prefix of the verified window."""
     return lib().ix_gdn_commit_window(ctypes.byref(cfg), B, K, _ptr(accepted), _ptr(x), _ptr(record),
                                       _ptr(conv_state), _ptr(state), _stream(s))
+
+
+# ---- projections ----------------------------------------------------------------------------
+
+def ix_bf16_gemv(x, w, y, n_in, n_out, s=None) -> int:
+    return lib().ix_bf16_gemv(_ptr(x), _ptr(w), _ptr(y), n_in, n_out, _stream(s))
+
+
+def ix_bf16_gemv_pair(x, w1, y1, n_out1, w2, y2, n_out2, n_in, s=None) -> int:
+    return lib().ix_bf16_gemv_pair(_ptr(x), _ptr(w1), _ptr(y1), n_out1, _ptr(w2), _ptr(y2), n_out2, n_in, _stream(s))
+
+
+def ix_bf16_gemv_split(x, w, y, n_in, n_out, threads_per_row, s=None) -> int:
+    return lib().ix_bf16_gemv_split(_ptr(x), _ptr(w), _ptr(y), n_in, n_out, threads_per_row, _stream(s))
+
+
+def ix_mmvq_q8_0(weights, x_q8_1, y, n_in, n_out, ncols, s=None) -> int:
+    return lib().ix_mmvq_q8_0(_ptr(weights), _ptr(x_q8_1), _ptr(y), n_in, n_out, ncols, _stream(s))
+
+
+def ix_gdn_in_proj_width(cfg: Cfg) -> int:
+    return lib().ix_gdn_in_proj_width(ctypes.byref(cfg))
+
+
+def ix_gdn_in_proj(cfg: Cfg, B, hidden, h, w, x, z, a, b, y=None, s=None) -> int:
+    """[x | z | a | b] = h W^T for B rows: h [B][hidden], W [N][hidden] bf16 -> bf16 pieces."""
+    return lib().ix_gdn_in_proj(ctypes.byref(cfg), B, hidden, _ptr(h), _ptr(w), _ptr(x), _ptr(z), _ptr(a), _ptr(b),
+                                _ptr(y), _stream(s))
 
 
 def version() -> str:

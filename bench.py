@@ -186,6 +186,44 @@ def window_bench(args, K=4, iters=64):
                 us_per_token_window=round((out["verify"] + out["commit"]) / K, 2))
 
 
+def in_proj_bench(args, hidden=2048, iters=100):
+    """The layer's input projection at the decode batch: y = h W^T for B = 64 rows, hidden
+    2048 (Qwen3-Next), N = 12352 outputs (x | z | a | b). Weight-streaming bound: reports
+    microseconds per call, the weight bytes' GB/s and TFLOP/s."""
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    B = args.batch
+    N = bx.ix_gdn_in_proj_width(cfg)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x6D4E0006)
+    nw = 4                                                    # rotated weight copies (MALL defeated)
+    ws = [(torch.randn(N, hidden, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(nw)]
+    h = torch.randn(B, hidden, generator=g, device=dev).to(torch.bfloat16)
+    x = torch.empty(B, cfg.channels, dtype=torch.bfloat16, device=dev)
+    z = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device=dev)
+    a = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device=dev)
+    b = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream()
+    for i in range(8):
+        bx.check("ix_gdn_in_proj", bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[i % nw], x, z, a, b, None, stream))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    rcs = [bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[i % nw], x, z, a, b, None, stream) for i in range(iters)]
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for rc in rcs:
+        bx.check("ix_gdn_in_proj", rc)
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    wbytes = N * hidden * 2
+    return dict(B=B, hidden=hidden, N=N, us=round(us, 2), weight_gbs=round(wbytes / us / 1e3, 1),
+                tflops=round(2.0 * B * hidden * N / us / 1e6, 2))
+
+
 def decode_latency(iters=200):
     """Configuration 1: one decode token at B = 1 (2 MiB state), microseconds per call."""
     import torch
@@ -365,6 +403,7 @@ def main():
     d = decode_bench(args)
     dg = decode_bench(args, gated=True)
     win = window_bench(args)
+    ip = in_proj_bench(args)
     lat = decode_latency()
     pf = prefill_bench()
     ceiling = hbm_ceiling()
@@ -392,6 +431,7 @@ def main():
         "decode_gated": {"avg_kernel_us": round(dg["avg_kernel_us"], 2), "state_gbs": dg["roofline"]["achieved"],
                          "note": "same step with the gated RMS output norm fused in (bf16 y instead of bf16 o)"},
         "spec_window": win,
+        "in_proj": ip,
         "prefill": pf,
         "roofline": d["roofline"],
         "cpu_baseline": cpu,

@@ -208,6 +208,53 @@ hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, const int32
                                 const void* record, uint16_t* conv_state, float* state,
                                 hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* ---------------------------------------------------------------------------------------
+ * Projections feeding the layer
+ * --------------------------------------------------------------------------------------- */
+
+/* bf16 GEMV y[o] = sum_i x[i] * w[o][i], fp32 accumulation and result; w [n_out][n_in] bf16,
+ * x [n_in] bf16. Replaces ix_bf16_gemv, src/ix_bf16_gemv.cu:90-101. Requires n_in > 0,
+ * n_out > 0. Summation order is this library's own (within float tolerance of a double
+ * reference); rows are 16-byte loads when n_in % 8 == 0 and x, w are 16-byte aligned. */
+hipError_t ix_bf16_gemv(const uint16_t* x, const uint16_t* w, float* y, long long n_in, long long n_out,
+                        hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Two GEMVs sharing x: y1 = w1 x (n_out1 rows), y2 = w2 x (n_out2 rows). Replaces
+ * ix_bf16_gemv_pair, src/ix_bf16_gemv.cu:103-111. Each result is bit-identical to
+ * ix_bf16_gemv on the same operands. Requires n_in > 0 and n_out1 > 0 or n_out2 > 0. */
+hipError_t ix_bf16_gemv_pair(const uint16_t* x, const uint16_t* w1, float* y1, long long n_out1, const uint16_t* w2,
+                             float* y2, long long n_out2, long long n_in, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* GEMV with threads_per_row threads cooperating on each row. Replaces ix_bf16_gemv_split,
+ * src/ix_bf16_gemv.cu:113-126: 64 is one wave per row (bit-identical to ix_bf16_gemv);
+ * otherwise a power of two up to 1024, else hipErrorInvalidValue. */
+hipError_t ix_bf16_gemv_split(const uint16_t* x, const uint16_t* w, float* y, long long n_in, long long n_out,
+                              int threads_per_row, hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Q8_0 weights times q8_1 activations for ncols (1..8) activation columns. Replaces
+ * ix_mmvq::ix_mmvq_q8_0, src/ix_mmvq_wave.cu:120-123 (formats :22-25):
+ *   weights [n_out][n_in/32] Q8_0 blocks (fp16 scale, 32 int8; 34 bytes, 2-byte aligned)
+ *   x_q8_1  [ncols][n_in/32] q8_1 blocks (fp16 scale, fp16 sum, 32 int8; 36 bytes, 4-byte aligned)
+ *   y       [ncols][n_out] fp32 = sum over blocks of d_w * d_x * (integer dot of the block)
+ * Requires n_in > 0, n_in % 32 == 0, n_out > 0, 1 <= ncols <= 8, non-NULL pointers. A
+ * column's result does not depend on ncols. */
+hipError_t ix_mmvq_q8_0(const void* weights, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
+                        hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* Output width N of the layer's input projection: C + h_v*d_v + 2*h_v (x | z | a | b), or 0
+ * for an invalid description. */
+int ix_gdn_in_proj_width(const ix_gdn_cfg* cfg);
+
+/* Input projection of B token rows (addition; no reference counterpart -- the reference runs
+ * per-token GEMVs): y = h W^T with h [B][hidden] bf16, W [N][hidden] bf16 (N as above), fp32
+ * accumulation on bf16 MFMA, written as bf16 (RNE) pieces x [B][C], z [B][h_v][d_v],
+ * a [B][h_v], b [B][h_v] -- the inputs of ix_gdn_decode(_gated) and ix_gdn_prefill(_gated) --
+ * and, when y is not NULL, as fp32 y [B][N]. Requires hidden % 128 == 0, h and W 16-byte
+ * aligned. */
+hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, const uint16_t* h, const uint16_t* w,
+                          uint16_t* x, uint16_t* z, uint16_t* a, uint16_t* b, float* y,
+                          hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* Library version string. */
 const char* ix_gdn_version(void);
 

@@ -1,0 +1,89 @@
+"""CPU references for the projections feeding the GDN layer (test infrastructure only).
+
+Restates the reference's double-precision host checks:
+  * bf16 GEMV: tests/test_bf16_gemv.cu:21-22 -- y[o] = sum_i x[i] w[o][i] in double, with the
+    per-row magnitude sum_i |x[i] w[o][i]| that scales the tolerance (:11, 2e-5 x magnitude);
+  * Q8_0 x q8_1: tests/mmvq_wave_ref.h:37-47 -- y[c][r] = sum over blocks of
+    d_w * d_x * (integer dot of the block's 32 int8 pairs) in double, with the scale
+    sum |d_w d_x| * 32 * 127 * 127 of tests/test_mmvq_wave.cu:57-58 (tolerance 1e-5 x scale);
+  * the block formats of src/ix_mmvq_wave.cu:22-25: Q8_0 = fp16 d + 32 int8 (34 bytes),
+    q8_1 = fp16 d, fp16 s + 32 int8 (36 bytes), little endian, packed back to back.
+The layer's input projection is the same GEMV for B rows, split into the pieces
+x | z | a | b (include/ix_gdn.h).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import bf16
+from .inputs import Gen
+
+
+def gemv_ref(x_bits, w_bits):
+    """x [n_in] and w [n_out][n_in] as bf16 bits -> (y, magnitude), float64 [n_out]."""
+    x = bf16.to_f32(np.asarray(x_bits, np.uint16)).astype(np.float64)
+    w = bf16.to_f32(np.asarray(w_bits, np.uint16)).astype(np.float64)
+    return w @ x, np.abs(w) @ np.abs(x)
+
+
+def in_proj_ref(h_bits, w_bits):
+    """h [B][K], W [N][K] bf16 bits -> (y, magnitude), float64 [B][N]."""
+    h = bf16.to_f32(np.asarray(h_bits, np.uint16)).astype(np.float64)
+    w = bf16.to_f32(np.asarray(w_bits, np.uint16)).astype(np.float64)
+    return h @ w.T, np.abs(h) @ np.abs(w).T
+
+
+def in_proj_split(cfg, y):
+    """Split [B][N] columns into the layer's pieces x [B][C], z [B][h_v][d_v], a, b [B][h_v]."""
+    C = 2 * cfg.h_k * cfg.d_k + cfg.h_v * cfg.d_v
+    Z = cfg.h_v * cfg.d_v
+    B = y.shape[0]
+    return (y[:, :C], y[:, C:C + Z].reshape(B, cfg.h_v, cfg.d_v), y[:, C + Z:C + Z + cfg.h_v],
+            y[:, C + Z + cfg.h_v:C + Z + 2 * cfg.h_v])
+
+
+# ---- Q8_0 / q8_1 ---------------------------------------------------------------------------
+
+def half_exact(v):
+    """float values that are exactly representable in fp16 -> fp16 bits."""
+    return np.asarray(v, np.float16).view(np.uint16)
+
+
+def q8_blocks(seed, tid, rows, nb):
+    """Random blocks like tests/test_mmvq_wave.cu:30-31: scales (1 + u % 2047) / 1024 (exact in
+    fp16), quants uniform in [-127, 127]. Returns (d bits uint16 [rows][nb], qs int8 [rows][nb][32])."""
+    g = Gen(seed)
+    u = (g._bits(tid, rows * nb) % np.uint64(2047)).astype(np.float64)
+    d = half_exact(((1.0 + u) / 1024.0).astype(np.float32)).reshape(rows, nb)
+    q = ((g._bits(tid + 1, rows * nb * 32) % np.uint64(255)).astype(np.int64) - 127).astype(np.int8)
+    return d, q.reshape(rows, nb, 32)
+
+
+def pack_q8_0(d, qs) -> np.ndarray:
+    """[rows][nb] blocks -> bytes: per block fp16 d then 32 int8 (34 bytes)."""
+    rows, nb = d.shape
+    out = np.zeros((rows, nb, 34), np.uint8)
+    out[..., 0:2] = d.astype("<u2")[..., None].view(np.uint8)
+    out[..., 2:34] = qs.view(np.uint8)
+    return out.reshape(-1)
+
+
+def pack_q8_1(d, qs, s=None) -> np.ndarray:
+    """[cols][nb] blocks -> bytes: per block fp16 d, fp16 s, then 32 int8 (36 bytes)."""
+    cols, nb = d.shape
+    s = np.zeros_like(d) if s is None else s
+    out = np.zeros((cols, nb, 36), np.uint8)
+    out[..., 0:2] = d.astype("<u2")[..., None].view(np.uint8)
+    out[..., 2:4] = s.astype("<u2")[..., None].view(np.uint8)
+    out[..., 4:36] = qs.view(np.uint8)
+    return out.reshape(-1)
+
+
+def q8_0_ref(wd, wq, xd, xq):
+    """y [ncols][n_out] and scale [ncols][n_out] in float64."""
+    dw = wd.view(np.float16).astype(np.float64)                   # [n_out][nb]
+    dx = xd.view(np.float16).astype(np.float64)                   # [nc][nb]
+    dots = np.einsum("rbk,cbk->crb", wq.astype(np.int64), xq.astype(np.int64))   # exact integers
+    y = np.einsum("crb,rb,cb->cr", dots.astype(np.float64), dw, dx)
+    sc = np.einsum("rb,cb->cr", np.abs(dw), np.abs(dx)) * 32 * 127 * 127
+    return y, sc

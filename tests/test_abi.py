@@ -17,7 +17,7 @@ INVALID = bx.HIP_ERROR_INVALID_VALUE
 def declared_functions():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(ix_gdn_[a-z0-9_]+)\s*\(",
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(ix_[a-z0-9_]+)\s*\(",
                                  text, flags=re.M)))
 
 
@@ -189,3 +189,26 @@ def test_window_validation_without_launch():
         assert f(4, rec=NULL) == INVALID
     assert verify(4, state=ctypes.c_void_p((1 << 20) + 8)) == INVALID  # state not 16-byte aligned
     assert commit(4, acc=NULL) == INVALID
+
+
+def test_projection_validation_without_launch():
+    L = bx.lib()
+    p = ctypes.c_void_p(1 << 20)
+    for nin, nout in [(0, 4), (4, 0), (-1, 4)]:
+        assert L.ix_bf16_gemv(p, p, p, nin, nout, NULL) == INVALID
+    assert L.ix_bf16_gemv_pair(p, p, p, 0, p, p, 0, 8, NULL) == INVALID
+    assert L.ix_bf16_gemv_pair(p, p, p, 4, p, p, 4, 0, NULL) == INVALID
+    for tpr in (0, -64, 48, 2048):
+        assert L.ix_bf16_gemv_split(p, p, p, 8, 4, tpr, NULL) == INVALID
+    for n_in, n_out, nc in [(0, 1, 1), (33, 1, 1), (32, 0, 1), (32, 1, 0), (32, 1, 9)]:
+        assert L.ix_mmvq_q8_0(p, p, p, n_in, n_out, nc, NULL) == INVALID
+    assert L.ix_mmvq_q8_0(NULL, p, p, 32, 1, 1, NULL) == INVALID
+    assert L.ix_mmvq_q8_0(ctypes.c_void_p((1 << 20) + 1), p, p, 32, 1, 1, NULL) == INVALID     # Q8_0 is 2-byte aligned
+    cfg = bx.make_cfg()
+    assert bx.ix_gdn_in_proj_width(cfg) == 8192 + 4096 + 64
+    assert bx.ix_gdn_in_proj_width(bx.make_cfg(d_k=64)) == 0
+    ok = (p, p, p, p, p, p, NULL, NULL)
+    for B, K in [(0, 2048), (4, 0), (4, 100), (4, 2050)]:
+        assert L.ix_gdn_in_proj(ctypes.byref(cfg), B, K, *ok) == INVALID
+    assert L.ix_gdn_in_proj(ctypes.byref(cfg), 4, 2048, ctypes.c_void_p((1 << 20) + 8), p, p, p, p, p, NULL,
+                            NULL) == INVALID                                    # h must be 16-byte aligned
