@@ -9,21 +9,24 @@
 // of the recurrence that the reference runs as per-token bf16 GEMVs.
 //
 // At decode batch sizes the product is a skinny GEMM that streams W once from HBM (about 2
-// FLOP per weight byte at B = 64, so HBM-bound). One workgroup owns 32 output columns and
-// 64 rows; its 4 waves split K in quarters, each running v_mfma_f32_16x16x32_bf16 on
-// operands loaded straight from memory in the instruction's lane layout (lane l holds row
-// or column l % 16 and k = 8 (l / 16) .. +7: one 16-byte load per operand tile), weights with
-// nontemporal loads. The four partial tiles are added in wave order through LDS, so the
-// result does not depend on timing.
+// FLOP per weight byte at B = 64), so the work is moving bytes, not MFMA throughput. One
+// workgroup owns 64 output columns and 64 rows; its 8 waves split K into contiguous ranges,
+// and each wave runs v_mfma_f32_16x16x32_bf16 on all 4 x 4 tiles of the 64 x 64 output with
+// operands loaded straight from memory. The k-slots of the instruction are filled so that a
+// lane's two consecutive k-steps are adjacent in memory: for a 64-k super-step, lanes
+// 16 g .. 16 g + 15 hold k = 16 g .. 16 g + 15 of their row (8 for each of two MFMAs), so four
+// lanes read one full 128-byte line of each row per super-step. A and B use the same slot
+// assignment, so the products are unchanged. The 8 partial tiles are added in wave order
+// through LDS, so the result does not depend on timing.
 #include "gdn_common.h"
 
 namespace ixg {
 namespace {
 
-constexpr int kNt = 32;                 // output columns per workgroup
-constexpr int kMt = 64;                 // rows per workgroup
-constexpr int kWaves = 4;               // K quarters
-constexpr int kKStep = 32;              // k per MFMA
+constexpr int kNt = 64;                 // output columns per workgroup (4 MFMA n-tiles)
+constexpr int kMt = 64;                 // rows per workgroup (4 MFMA m-tiles)
+constexpr int kWaves = 8;               // contiguous K ranges
+constexpr int kSuper = 64;              // k per super-step (two MFMA k-steps)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -54,59 +57,61 @@ __global__ void __launch_bounds__(kWaves * kWave) in_proj_kernel(const InProj p)
     const int tid = threadIdx.x, wv = tid / kWave, lane = tid & (kWave - 1);
     const int r16 = lane & 15, kg = lane >> 4;
     const int n0 = blockIdx.x * kNt, m0 = blockIdx.y * kMt;
-    const int kq = p.K / kWaves, k0 = wv * kq;
+    const int nsup = p.K / kSuper;                                   // super-steps in K
+    const int s_lo = wv * nsup / kWaves, s_hi = (wv + 1) * nsup / kWaves;
 
     // Operand rows of this lane (clamped into range: rows and columns past the end compute
     // values that are never stored).
     const bf16x8* ap[4];
-    const bf16x8* bp[2];
+    const bf16x8* bp[4];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
-        const int r = min(m0 + 16 * mi + r16, p.B - 1);
-        ap[mi] = reinterpret_cast<const bf16x8*>(p.h + (size_t)r * p.K + k0 + 8 * kg);
-    }
-#pragma unroll
-    for (int ni = 0; ni < 2; ++ni) {
-        const int c = min(n0 + 16 * ni + r16, p.N - 1);
-        bp[ni] = reinterpret_cast<const bf16x8*>(p.w + (size_t)c * p.K + k0 + 8 * kg);
+    for (int i = 0; i < 4; ++i) {
+        const int r = min(m0 + 16 * i + r16, p.B - 1), c = min(n0 + 16 * i + r16, p.N - 1);
+        ap[i] = reinterpret_cast<const bf16x8*>(p.h + (size_t)r * p.K + 16 * kg);
+        bp[i] = reinterpret_cast<const bf16x8*>(p.w + (size_t)c * p.K + 16 * kg);
     }
 
-    f32x4 acc[4][2];
+    f32x4 acc[4][4];
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-#pragma unroll 4
-    for (int s = 0; s < kq / kKStep; ++s) {
-        bf16x8 bv[2], av[4];
+#pragma unroll 2
+    for (int sp = s_lo; sp < s_hi; ++sp) {
+        bf16x8 av[4][2], bv[4][2];
+        const int o = sp * (kSuper / 8);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) bv[ni] = __builtin_nontemporal_load(bp[ni] + s * (kKStep / 8));
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) av[mi] = ap[mi][s * (kKStep / 8)];
+            for (int q = 0; q < 2; ++q) { bv[i][q] = bp[i][o + q]; av[i][q] = ap[i][o + q]; }
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
-            for (int ni = 0; ni < 2; ++ni)
-                acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mi], bv[ni], acc[mi][ni], 0, 0, 0);
+            for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                for (int ni = 0; ni < 4; ++ni)
+                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mi][q], bv[ni][q], acc[mi][ni], 0, 0, 0);
     }
 
-    // acc[mi][ni][r] is output (row 16 mi + 4 kg + r, column 16 ni + r16) of this wave's K quarter.
+    // acc[mi][ni][r] is output (row 16 mi + 4 kg + r, column 16 ni + r16) of this wave's K range.
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
+        for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wv][16 * mi + 4 * kg + r][16 * ni + r16] = acc[mi][ni][r];
     __syncthreads();
-    // 2048 outputs, 8 per thread: row tid / 4, columns 8 (tid % 4) .. +7.
-    const int row = tid >> 2, c0 = 8 * (tid & 3);
+    // 4096 outputs, 8 per thread: row tid / 8, columns 8 (tid % 8) .. +7.
+    const int row = tid >> 3, c0 = 8 * (tid & 7);
     if (m0 + row < p.B) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int col = n0 + c0 + e;
             if (col < p.N) {
-                const float v = ((red[0][row][c0 + e] + red[1][row][c0 + e]) + red[2][row][c0 + e]) + red[3][row][c0 + e];
+                float v = red[0][row][c0 + e];
+#pragma unroll
+                for (int q = 1; q < kWaves; ++q) v += red[q][row][c0 + e];
                 store_out(p, m0 + row, col, v);
             }
         }
@@ -128,7 +133,7 @@ extern "C" hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, c
     using namespace ixg;
     const hipError_t e = ix_gdn_check_cfg_(cfg);
     if (e != hipSuccess) return e;
-    if (B <= 0 || B > 65535 * kMt || hidden <= 0 || hidden % (kWaves * kKStep) != 0) return hipErrorInvalidValue;
+    if (B <= 0 || B > 65535 * kMt || hidden <= 0 || hidden % kSuper != 0) return hipErrorInvalidValue;
     if (!h || !w || !x || !z || !a || !b) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(w)) & 15) return hipErrorInvalidValue;
     if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(a) |

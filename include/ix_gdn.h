@@ -249,7 +249,7 @@ int ix_gdn_in_proj_width(const ix_gdn_cfg* cfg);
  * per-token GEMVs): y = h W^T with h [B][hidden] bf16, W [N][hidden] bf16 (N as above), fp32
  * accumulation on bf16 MFMA, written as bf16 (RNE) pieces x [B][C], z [B][h_v][d_v],
  * a [B][h_v], b [B][h_v] -- the inputs of ix_gdn_decode(_gated) and ix_gdn_prefill(_gated) --
- * and, when y is not NULL, as fp32 y [B][N]. Requires hidden % 128 == 0, h and W 16-byte
+ * and, when y is not NULL, as fp32 y [B][N]. Requires hidden % 64 == 0, h and W 16-byte
  * aligned. */
 hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, const uint16_t* h, const uint16_t* w,
                           uint16_t* x, uint16_t* z, uint16_t* a, uint16_t* b, float* y,
