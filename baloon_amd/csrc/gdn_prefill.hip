@@ -38,8 +38,6 @@ namespace ixg {
 namespace {
 
 constexpr int kChunk = 64;
-constexpr int kSlice = 16;                     // state columns per chain workgroup
-constexpr int kSlices = kD / kSlice;           // 8
 constexpr int kPlanThreads = 1024;
 
 typedef float v4 __attribute__((ext_vector_type(4)));
@@ -61,13 +59,15 @@ struct Ws {
     float* vv;           // [h_v][T][128] conv output v
     float* lg;           // [h_v][T] log decay
     float* bt;           // [h_v][T] beta
-    float* W;            // [NC][h_v][64][128]
+    uint16_t* Wf;        // [NC][h_v] W (64 x 128) as split-bf16 A fragments
     float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
-    float* M;            // [NC][h_v][64][64]
+    uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
     float* G;            // [NC][h_v][64] cumulative log decay (padded rows repeat the last)
-    float* Kt;           // [NC][h_k][128][64]  K transposed, zero beyond the chunk length
+    uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
+    uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
+    float* sink;         // [16][64] target of the chain's stores for rows past a sequence end
 };
-constexpr int kWsSections = 14;
+constexpr int kWsSections = 16;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -81,7 +81,8 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
         sizeof(float) * c->h_v * (size_t)T,
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk,
-        sizeof(float) * NC * c->h_k * kD * kChunk,
+        sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
+        sizeof(float) * 16 * kWave,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -99,11 +100,13 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.vv = reinterpret_cast<float*>(base + off[6]);
     w.lg = reinterpret_cast<float*>(base + off[7]);
     w.bt = reinterpret_cast<float*>(base + off[8]);
-    w.W = reinterpret_cast<float*>(base + off[9]);
+    w.Wf = reinterpret_cast<uint16_t*>(base + off[9]);
     w.Ut = reinterpret_cast<float*>(base + off[10]);
-    w.M = reinterpret_cast<float*>(base + off[11]);
+    w.Mf = reinterpret_cast<uint16_t*>(base + off[11]);
     w.G = reinterpret_cast<float*>(base + off[12]);
-    w.Kt = reinterpret_cast<float*>(base + off[13]);
+    w.Ktf = reinterpret_cast<uint16_t*>(base + off[13]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[14]);
+    w.sink = reinterpret_cast<float*>(base + off[15]);
     return w;
 }
 
@@ -299,9 +302,50 @@ __global__ void __launch_bounds__(256) commit_kernel(const PrefillParams p) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Split-bf16 operand fragments.
+//
+// The chain runs its products on v_mfma_f32_16x16x32_bf16 with each fp32 operand x split
+// into x_hi = bf16(x) and x_lo = bf16(x - x_hi); a product is hi*hi + hi*lo + lo*hi in fp32
+// accumulators (relative error ~2^-16, against 2^-8 for one bf16 product). The chunk kernel
+// writes the chain's A operands already split, in the instruction's A layout: fragment
+// (m, ks) of a (rows x k) tile covers rows 16m..16m+15 and k = 32ks..32ks+31, and lane l of
+// it holds row 16m + l%16, k = 32ks + 8(l/16) .. +7 as 8 bf16 (16 bytes). Stored
+// [m][ks][plane hi, lo][lane][8]: one coalesced 16-byte load per lane per fragment and plane.
+// ---------------------------------------------------------------------------------------
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ size_t frag_at(int m, int ks, int nks, int plane, int lane) {
+    return ((((size_t)m * nks + ks) * 2 + plane) * kWave + lane) * 8;       // in bf16 elements
+}
+
+// Split 8 fp32 values into hi and lo bf16 vectors.
+__device__ __forceinline__ void split8(const float (&x)[8], bf8& hi, bf8& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const __bf16 h = (__bf16)x[e];
+        hi[e] = h;
+        lo[e] = (__bf16)(x[e] - (float)h);
+    }
+}
+
+__device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nks, int lane, const float (&x)[8]) {
+    bf8 hi, lo;
+    split8(x, hi, lo);
+    *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 0, lane)) = hi;
+    *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 1, lane)) = lo;
+}
+
+// Fragment sizes in bf16 elements: (rows/16) x (k/32) fragments x 2 planes x 512.
+constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (W, Q)
+constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (M)
+constexpr size_t kFragKt = 8 * 2 * 2 * 512;    // 128 x 64 (K^T)
+
+// ---------------------------------------------------------------------------------------
 // chunk-local: grid (NC, h_v), 256 threads; workgroup = (chunk, v head)
 // ---------------------------------------------------------------------------------------
-constexpr int kKS = kD + 4;          // padded LDS row stride of the K tile
+constexpr int kKS = kD + 4;          // padded LDS row stride of the K / W tile
+constexpr int kMS = kChunk + 4;      // padded LDS row stride of the M tile
 
 // The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
 __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
@@ -309,9 +353,16 @@ __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
     bc = i - br * (br + 1) / 2;
 }
 
+// Phases (one workgroup): stage K | K K^T and Q K^T (fp32 MFMA) -> A, M in LDS | M (and, for
+// the first v head of a q/k head, K^T and Q) as fragments; the right-hand sides into
+// registers | forward substitution (I + A) X = R, one column per thread | W and U columns
+// back to LDS | W as fragments, U transposed, with coalesced stores.
 __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float K_s[kChunk][kKS];
-    __shared__ __align__(16) float A_s[kChunk][kChunk];
+    __shared__ __align__(16) float lds[kChunk * kKS + kChunk * kChunk + kChunk * kMS];
+    float (*K_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);                       // K, then W
+    float (*A_s)[kChunk] = reinterpret_cast<float (*)[kChunk]>(lds + kChunk * kKS);
+    float (*M_s)[kMS] = reinterpret_cast<float (*)[kMS]>(lds + kChunk * kKS + kChunk * kChunk);
+    float* U_s = lds + kChunk * kKS;       // after the substitution: U^T [128][64], 16-byte chunks swizzled
     __shared__ float G_s[kChunk], B_s[kChunk];
 
     ChunkGeo g;
@@ -319,9 +370,10 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
     if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
     const int h = blockIdx.y, src = src_of(L, h);
+    const bool first_head = mapped_head(L, src, 0) == h;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int li = lane & 15, lg4 = lane >> 4;
-    const size_t ch = (size_t)c * L.h_v + h;
+    const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
     const float* kbase = p.ws.kn + ((size_t)src * p.T + g.t0) * kD;
     const float* qbase = p.ws.qn + ((size_t)src * p.T + g.t0) * kD;
 
@@ -345,9 +397,8 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
     }
     __syncthreads();
 
-    // K K^T and Q K^T on the lower block triangle, then A (into LDS) and M (to the workspace).
+    // K K^T and Q K^T on the lower block triangle -> A and M (LDS; upper blocks zero).
     // MFMA k index of (block 4m + e, lane group g) is 16 m + 4 g + e for both operands.
-    float* Mg = p.ws.M + ch * kChunk * kChunk;
     for (int i = w; i < 10; i += 4) {
         int br, bc;
         tri_block(i, br, bc);
@@ -376,99 +427,170 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
                 if (s < t) av = B_s[t] * e * kk[r];
             }
             A_s[t][s] = av;
-            Mg[t * kChunk + s] = mv;
+            M_s[t][s] = mv;
         }
     }
-    // the upper blocks of M are zero
     for (int e = tid; e < 6 * 256; e += 256) {
         const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
         const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
-        Mg[(16 * br + r) * kChunk + 16 * bc + col] = 0.0f;
+        A_s[16 * br + r][16 * bc + col] = 0.0f;
+        M_s[16 * br + r][16 * bc + col] = 0.0f;
     }
     __syncthreads();
 
-    // Forward substitution (I + A) X = R for the 256 columns of R = [diag(beta Gam) K | diag(beta) V]:
-    // waves 0-1 own the W columns, waves 2-3 the U columns (a wave-uniform split).
-    {
-        const int j = tid & (kD - 1);
-        const bool is_w = tid < kD;
-        float xr[kChunk];
-        if (is_w) {
+    // M as fragments (4 x 2 fragments x 64 lanes: 512 units, 2 per thread).
+    uint16_t* Mf = p.ws.Mf + ch * kFragM;
+    for (int u = tid; u < 4 * 2 * kWave; u += 256) {
+        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
+        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+        float x[8];
 #pragma unroll
-            for (int t = 0; t < kChunk; ++t) xr[t] = B_s[t] * expf(G_s[t]) * K_s[t][j];
-        } else {
-            const float* vsrc = p.ws.vv + ((size_t)h * p.T + g.t0) * kD + j;
+        for (int e = 0; e < 8; ++e) x[e] = M_s[row][k0 + e];
+        store_frag(Mf, m, ks, 2, ln, x);
+    }
+    // K^T and Q of the q/k head, once per (chunk, q/k head). K^T (rows i, k = token t):
+    // 8 x 2 fragments; Q (rows t, k = i): 4 x 4 fragments, zero rows past the chunk end.
+    if (first_head) {
+        uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
+        for (int u = tid; u < 8 * 2 * kWave; u += 256) {
+            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            float x[8];
 #pragma unroll
-            for (int t = 0; t < kChunk; ++t) xr[t] = t < g.len ? B_s[t] * vsrc[(size_t)t * kD] : 0.0f;
+            for (int e = 0; e < 8; ++e) x[e] = K_s[k0 + e][row];
+            store_frag(Ktf, m, ks, 2, ln, x);
         }
-        // Four partial sums per row keep the dependent FMA chain short.
+        uint16_t* Qf = p.ws.Qf + cs * kFragW;
+        for (int u = tid; u < 4 * 4 * kWave; u += 256) {
+            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (row < g.len) {
+                const v4 a = *reinterpret_cast<const v4*>(qbase + (size_t)row * kD + k0);
+                const v4 b = *reinterpret_cast<const v4*>(qbase + (size_t)row * kD + k0 + 4);
 #pragma unroll
-        for (int t = 1; t < kChunk; ++t) {
-            float r[4] = {xr[t], 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int q4 = 0; q4 < t; q4 += 4) {
-                const v4 av = *reinterpret_cast<const v4*>(&A_s[t][q4]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (q4 + e < t) r[e] = fmaf(-av[e], xr[q4 + e], r[e]);
+                for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
             }
-            xr[t] = (r[0] + r[1]) + (r[2] + r[3]);
-        }
-        if (is_w) {
-            float* dst = p.ws.W + ch * kChunk * kD + j;
-#pragma unroll
-            for (int t = 0; t < kChunk; ++t) dst[(size_t)t * kD] = xr[t];
-        } else {
-            v4* dst = reinterpret_cast<v4*>(p.ws.Ut + (ch * kD + j) * kChunk);     // column j of U, contiguous
-#pragma unroll
-            for (int t4 = 0; t4 < kChunk / 4; ++t4) dst[t4] = v4{xr[4 * t4], xr[4 * t4 + 1], xr[4 * t4 + 2], xr[4 * t4 + 3]};
+            store_frag(Qf, m, ks, 4, ln, x);
         }
     }
-    // K^T of the chunk for the chain's state update, written once per (chunk, q/k head) by the
-    // workgroup of its first mapped v head: thread (i = tid / 2, half = tid % 2) writes
-    // tokens 32 half .. +31 of row i.
-    if (mapped_head(L, src, 0) == h) {
-        const int i = tid >> 1, t0h = 32 * (tid & 1);
-        v4* dst = reinterpret_cast<v4*>(p.ws.Kt + (((size_t)c * L.h_k + src) * kD + i) * kChunk + t0h);
+
+    // Forward substitution (I + A) X = R for the 256 columns of R = [diag(beta Gam) K | diag(beta) V]:
+    // waves 0-1 own the W columns, waves 2-3 the U columns (a wave-uniform split).
+    const int j = tid & (kD - 1);
+    const bool is_w = tid < kD;
+    float xr[kChunk];
+    if (is_w) {
 #pragma unroll
-        for (int t4 = 0; t4 < 8; ++t4)
-            dst[t4] = v4{K_s[t0h + 4 * t4][i], K_s[t0h + 4 * t4 + 1][i], K_s[t0h + 4 * t4 + 2][i], K_s[t0h + 4 * t4 + 3][i]};
+        for (int t = 0; t < kChunk; ++t) xr[t] = B_s[t] * expf(G_s[t]) * K_s[t][j];
+    } else {
+        const float* vsrc = p.ws.vv + ((size_t)h * p.T + g.t0) * kD + j;
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) xr[t] = t < g.len ? B_s[t] * vsrc[(size_t)t * kD] : 0.0f;
+    }
+    // Four partial sums per row keep the dependent FMA chain short.
+#pragma unroll
+    for (int t = 1; t < kChunk; ++t) {
+        float r[4] = {xr[t], 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int q4 = 0; q4 < t; q4 += 4) {
+            const v4 av = *reinterpret_cast<const v4*>(&A_s[t][q4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (q4 + e < t) r[e] = fmaf(-av[e], xr[q4 + e], r[e]);
+        }
+        xr[t] = (r[0] + r[1]) + (r[2] + r[3]);
+    }
+    __syncthreads();                           // K_s, A_s and M_s are free: W and U^T take their place
+    if (is_w) {
+#pragma unroll
+        for (int t = 0; t < kChunk; ++t) K_s[t][j] = xr[t];
+    } else {
+        // row j of U^T, 16 chunks of 4 tokens at chunk position e ^ (j & 15)
+#pragma unroll
+        for (int e = 0; e < kChunk / 4; ++e)
+            *reinterpret_cast<v4*>(U_s + j * kChunk + 4 * (e ^ (j & 15))) =
+                v4{xr[4 * e], xr[4 * e + 1], xr[4 * e + 2], xr[4 * e + 3]};
+    }
+    __syncthreads();
+    // W as fragments (4 x 4 x 64 = 1024 units), U^T row by row (2048 16-byte chunks).
+    uint16_t* Wf = p.ws.Wf + ch * kFragW;
+    for (int u = tid; u < 4 * 4 * kWave; u += 256) {
+        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
+        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+        float x[8];
+        const v4 a = *reinterpret_cast<const v4*>(&K_s[row][k0]), b = *reinterpret_cast<const v4*>(&K_s[row][k0 + 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
+        store_frag(Wf, m, ks, 4, ln, x);
+    }
+    v4* Ut = reinterpret_cast<v4*>(p.ws.Ut + ch * kD * kChunk);
+    for (int u = tid; u < kD * kChunk / 4; u += 256) {
+        const int jj = u >> 4, e = u & 15;
+        Ut[u] = *reinterpret_cast<const v4*>(U_s + jj * kChunk + 4 * (e ^ (jj & 15)));
     }
 }
 
 // ---------------------------------------------------------------------------------------
-// chain: one workgroup per (sequence, v head, 16-column slice), 256 threads
+// chain: one workgroup per (sequence, v head, 32-column state slice), 512 threads
 // ---------------------------------------------------------------------------------------
-// LDS tiles of the chain are stored column by column (4 padding words per column), so the
-// 4 consecutive rows of one column that a lane needs are one 16-byte access.
-constexpr int kSCol = kD + 4;          // state slice column stride
-constexpr int kDCol = kChunk + 4;      // D tile column stride
-
-// The chain workgroup has 8 waves in two roles that meet at two barriers per chunk:
+// The workgroup has 8 waves in two roles that meet at two barriers per chunk:
 //   state waves (0-3): S -> LDS | W S, D = U - W S -> LDS | S' = Gam_last S + K^T (exp(G_last - G) D)
 //   output waves (4-7):          | Q S                   | O = diag(Gam) Q S + M D
+// All products are split-bf16 MFMA (16x16x32). The A operands (W, K^T, Q, M) come from the
+// chunk kernel's fragments; the B operands (S, D, Dg) are split by their producer wave into
+// LDS fragments of the B layout: fragment (ks, nt) covers k = 32ks..32ks+31 and columns
+// 16nt..16nt+15; lane l holds column 16nt + l%16, k = 32ks + 8(l/16) .. +7.
+// Lane (li = lane & 15, lg4 = lane >> 4) of role wave r: output rows 16r + 4lg4 + i in C layout;
+// state wave r owns state rows 32r .. 32r + 31 (two 16-row m-tiles) of the slice's 32 columns.
 // Each role loads the next chunk's operands (double buffer) while it computes the current one.
-// Lane (li = lane & 15, lg4 = lane >> 4) of role wave r uses rows 16 r + li of the 64-row
-// chunk tiles as MFMA A operands and rows 16 r + 4 lg4 + i in C layout; state wave r owns
-// state rows (k index) 32 r .. 32 r + 31.
+constexpr int kSlice = 32;                      // state columns per chain workgroup
+constexpr int kSlices = kD / kSlice;            // 4
+constexpr int kNT = kSlice / 16;                // 16-column tiles per slice
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+
+// B-fragment LDS tiles of the chain (bf16 elements): S (k = state row, 4 ks), D and Dg (k = token, 2 ks).
+constexpr int kBFrag = 2 * kWave * 8;                       // one (ks, nt) fragment, both planes
+__device__ __forceinline__ int bfrag_at(int ks, int nt, int plane, int ln) {
+    return ((ks * kNT + nt) * 2 + plane) * kWave * 8 + ln * 8;
+}
+
+// Write 4 consecutive k values (k = 4 q .. 4 q + 3 within the fragment's 32, q = 0..7) of
+// column n (0..15) of fragment (ks, nt), split, into a B-fragment tile.
+__device__ __forceinline__ void bfrag_put4(uint16_t* tile, int ks, int nt, int q, int n, const f4& v) {
+    const int ln = 16 * (q >> 1) + n, e0 = 4 * (q & 1);
+    uint16_t hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const __bf16 hb = (__bf16)v[e];
+        hi[e] = __builtin_bit_cast(uint16_t, hb);
+        lo[e] = __builtin_bit_cast(uint16_t, (__bf16)(v[e] - (float)hb));
+    }
+    uint2 h2 = {(uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16)};
+    uint2 l2 = {(uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16)};
+    *reinterpret_cast<uint2*>(tile + bfrag_at(ks, nt, 0, ln) + e0) = h2;
+    *reinterpret_cast<uint2*>(tile + bfrag_at(ks, nt, 1, ln) + e0) = l2;
+}
+
 struct StateOps {
-    v4 aw[8];             // W row 16r+li, k = 16 m + 4 lg4 + e
-    v4 kt[2][4];          // K^T row 32 r + 16 tt + li, token 16 q + 4 lg4 + e
-    v4 u;                 // U rows 16r + 4 lg4 + i, column j0 + li
-    v4 gv;                // G at those rows
+    bf8 w[4][2];          // W fragments (m = r, ks 0..3), planes
+    bf8 kt[2][2][2];      // K^T fragments (m = 2r + mt, ks 0..1), planes
+    f4 u[kNT];            // U rows 16r + 4lg4 + i, columns j0 + 16nt + li
+    f4 gv;                // G at those rows
     float glast;          // G of the chunk's last row
 };
 struct OutOps {
-    v4 aq[8];             // Q row 16r+li (the last row again past the chunk end)
-    v4 am[4];             // M row 16r+li, s = 16 m + 4 lg4 + e
-    v4 gv;
+    bf8 q[4][2];          // Q fragments (m = r, ks 0..3), planes
+    bf8 m[2][2];          // M fragments (m = r, ks 0..1), planes
+    f4 gv;
     int t0, len;
 };
 
 struct ChainCtx {
     const PrefillParams* p;
-    const float* qbase;   // q rows of the head's q/k head
-    int h, src, seq_lo, seq_hi, c_begin, j0, r, li, lg4;
+    int h, src, seq_lo, seq_hi, c_begin, j0, r, li, lg4, lane;
 };
 
 __device__ __forceinline__ size_t chain_ch(const ChainCtx& x, int c) { return (size_t)c * x.p->L.h_v + x.h; }
@@ -476,19 +598,25 @@ __device__ __forceinline__ size_t chain_ch(const ChainCtx& x, int c) { return (s
 __device__ __forceinline__ void load_state_ops(const ChainCtx& x, int c, StateOps& o) {
     const PrefillParams& p = *x.p;
     const size_t ch = chain_ch(x, c);
-    const float* Wc = p.ws.W + ch * kChunk * kD;
+    const uint16_t* Wf = p.ws.Wf + ch * kFragW;
+    const uint16_t* Kf = p.ws.Ktf + ((size_t)c * p.L.h_k + x.src) * kFragKt;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) o.w[ks][pl] = *reinterpret_cast<const bf8*>(Wf + frag_at(x.r, ks, 4, pl, x.lane));
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl)
+                o.kt[mt][ks][pl] = *reinterpret_cast<const bf8*>(Kf + frag_at(2 * x.r + mt, ks, 2, pl, x.lane));
+    const int crow = 16 * x.r + 4 * x.lg4;
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+        o.u[nt] = *reinterpret_cast<const f4*>(p.ws.Ut + (ch * kD + x.j0 + 16 * nt + x.li) * kChunk + crow);
     const float* Gc = p.ws.G + ch * kChunk;
-    const float* Kc = p.ws.Kt + ((size_t)c * p.L.h_k + x.src) * kD * kChunk;
-    const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
-#pragma unroll
-    for (int m = 0; m < 8; ++m) o.aw[m] = *reinterpret_cast<const v4*>(Wc + (size_t)arow * kD + 16 * m + 4 * x.lg4);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            o.kt[tt][q] = *reinterpret_cast<const v4*>(Kc + (size_t)(32 * x.r + 16 * tt + x.li) * kChunk + 16 * q + 4 * x.lg4);
-    o.u = *reinterpret_cast<const v4*>(p.ws.Ut + (ch * kD + x.j0 + x.li) * kChunk + crow);
-    o.gv = *reinterpret_cast<const v4*>(Gc + crow);
+    o.gv = *reinterpret_cast<const f4*>(Gc + crow);
     o.glast = Gc[kChunk - 1];
 }
 
@@ -497,107 +625,197 @@ __device__ __forceinline__ void load_out_ops(const ChainCtx& x, int c, OutOps& o
     const size_t ch = chain_ch(x, c);
     o.t0 = x.seq_lo + (c - x.c_begin) * kChunk;            // chunk c of the sequence (no table lookup)
     o.len = min(kChunk, x.seq_hi - o.t0);
-    const int arow = 16 * x.r + x.li, crow = 16 * x.r + 4 * x.lg4;
-    // Q rows past the chunk end re-read its last row: an MFMA output row depends only on its
-    // own A row, so those rows only produce output rows that are never stored.
-    const float* qr = x.qbase + (size_t)(o.t0 + min(arow, o.len - 1)) * kD + 4 * x.lg4;
+    const uint16_t* Qf = p.ws.Qf + ((size_t)c * p.L.h_k + x.src) * kFragW;
+    const uint16_t* Mf = p.ws.Mf + ch * kFragM;
 #pragma unroll
-    for (int m = 0; m < 8; ++m) o.aq[m] = *reinterpret_cast<const v4*>(qr + 16 * m);
-    const float* Mc = p.ws.M + ch * kChunk * kChunk;
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) o.am[m] = *reinterpret_cast<const v4*>(Mc + (size_t)arow * kChunk + 16 * m + 4 * x.lg4);
-    o.gv = *reinterpret_cast<const v4*>(p.ws.G + ch * kChunk + crow);
+        for (int pl = 0; pl < 2; ++pl) o.q[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(x.r, ks, 4, pl, x.lane));
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) o.m[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(x.r, ks, 2, pl, x.lane));
+    o.gv = *reinterpret_cast<const f4*>(p.ws.G + ch * kChunk + 16 * x.r + 4 * x.lg4);
 }
 
 // State waves, one chunk: D = U - W S, S' = Gam_last S + K^T (exp(G_last - G) D).
-__device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o, v4 (&S)[2], float* S_l,
-                                           float* D_l, float* Dg_l) {
-    const int r = x.r, li = x.li, lg4 = x.lg4, crow = 16 * r + 4 * lg4;
+// S[mt][nt]: rows 32r + 16mt + 4lg4 + i, columns 16nt + li of the slice.
+__device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o, f4 (&S)[2][kNT], uint16_t* S_f,
+                                           uint16_t* D_f, uint16_t* Dg_f) {
+    const int r = x.r, li = x.li, lg4 = x.lg4, lane = x.lane;
+    // S into B fragments: state row i = 32r + 16mt + 4lg4 + e -> ks = r, q = 4mt + lg4
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(S_l + li * kSCol + 32 * r + 16 * tt + 4 * lg4) = S[tt];
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) bfrag_put4(S_f, r, nt, 4 * mt + lg4, li, S[mt][nt]);
     lds_barrier();                                                    // (A) state slice visible
 
-    // W S for rows 16r..16r+15; k index of block (m, e), lane group g: 16 m + 4 g + e (each
-    // load instruction of a wave then reads 64 contiguous bytes of 16 operand rows).
-    v4 ws[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // W S: the three split products and the column tiles accumulate separately (six
+    // independent MFMA chains), and all B fragments of a k-step are read before its MFMAs.
+    f4 ws[kNT][3];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 16 * m + 4 * lg4);
+    for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ws[m & 1] = mfma4(o.aw[m][e], bv[e], ws[m & 1]);
+        for (int q = 0; q < 3; ++q) ws[nt][q] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        bf8 bh[kNT], bl[kNT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            bh[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 0, lane));
+            bl[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 1, lane));
+        }
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            ws[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][0], bh[nt], ws[nt][0], 0, 0, 0);
+            ws[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][0], bl[nt], ws[nt][1], 0, 0, 0);
+            ws[nt][2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][1], bh[nt], ws[nt][2], 0, 0, 0);
+        }
     }
-    v4 d, dg;
+    f4 d[kNT], dg[kNT];
+    f4 eg;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        d[i] = o.u[i] - (ws[0][i] + ws[1][i]);
-        dg[i] = expf(o.glast - o.gv[i]) * d[i];
+    for (int i = 0; i < 4; ++i) eg[i] = expf(o.glast - o.gv[i]);
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            d[nt][i] = o.u[nt][i] - (ws[nt][0][i] + (ws[nt][1][i] + ws[nt][2][i]));
+            dg[nt][i] = eg[i] * d[nt][i];
+        }
     }
-    *reinterpret_cast<v4*>(D_l + li * kDCol + crow) = d;
-    *reinterpret_cast<v4*>(Dg_l + li * kDCol + crow) = dg;
+    // D, Dg into B fragments: token t = 16r + 4lg4 + e -> ks = r >> 1, q = 4 (r & 1) + lg4
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+        bfrag_put4(D_f, r >> 1, nt, 4 * (r & 1) + lg4, li, d[nt]);
+        bfrag_put4(Dg_f, r >> 1, nt, 4 * (r & 1) + lg4, li, dg[nt]);
+    }
     lds_barrier();                                                    // (B) D visible
 
-    // S' = Gam_last S + K^T Dg; token index of block (q, e): 16 q + 4 g + e.
+    // S' = Gam_last S + K^T Dg: the state tile takes the hi*hi products; hi*lo and lo*hi
+    // go to a second accumulator per tile, added at the end.
     const float gl = expf(o.glast);
-    v4 dgv[4];
+    f4 sx[2][kNT];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) dgv[m] = *reinterpret_cast<const v4*>(Dg_l + li * kDCol + 16 * m + 4 * lg4);
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        v4 acc = {0.f, 0.f, 0.f, 0.f};
-        S[tt] *= gl;
+        for (int nt = 0; nt < kNT; ++nt) { S[mt][nt] *= gl; sx[mt][nt] = f4{0.f, 0.f, 0.f, 0.f}; }
 #pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            if (b & 1) acc = mfma4(o.kt[tt][b >> 2][b & 3], dgv[b >> 2][b & 3], acc);
-            else S[tt] = mfma4(o.kt[tt][b >> 2][b & 3], dgv[b >> 2][b & 3], S[tt]);
+    for (int ks = 0; ks < 2; ++ks) {
+        bf8 bh[kNT], bl[kNT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            bh[nt] = *reinterpret_cast<const bf8*>(Dg_f + bfrag_at(ks, nt, 0, lane));
+            bl[nt] = *reinterpret_cast<const bf8*>(Dg_f + bfrag_at(ks, nt, 1, lane));
         }
-        S[tt] += acc;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt) {
+                S[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][0], bh[nt], S[mt][nt], 0, 0, 0);
+                sx[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][0], bl[nt], sx[mt][nt], 0, 0, 0);
+                sx[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][1], bh[nt], sx[mt][nt], 0, 0, 0);
+            }
     }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) S[mt][nt] += sx[mt][nt];
 }
 
-// Output waves, one chunk: O = diag(Gam) Q S + M D for rows 16r..16r+15.
-__device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, const float* S_l, const float* D_l) {
+// Output waves, one chunk: O = diag(Gam) Q S + M D for rows 16r..16r+15. OUT: bit 0 fp32 o,
+// bit 1 bf16 o. Every store is issued (rows past the sequence end go to the sink), so the
+// number of memory operations per chunk is fixed and the next chunk's operand loads never
+// have to wait for this chunk's stores.
+template <int OUT>
+__device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, const uint16_t* S_f, const uint16_t* D_f) {
     const PrefillParams& p = *x.p;
-    const int r = x.r, li = x.li, lg4 = x.lg4, crow = 16 * r + 4 * lg4;
+    const int r = x.r, li = x.li, lg4 = x.lg4, lane = x.lane, crow = 16 * r + 4 * lg4;
     lds_barrier();                                                    // (A)
-    v4 qs[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    f4 qs[kNT][3];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(S_l + li * kSCol + 16 * m + 4 * lg4);
+    for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) qs[m & 1] = mfma4(o.aq[m][e], bv[e], qs[m & 1]);
+        for (int q = 0; q < 3; ++q) qs[nt][q] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        bf8 bh[kNT], bl[kNT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            bh[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 0, lane));
+            bl[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 1, lane));
+        }
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            qs[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][0], bh[nt], qs[nt][0], 0, 0, 0);
+            qs[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][0], bl[nt], qs[nt][1], 0, 0, 0);
+            qs[nt][2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][1], bh[nt], qs[nt][2], 0, 0, 0);
+        }
     }
     lds_barrier();                                                    // (B)
-    v4 ov[2];
+    f4 eg;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) { ov[0][i] = expf(o.gv[i]) * (qs[0][i] + qs[1][i]); ov[1][i] = 0.0f; }
+    for (int i = 0; i < 4; ++i) eg[i] = expf(o.gv[i]);
+    f4 md[kNT][2];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const v4 bv = *reinterpret_cast<const v4*>(D_l + li * kDCol + 16 * m + 4 * lg4);
+    for (int nt = 0; nt < kNT; ++nt) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[m & 1] = mfma4(o.am[m][e], bv[e], ov[m & 1]);
+        for (int i = 0; i < 4; ++i) md[nt][0][i] = eg[i] * (qs[nt][0][i] + (qs[nt][1][i] + qs[nt][2][i]));
+        md[nt][1] = f4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = crow + i;
-        if (t < o.len) {
-            const size_t oo = ((size_t)(o.t0 + t) * p.L.h_v + x.h) * kD + x.j0 + li;
-            const float ovr = ov[0][i] + ov[1][i];
-            if (p.o) p.o[oo] = ovr;
-            if (p.o_bf16) p.o_bf16[oo] = f32_to_bf16(ovr);
+    for (int ks = 0; ks < 2; ++ks) {
+        bf8 bh[kNT], bl[kNT];
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            bh[nt] = *reinterpret_cast<const bf8*>(D_f + bfrag_at(ks, nt, 0, lane));
+            bl[nt] = *reinterpret_cast<const bf8*>(D_f + bfrag_at(ks, nt, 1, lane));
+        }
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) {
+            md[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][0], bh[nt], md[nt][0], 0, 0, 0);
+            md[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][0], bl[nt], md[nt][1], 0, 0, 0);
+            md[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][1], bh[nt], md[nt][1], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+        const f4 ov = md[nt][0] + md[nt][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = crow + i;
+            const size_t oo = ((size_t)(o.t0 + t) * p.L.h_v + x.h) * kD + x.j0 + 16 * nt + li;
+            const bool in = t < o.len;
+            if constexpr ((OUT & 1) != 0) *(in ? p.o + oo : p.ws.sink + lane) = ov[i];
+            if constexpr ((OUT & 2) != 0)
+                *(in ? p.o_bf16 + oo : reinterpret_cast<uint16_t*>(p.ws.sink) + lane) = f32_to_bf16(ov[i]);
         }
     }
 }
 
+// As many stores as one out_step issues, all to the sink: issued once before the loop so
+// that the memory operations in flight at the loop head are the same on entry as around the
+// loop, and the compiler's wait for the next operands does not cover the last stores.
+template <int OUT>
+__device__ __forceinline__ void sink_stores(const PrefillParams& p, int lane) {
+#pragma unroll
+    for (int i = 0; i < kNT * 4; ++i) {            // distinct addresses: none of them is redundant
+        if constexpr ((OUT & 1) != 0) p.ws.sink[i * kWave + lane] = 0.0f;
+        if constexpr ((OUT & 2) != 0) reinterpret_cast<uint16_t*>(p.ws.sink + 8 * kWave)[i * kWave + lane] = 0;
+    }
+}
+
+template <int OUT>
 __global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float S_l[kSlice * kSCol];
-    __shared__ __align__(16) float D_l[kSlice * kDCol];
-    __shared__ __align__(16) float Dg_l[kSlice * kDCol];
+    __shared__ __align__(16) uint16_t S_f[4 * kNT * kBFrag];
+    __shared__ __align__(16) uint16_t D_f[2 * kNT * kBFrag];
+    __shared__ __align__(16) uint16_t Dg_f[2 * kNT * kBFrag];
 
     const Layer& L = p.L;
-    // XCD-aware mapping: the 8 slices of one (sequence, head) pair share an XCD (and its L2).
+    // XCD-aware mapping: the 4 slices of one (sequence, head) pair share an XCD (and its L2).
     const int lin = blockIdx.x, xcd = lin & 7, k = lin >> 3;
-    const int slice = k & 7;
-    const int pair = (k >> 3) * 8 + xcd;
+    const int slice = k & (kSlices - 1);
+    const int pair = (k / kSlices) * 8 + xcd;
     if (pair >= p.n_seq * L.h_v) return;
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
     const int c_begin = p.ws.chunk_off[s], c_end = p.ws.chunk_off[s + 1];
@@ -606,7 +824,6 @@ __global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
 
     ChainCtx x;
     x.p = &p;
-    x.qbase = p.ws.qn + (size_t)src * p.T * kD;
     x.h = h;
     x.src = src;
     x.seq_lo = p.ws.seq_lo[s];
@@ -616,14 +833,18 @@ __global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
     x.r = w & 3;
     x.li = lane & 15;
     x.lg4 = lane >> 4;
+    x.lane = lane;
 
     if (w < 4) {
-        // State slice: rows 32 r + 16 tt + 4 lg4 + i (k index), column j0 + li (v index); the
-        // state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
-        float* st = p.state + (((size_t)s * L.h_v + h) * kD + x.j0 + x.li) * kD + 32 * x.r + 4 * x.lg4;
-        v4 S[2];
+        // State slice: rows 32 r + 16 mt + 4 lg4 + i (k index), columns j0 + 16 nt + li (v
+        // index); the state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
+        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD;
+        f4 S[2][kNT];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) S[tt] = *reinterpret_cast<const v4*>(st + 16 * tt);
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt)
+                S[mt][nt] = *reinterpret_cast<const f4*>(st + (size_t)(x.j0 + 16 * nt + x.li) * kD + 32 * x.r + 16 * mt + 4 * x.lg4);
         __builtin_amdgcn_s_waitcnt(0);             // the state is in registers before the loop
         // Prefetches are unconditional (past the last chunk they re-read it): a load that is
         // skipped on one path forces the compiler to wait for every load in flight.
@@ -632,28 +853,32 @@ __global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
         int c = c_begin;
         for (; c + 1 < c_end; c += 2) {
             load_state_ops(x, c + 1, B);
-            state_step(x, A, S, S_l, D_l, Dg_l);
+            state_step(x, A, S, S_f, D_f, Dg_f);
             __builtin_amdgcn_sched_barrier(0);     // keep A's reload after A's last use
             load_state_ops(x, min(c + 2, c_end - 1), A);
-            state_step(x, B, S, S_l, D_l, Dg_l);
+            state_step(x, B, S, S_f, D_f, Dg_f);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c < c_end) state_step(x, A, S, S_l, D_l, Dg_l);
+        if (c < c_end) state_step(x, A, S, S_f, D_f, Dg_f);
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<v4*>(st + 16 * tt) = S[tt];
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < kNT; ++nt)
+                *reinterpret_cast<f4*>(st + (size_t)(x.j0 + 16 * nt + x.li) * kD + 32 * x.r + 16 * mt + 4 * x.lg4) = S[mt][nt];
     } else {
         OutOps A, B;                               // same schedule as the state waves
         load_out_ops(x, c_begin, A);
+        sink_stores<OUT>(p, lane);
         int c = c_begin;
         for (; c + 1 < c_end; c += 2) {
             load_out_ops(x, c + 1, B);
-            out_step(x, A, S_l, D_l);
+            out_step<OUT>(x, A, S_f, D_f);
             __builtin_amdgcn_sched_barrier(0);
             load_out_ops(x, min(c + 2, c_end - 1), A);
-            out_step(x, B, S_l, D_l);
+            out_step<OUT>(x, B, S_f, D_f);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c < c_end) out_step(x, A, S_l, D_l);
+        if (c < c_end) out_step<OUT>(x, A, S_f, D_f);
     }
 }
 
@@ -733,7 +958,13 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     hipLaunchKernelGGL(commit_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, s, p);
     hipLaunchKernelGGL(chunk_kernel, dim3((unsigned)NC, (unsigned)cfg->h_v), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
-    hipLaunchKernelGGL(chain_kernel, dim3((unsigned)(groups * 64)), dim3(512), 0, s, p);
+    const dim3 cgrid((unsigned)(groups * 8 * kSlices));
+    switch ((p.o ? 1 : 0) | (p.o_bf16 ? 2 : 0)) {
+        case 0: hipLaunchKernelGGL(chain_kernel<0>, cgrid, dim3(512), 0, s, p); break;
+        case 1: hipLaunchKernelGGL(chain_kernel<1>, cgrid, dim3(512), 0, s, p); break;
+        case 2: hipLaunchKernelGGL(chain_kernel<2>, cgrid, dim3(512), 0, s, p); break;
+        default: hipLaunchKernelGGL(chain_kernel<3>, cgrid, dim3(512), 0, s, p); break;
+    }
     if (gate)
         hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o,
                            make_out_gate(gate), rows);
