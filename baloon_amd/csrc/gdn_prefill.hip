@@ -345,7 +345,6 @@ constexpr size_t kFragKt = 8 * 2 * 2 * 512;    // 128 x 64 (K^T)
 // chunk-local: grid (NC, h_v), 256 threads; workgroup = (chunk, v head)
 // ---------------------------------------------------------------------------------------
 constexpr int kKS = kD + 4;          // padded LDS row stride of the K / W tile
-constexpr int kMS = kChunk + 4;      // padded LDS row stride of the M tile
 
 // The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
 __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
@@ -353,16 +352,36 @@ __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
     bc = i - br * (br + 1) / 2;
 }
 
-// Phases (one workgroup): stage K | K K^T and Q K^T (fp32 MFMA) -> A, M in LDS | M (and, for
-// the first v head of a q/k head, K^T and Q) as fragments; the right-hand sides into
-// registers | forward substitution (I + A) X = R, one column per thread | W and U columns
-// back to LDS | W as fragments, U transposed, with coalesced stores.
+// C += X (16 x 16 at x, row stride xs) * Y (16 x 16 at y, row stride ys) on fp32 MFMA
+// (four 16x16x4 steps). Lane l supplies X[l%16][4k + l/16] and Y[4k + l/16][l%16]; C is in
+// the MFMA layout (c[r] = C[4 (l/16) + r][l%16]).
+__device__ __forceinline__ v4 mm16(const float* x, int xs, const float* y, int ys, v4 c, int lane) {
+    const int r16 = lane & 15, k4 = lane >> 4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c = mfma4(x[r16 * xs + 4 * k + k4], y[(4 * k + k4) * ys + r16], c);
+    return c;
+}
+__device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, float scale) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) z[(4 * (lane >> 4) + r) * zs + (lane & 15)] = scale * c[r];
+}
+
+// Phases (one workgroup):
+//   stage K | K K^T and Q K^T (fp32 MFMA) -> A, M in LDS | M (and, for the first v head of a
+//   q/k head, K^T and Q) as split fragments; K rows scaled by beta Gam | T = (I + A)^-1:
+//   the four 16 x 16 diagonal blocks by substitution (one wave), then the off-diagonal
+//   blocks T_ij = -T_ii sum_k A_ik T_kj in three dependency levels of fp32 MFMA block
+//   products | W = T diag(beta Gam) K and U = T diag(beta) V as fp32 MFMA GEMMs (the zero
+//   blocks of T skipped) | W through LDS into fragments, U^T stored from the MFMA layout.
+constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
+
 __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[kChunk * kKS + kChunk * kChunk + kChunk * kMS];
+    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
     float (*K_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);                       // K, then W
-    float (*A_s)[kChunk] = reinterpret_cast<float (*)[kChunk]>(lds + kChunk * kKS);
-    float (*M_s)[kMS] = reinterpret_cast<float (*)[kMS]>(lds + kChunk * kKS + kChunk * kChunk);
-    float* U_s = lds + kChunk * kKS;       // after the substitution: U^T [128][64], 16-byte chunks swizzled
+    float* A_s = lds + kChunk * kKS;                                                 // [64][kTS]
+    float* M_s = A_s + kChunk * kTS;                                                 // M, then T
+    float* T_s = M_s;
+    float* P_s = M_s + kChunk * kTS;                                                 // [3][16][17]
     __shared__ float G_s[kChunk], B_s[kChunk];
 
     ChunkGeo g;
@@ -376,6 +395,7 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
     const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
     const float* kbase = p.ws.kn + ((size_t)src * p.T + g.t0) * kD;
     const float* qbase = p.ws.qn + ((size_t)src * p.T + g.t0) * kD;
+    const float* vbase = p.ws.vv + ((size_t)h * p.T + g.t0) * kD;
 
     // Stage the K rows of the chunk (zero beyond its length); wave 0 also scans the decay.
     for (int e = tid; e < kChunk * (kD / 4); e += 256) {
@@ -394,6 +414,16 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
         G_s[lane] = lgt;
         B_s[lane] = lane < g.len ? p.ws.bt[(size_t)h * p.T + g.t0 + lane] : 0.0f;
         p.ws.G[ch * kChunk + lane] = lgt;
+    }
+    // The U operand rows this lane needs later (beta V, tokens s = 4 ks + lg4, columns
+    // 16 (2 w + nt) + li), loaded now so that their latency overlaps the triangle.
+    float vb[16][2];
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+        const int sr = 4 * ks + lg4;
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            vb[ks][nt] = sr < g.len ? vbase[(size_t)sr * kD + 16 * (2 * w + nt) + li] : 0.0f;
     }
     __syncthreads();
 
@@ -426,15 +456,15 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
                 mv = e * qk[r];
                 if (s < t) av = B_s[t] * e * kk[r];
             }
-            A_s[t][s] = av;
-            M_s[t][s] = mv;
+            A_s[t * kTS + s] = av;
+            M_s[t * kTS + s] = mv;
         }
     }
     for (int e = tid; e < 6 * 256; e += 256) {
         const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
         const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
-        A_s[16 * br + r][16 * bc + col] = 0.0f;
-        M_s[16 * br + r][16 * bc + col] = 0.0f;
+        A_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
+        M_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
     }
     __syncthreads();
 
@@ -445,7 +475,7 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
         const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
         float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = M_s[row][k0 + e];
+        for (int e = 0; e < 8; ++e) x[e] = M_s[row * kTS + k0 + e];
         store_frag(Mf, m, ks, 2, ln, x);
     }
     // K^T and Q of the q/k head, once per (chunk, q/k head). K^T (rows i, k = token t):
@@ -474,46 +504,100 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
             store_frag(Qf, m, ks, 4, ln, x);
         }
     }
+    __syncthreads();                       // M_s and the raw K_s are no longer read
 
-    // Forward substitution (I + A) X = R for the 256 columns of R = [diag(beta Gam) K | diag(beta) V]:
-    // waves 0-1 own the W columns, waves 2-3 the U columns (a wave-uniform split).
-    const int j = tid & (kD - 1);
-    const bool is_w = tid < kD;
-    float xr[kChunk];
-    if (is_w) {
-#pragma unroll
-        for (int t = 0; t < kChunk; ++t) xr[t] = B_s[t] * expf(G_s[t]) * K_s[t][j];
-    } else {
-        const float* vsrc = p.ws.vv + ((size_t)h * p.T + g.t0) * kD + j;
-#pragma unroll
-        for (int t = 0; t < kChunk; ++t) xr[t] = t < g.len ? B_s[t] * vsrc[(size_t)t * kD] : 0.0f;
+    // Scale the K rows by beta Gam (the W right-hand side); wave 0 inverts the four unit
+    // lower-triangular diagonal blocks of I + A (lane = 16 b + column c), the other waves
+    // clear the upper blocks of T.
+    for (int e = tid; e < kChunk * (kD / 4); e += 256) {
+        const int t = e / (kD / 4), c4 = e % (kD / 4);
+        const float sc = B_s[t] * expf(G_s[t]);
+        v4 kv = *reinterpret_cast<const v4*>(&K_s[t][4 * c4]);
+        *reinterpret_cast<v4*>(&K_s[t][4 * c4]) = kv * sc;
     }
-    // Four partial sums per row keep the dependent FMA chain short.
+    if (w == 0) {
+        const int b = lane >> 4, cc = lane & 15;
+        const float* Ab = A_s + (16 * b) * kTS + 16 * b;
+        float x[16];
 #pragma unroll
-    for (int t = 1; t < kChunk; ++t) {
-        float r[4] = {xr[t], 0.0f, 0.0f, 0.0f};
+        for (int r = 0; r < 16; ++r) {
+            float acc = r == cc ? 1.0f : 0.0f;
 #pragma unroll
-        for (int q4 = 0; q4 < t; q4 += 4) {
-            const v4 av = *reinterpret_cast<const v4*>(&A_s[t][q4]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (q4 + e < t) r[e] = fmaf(-av[e], xr[q4 + e], r[e]);
+            for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
+            x[r] = acc;
         }
-        xr[t] = (r[0] + r[1]) + (r[2] + r[3]);
-    }
-    __syncthreads();                           // K_s, A_s and M_s are free: W and U^T take their place
-    if (is_w) {
 #pragma unroll
-        for (int t = 0; t < kChunk; ++t) K_s[t][j] = xr[t];
+        for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
     } else {
-        // row j of U^T, 16 chunks of 4 tokens at chunk position e ^ (j & 15)
-#pragma unroll
-        for (int e = 0; e < kChunk / 4; ++e)
-            *reinterpret_cast<v4*>(U_s + j * kChunk + 4 * (e ^ (j & 15))) =
-                v4{xr[4 * e], xr[4 * e + 1], xr[4 * e + 2], xr[4 * e + 3]};
+        for (int e = tid - kWave; e < 6 * 256; e += 256 - kWave) {
+            const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
+            const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
+            T_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
+        }
     }
     __syncthreads();
-    // W as fragments (4 x 4 x 64 = 1024 units), U^T row by row (2048 16-byte chunks).
+    // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
+    // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
+#pragma unroll
+    for (int lev = 1; lev <= 3; ++lev) {
+        if (w < 4 - lev) {
+            const int j = w, i = w + lev;
+            v4 pc = {0.f, 0.f, 0.f, 0.f};
+            for (int k = j; k < i; ++k)
+                pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
+            float* Pw = P_s + w * 16 * 17;
+            put16(Pw, 17, pc, lane, 1.0f);
+            __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0): this wave's P stores done
+            const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
+            put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
+        }
+        __syncthreads();
+    }
+
+    // W = T (beta Gam K) and U = T (beta V): wave w takes columns 16 (2 w + nt) .. +15 of
+    // both, all four 16-row tiles; T[t][s] = 0 for s > t, so tile mt stops at k-step 4 mt + 3.
+    v4 wacc[4][2], uacc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) { wacc[mt][nt] = v4{0.f, 0.f, 0.f, 0.f}; uacc[mt][nt] = wacc[mt][nt]; }
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+        const int sr = 4 * ks + lg4;
+        const float bs = B_s[sr];
+        float bw[2], bu[2];
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+            bw[nt] = K_s[sr][16 * (2 * w + nt) + li];
+            bu[nt] = bs * vb[ks][nt];
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            if (ks > 4 * mt + 3) continue;                   // compile-time after unrolling
+            const float a = T_s[(16 * mt + li) * kTS + 4 * ks + lg4];
+#pragma unroll
+            for (int nt = 0; nt < 2; ++nt) {
+                wacc[mt][nt] = mfma4(a, bw[nt], wacc[mt][nt]);
+                uacc[mt][nt] = mfma4(a, bu[nt], uacc[mt][nt]);
+            }
+        }
+    }
+    // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
+    float* Ut = p.ws.Ut + ch * kD * kChunk;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+            *reinterpret_cast<v4*>(Ut + (size_t)(16 * (2 * w + nt) + li) * kChunk + 16 * mt + 4 * lg4) = uacc[mt][nt];
+    __syncthreads();                       // every wave is done reading K_s: W takes its place
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) K_s[16 * mt + 4 * lg4 + r][16 * (2 * w + nt) + li] = wacc[mt][nt][r];
+    __syncthreads();
+    // W as fragments (4 x 4 x 64 = 1024 units).
     uint16_t* Wf = p.ws.Wf + ch * kFragW;
     for (int u = tid; u < 4 * 4 * kWave; u += 256) {
         const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
@@ -523,11 +607,6 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
         store_frag(Wf, m, ks, 4, ln, x);
-    }
-    v4* Ut = reinterpret_cast<v4*>(p.ws.Ut + ch * kD * kChunk);
-    for (int u = tid; u < kD * kChunk / 4; u += 256) {
-        const int jj = u >> 4, e = u & 15;
-        Ut[u] = *reinterpret_cast<const v4*>(U_s + jj * kChunk + 4 * (e ^ (jj & 15)));
     }
 }
 
