@@ -192,87 +192,93 @@ __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGe
 
 // ---------------------------------------------------------------------------------------
 // prep: grid (NC, 2 h_k + h_v), 256 threads; workgroup = (chunk, one q, k or v head).
-// Thread (c = tid & 127, th = tid >> 7) owns channel c of the head for tokens 32 th .. 32 th
-// + 31 of the chunk: its history and all its inputs are loaded up front, then the conv runs
-// along the tokens. q and k rows are L2-normalised (one wave sum per token and wave, two
-// waves per token half).
+// Wave q owns tokens 16 q .. 16 q + 15 of the chunk and lane l channels 2 l, 2 l + 1 of the
+// head: every x access of a wave is one 256-byte row segment (bf16 pairs), every output
+// store 512 bytes (float pairs), and the L2 norm of a q or k row is one wave sum. The
+// history of the first token is loaded up front, then the conv runs along the tokens.
 // ---------------------------------------------------------------------------------------
-constexpr int kPrepTok = kChunk / 2;
+constexpr int kPrepTok = kChunk / 4;
 
 template <int DC>
 __global__ void __launch_bounds__(256) prep_kernel(const PrefillParams p) {
-    __shared__ float part[2][2][kPrepTok];          // [token half][wave of the half][token]
     ChunkGeo g;
     if (!chunk_geo(p, blockIdx.x, g)) return;
     const Layer& L = p.L;
     const int lo = p.ws.seq_lo[g.s];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int c = tid & (kD - 1), th = tid >> 7, wh = (tid >> 6) & 1;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wq = tid / kWave;
+    const int c2 = 2 * lane;                                               // first of two channels
     const int y = blockIdx.y;
     const int kind = y < L.h_k ? 0 : (y < 2 * L.h_k ? 1 : 2);           // q, k, v
     const int head = kind == 0 ? y : (kind == 1 ? y - L.h_k : y - 2 * L.h_k);
-    const int ch = kind == 0 ? q_channel(L, head, c) : (kind == 1 ? k_channel(L, head, c) : v_channel(L, head, c));
-    const int tb = kPrepTok * th;                                          // first token of this thread
-    const int n = min(max(g.len - tb, 0), kPrepTok);
+    const int ch = kind == 0 ? q_channel(L, head, c2) : (kind == 1 ? k_channel(L, head, c2) : v_channel(L, head, c2));
+    const int tb = kPrepTok * wq;                                          // first token of this wave
+    const int n = min(max(g.len - tb, 0), kPrepTok);                      // wave-uniform
 
-    // History of the first token (only threads that own tokens read it: positions before
-    // the sequence start come from its conv state, the others lie inside the sequence).
-    float hist[DC - 1];
+    if (kind == 2 && tid < g.len) {                                       // gates of the v head's tokens
+        const size_t ab = (size_t)(g.t0 + tid) * L.h_v + head;
+        p.ws.lg[(size_t)head * p.T + g.t0 + tid] = log_gate(L, head, bf16_to_f32(p.a[ab]));
+        p.ws.bt[(size_t)head * p.T + g.t0 + tid] = sigmoid_f(bf16_to_f32(p.b[ab]));
+    }
+    if (n == 0) return;
+
+    // History of the first token: positions before the sequence start come from its conv
+    // state ([C][dc-1] per sequence: channel ch's entries, then channel ch+1's).
+    float h0[DC - 1], h1[DC - 1];
 #pragma unroll
     for (int i = 0; i < DC - 1; ++i) {
         const int pos = g.pos0 + tb - (DC - 1) + i;
-        uint16_t u = 0;
-        if (n > 0)
-            u = pos >= 0 ? p.x[(size_t)(lo + pos) * L.C + ch]
-                         : p.conv_state[((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + pos];
-        hist[i] = bf16_to_f32(u);
-    }
-    uint16_t xs[kPrepTok];
-#pragma unroll
-    for (int t = 0; t < kPrepTok; ++t) xs[t] = t < n ? p.x[(size_t)(g.t0 + tb + t) * L.C + ch] : (uint16_t)0;
-    const uint16_t* wr = L.conv_w + (size_t)ch * DC;
-    float wv[DC];
-#pragma unroll
-    for (int i = 0; i < DC; ++i) wv[i] = bf16_to_f32(wr[i]);
-
-    float yv[kPrepTok];
-#pragma unroll
-    for (int t = 0; t < kPrepTok; ++t) {
-        const float xv = bf16_to_f32(xs[t]);
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < DC - 1; ++i) acc = fmaf(hist[i], wv[i], acc);
-        acc = fmaf(xv, wv[DC - 1], acc);
-        if (L.conv_act == IX_GDN_ACT_SILU) acc = acc * sigmoid_f(acc);
-        yv[t] = acc;
-#pragma unroll
-        for (int i = 0; i < DC - 2; ++i) hist[i] = hist[i + 1];
-        hist[DC - 2] = xv;
-    }
-
-    if (kind == 2) {
-        float* dst = p.ws.vv + ((size_t)head * p.T + g.t0 + tb) * kD + c;
-#pragma unroll
-        for (int t = 0; t < kPrepTok; ++t)
-            if (t < n) dst[(size_t)t * kD] = yv[t];
-        if (tid < g.len) {
-            const size_t ab = (size_t)(g.t0 + tid) * L.h_v + head;
-            p.ws.lg[(size_t)head * p.T + g.t0 + tid] = log_gate(L, head, bf16_to_f32(p.a[ab]));
-            p.ws.bt[(size_t)head * p.T + g.t0 + tid] = sigmoid_f(bf16_to_f32(p.b[ab]));
+        uint32_t u;
+        if (pos >= 0) {
+            u = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(lo + pos) * L.C + ch);
+        } else {
+            const uint16_t* cs = p.conv_state + ((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + pos;
+            u = (uint32_t)cs[0] | ((uint32_t)cs[DC - 1] << 16);
         }
-        return;
+        h0[i] = __uint_as_float(u << 16);
+        h1[i] = __uint_as_float(u & 0xffff0000u);
     }
-#pragma unroll
-    for (int t = 0; t < kPrepTok; ++t) {
-        const float r = wave_sum(yv[t] * yv[t]);
-        if (lane == 0) part[th][wh][t] = r;
-    }
-    __syncthreads();
-    const float scale = kind == 0 ? L.q_scale : 1.0f;
-    float* dst = (kind == 0 ? p.ws.qn : p.ws.kn) + ((size_t)head * p.T + g.t0 + tb) * kD + c;
+    uint32_t xs[kPrepTok];
 #pragma unroll
     for (int t = 0; t < kPrepTok; ++t)
-        if (t < n) dst[(size_t)t * kD] = yv[t] * (scale / sqrtf(part[th][0][t] + part[th][1][t] + L.l2_eps));
+        xs[t] = t < n ? *reinterpret_cast<const uint32_t*>(p.x + (size_t)(g.t0 + tb + t) * L.C + ch) : 0u;
+    float w0[DC], w1[DC];                                                  // conv_w is [C][dc]
+#pragma unroll
+    for (int i = 0; i < DC; ++i) {
+        w0[i] = bf16_to_f32(L.conv_w[(size_t)ch * DC + i]);
+        w1[i] = bf16_to_f32(L.conv_w[(size_t)(ch + 1) * DC + i]);
+    }
+
+    float y0[kPrepTok], y1[kPrepTok];
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t) {
+        const float x0 = __uint_as_float(xs[t] << 16), x1 = __uint_as_float(xs[t] & 0xffff0000u);
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DC - 1; ++i) { a0 = fmaf(h0[i], w0[i], a0); a1 = fmaf(h1[i], w1[i], a1); }
+        a0 = fmaf(x0, w0[DC - 1], a0);
+        a1 = fmaf(x1, w1[DC - 1], a1);
+        if (L.conv_act == IX_GDN_ACT_SILU) { a0 = a0 * sigmoid_f(a0); a1 = a1 * sigmoid_f(a1); }
+        y0[t] = a0;
+        y1[t] = a1;
+#pragma unroll
+        for (int i = 0; i < DC - 2; ++i) { h0[i] = h0[i + 1]; h1[i] = h1[i + 1]; }
+        h0[DC - 2] = x0;
+        h1[DC - 2] = x1;
+    }
+
+    float* dst = (kind == 0 ? p.ws.qn : kind == 1 ? p.ws.kn : p.ws.vv) + ((size_t)head * p.T + g.t0 + tb) * kD + c2;
+    if (kind == 2) {
+#pragma unroll
+        for (int t = 0; t < kPrepTok; ++t)
+            if (t < n) *reinterpret_cast<float2*>(dst + (size_t)t * kD) = float2{y0[t], y1[t]};
+        return;
+    }
+    const float scale = kind == 0 ? L.q_scale : 1.0f;
+#pragma unroll
+    for (int t = 0; t < kPrepTok; ++t) {
+        const float inv = scale / sqrtf(wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t])) + L.l2_eps);
+        if (t < n) *reinterpret_cast<float2*>(dst + (size_t)t * kD) = float2{y0[t] * inv, y1[t] * inv};
+    }
 }
 
 // ---------------------------------------------------------------------------------------
