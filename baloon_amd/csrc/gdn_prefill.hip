@@ -127,53 +127,70 @@ struct PrefillParams {
 // ---------------------------------------------------------------------------------------
 // plan: one workgroup of 1024 threads, block scans in tiles of 1024 sequences
 // ---------------------------------------------------------------------------------------
+// Inclusive scan (max or sum) over the workgroup: within each wave by shuffles, then over
+// the 16 wave totals by wave 0; two barriers.
 template <bool IsMax>
-__device__ int block_inclusive_scan(int v, int* sh) {
-    const int tid = threadIdx.x;
-    sh[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < kPlanThreads; off <<= 1) {
-        const int o = tid >= off ? sh[tid - off] : (IsMax ? INT_MIN : 0);
-        __syncthreads();
-        v = IsMax ? max(v, o) : v + o;
-        sh[tid] = v;
-        __syncthreads();
+__device__ int block_inclusive_scan(int v, int* wave_tot) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int o = __shfl_up(v, off, kWave);
+        if (lane >= off) v = IsMax ? max(v, o) : v + o;
     }
+    if (lane == kWave - 1) wave_tot[w] = v;
+    __syncthreads();
+    if (w == 0) {
+        int t = lane < kPlanThreads / kWave ? wave_tot[lane] : (IsMax ? INT_MIN : 0);
+#pragma unroll
+        for (int off = 1; off < kPlanThreads / kWave; off <<= 1) {
+            const int o = __shfl_up(t, off, kWave);
+            if (lane >= off) t = IsMax ? max(t, o) : t + o;
+        }
+        if (lane < kPlanThreads / kWave) wave_tot[lane] = t;          // inclusive totals
+    }
+    __syncthreads();
+    if (w > 0) v = IsMax ? max(v, wave_tot[w - 1]) : v + wave_tot[w - 1];
     return v;
 }
 
 __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const PrefillParams p) {
-    __shared__ int sh[kPlanThreads];
+    __shared__ int wave_tot[kPlanThreads / kWave];
     __shared__ int carry;
     const int tid = threadIdx.x, n = p.n_seq;
     // seq_lo[s] = clamp(max(cu[0..s]), 0, T), s = 0..n
-    if (tid == 0) carry = 0;
-    __syncthreads();
+    int run = 0;                                                       // carry, same in every thread
     for (int base = 0; base <= n; base += kPlanThreads) {
         const int s = base + tid;
         int v = s <= n ? min(max(p.cu[s], 0), p.T) : 0;
-        v = max(block_inclusive_scan<true>(v, sh), carry);
+        v = max(block_inclusive_scan<true>(v, wave_tot), run);
         if (s <= n) p.ws.seq_lo[s] = v;
-        __syncthreads();
         if (tid == kPlanThreads - 1) carry = v;
+        __syncthreads();
+        run = carry;
         __syncthreads();
     }
     // chunk_off = exclusive prefix sum of ceil(len / 64)
-    if (tid == 0) carry = 0;
-    __syncthreads();
+    run = 0;
     for (int base = 0; base <= n; base += kPlanThreads) {
         const int s = base + tid;
         const int cnt = s < n ? (p.ws.seq_lo[s + 1] - p.ws.seq_lo[s] + kChunk - 1) / kChunk : 0;
-        const int inc = block_inclusive_scan<false>(cnt, sh) + carry;
+        const int inc = block_inclusive_scan<false>(cnt, wave_tot) + run;
         if (s <= n) p.ws.chunk_off[s] = inc - cnt;
-        if (s < n)
-            for (int j = 0; j < cnt; ++j) {
-                p.ws.chunk_seq[inc - cnt + j] = s;
-                p.ws.chunk_t0[inc - cnt + j] = p.ws.seq_lo[s] + j * kChunk;
-            }
-        __syncthreads();
         if (tid == kPlanThreads - 1) carry = inc;
         __syncthreads();
+        run = carry;
+        __syncthreads();
+    }
+    // the chunk table: chunk c belongs to the last sequence s with chunk_off[s] <= c
+    const int nc = run;
+    for (int c = tid; c < nc; c += kPlanThreads) {
+        int lo = 0, hi = n - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (p.ws.chunk_off[mid] <= c) lo = mid; else hi = mid - 1;
+        }
+        p.ws.chunk_seq[c] = lo;
+        p.ws.chunk_t0[c] = p.ws.seq_lo[lo] + (c - p.ws.chunk_off[lo]) * kChunk;
     }
 }
 
