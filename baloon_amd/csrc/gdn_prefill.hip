@@ -24,14 +24,17 @@
 //   prep_kernel    per (chunk, head): conv (history from conv_state at sequence starts), L2
 //                  norm of q and k, log decay and beta; fp32 q, k, v into the workspace
 //   commit_kernel  per sequence and channel: the new rolling conv history
-//   chunk_kernel   per (chunk, v head): K K^T and Q K^T on fp32 MFMA (lower block triangle),
-//                  A, M, and W | U by forward substitution (one column per thread)
-//   chain_kernel   per (sequence, v head, 16-column state slice): walks the chunks in
-//                  order carrying the state slice in MFMA accumulators; D, O and S' on fp32
-//                  MFMA, state and output work on separate waves. Columns of the state are
-//                  independent, so 8 slices per head fill the GPU even for a single sequence.
-// The fp32 matrix cores (v_mfma_f32_16x16x4_f32) keep the chunked result within ~1e-6 of
-// the token-by-token recurrence in double.
+//   chunk_kernel   per (chunk, v head): K K^T and Q K^T on fp32 MFMA (lower block triangle)
+//                  -> A, M; T = (I + A)^-1 by a blocked MFMA inverse; W = T diag(beta Gam) K
+//                  and U = T diag(beta) V as MFMA GEMMs; the chain's operands W, M, K^T, Q
+//                  written as split-bf16 MFMA fragments
+//   chain_kernel   per (sequence, v head, 32-column state slice): walks the chunks in order
+//                  carrying the state slice in MFMA accumulators; D, O and S' on split-bf16
+//                  MFMA (three bf16 products per fp32 product), state and output work on
+//                  separate waves. Columns of the state are independent, so 4 slices per
+//                  head share a head's chain.
+// fp32 MFMA for the chunk-local algebra and split-bf16 MFMA for the chain keep the chunked
+// result within ~1e-5 (state) of the token-by-token recurrence in double.
 #include "gdn_common.h"
 
 namespace ixg {
