@@ -31,13 +31,23 @@ FLAGS = [
 ]
 
 
+# Per-file additions. The decode kernels' atomics are single-lane group counters whose
+# results are used only at the end of a workgroup; the atomic optimizer would expand each
+# into a wave scan that broadcasts the result right away, waiting out the atomic's round
+# trip (and every load in flight) in the middle of the state stream.
+FILE_FLAGS = {
+    "gdn_decode.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src: str) -> tuple[str, str]:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-Rpass-analysis=kernel-resource-usage",
+           "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")

@@ -206,6 +206,11 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
     const bool conv_thread = tid < 128 + kHalfCols / 2;
     ConvPair<DC> cp;
     if (conv_thread) conv_pair_load<DC>(p, bseq, ch, cp);
+    // The gate inputs too are loaded ahead of the state (by every thread, from one address:
+    // a conditional load would make its branch wait for it before the state loads go out),
+    // so that computing the gates does not wait for the state loads of the gate thread's wave.
+    const size_t ab = (size_t)bseq * L.h_v + h;
+    const uint16_t a_in = p.a[ab], b_in = p.b[ab];
 
     // State: wave w owns columns hf*64 + 16 w + 2 u + half, u = 0..7.
     v4f* tile = reinterpret_cast<v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
@@ -226,14 +231,18 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
         const float r = wave_sum(fmaf(y0, y0, y1 * y1));
         if (lane == 0) scal_s[w] = r;
     }
-    if (tid == kThreads - 1) gates(p, bseq, h, gb_s);
-    __syncthreads();
+    if (tid == kThreads - 1) {
+        gb_s[0] = expf(log_gate(L, h, bf16_to_f32(a_in)));
+        gb_s[1] = sigmoid_f(bf16_to_f32(b_in));
+    }
+    // Everything shared below is in LDS, and the conv history values were consumed above, so
+    // their loads are complete: an LDS-only barrier, which leaves the state loads in flight.
+    lds_barrier();
 
     // Every thread's reads of the q/k conv history are complete: count this workgroup in.
-    if (tid == 0) {
-        const int members = mapped_count(L, src) * 2;
-        last_s = atomicAdd(counters + (size_t)bseq * L.h_k + src, 1) == members - 1;
-    }
+    // The result is needed only after the column updates, so its round trip overlaps them.
+    int old = 0;
+    if (tid == 0) old = atomicAdd(counters + (size_t)bseq * L.h_k + src, 1);
     const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
     const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
     const float kq = wave_sum(fmaf(q_s[lane], k_s[lane], q_s[lane + kWave] * k_s[lane + kWave])) * inv_q * inv_k;
@@ -266,7 +275,8 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
         for (int u = 0; u < kPairsPerWave; ++u) column_store(s[u], tile + (size_t)(j0 + 2 * u) * (kD / 4), kr, dv[u], g);
     }
 
-    __syncthreads();
+    if (tid == 0) last_s = old == mapped_count(L, src) * 2 - 1;
+    lds_barrier();
     if (last_s) {
         if (tid < 128) hist_store<DC>(p, bseq, ch, nh);
         if (tid == 0) counters[(size_t)bseq * L.h_k + src] = 0;
