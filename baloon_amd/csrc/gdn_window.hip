@@ -74,26 +74,30 @@ struct WindowParams {
 
 // ---------------------------------------------------------------------------------------
 // verify: grid (2 h_v, B)
+// The per-token inputs (conv outputs, squared norms, gates) do not depend on the state, so
+// they are computed for all K tokens first, into LDS, while the state loads are in flight;
+// after one barrier the K column updates run back to back in registers. The arithmetic and
+// its order are those of the decode kernel, token by token.
 // ---------------------------------------------------------------------------------------
 template <int DC>
 __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowParams p) {
-    __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kHalf];
-    __shared__ float scal_s[2], gb_s[2];
+    __shared__ __align__(16) float q_s[kMaxWindow][kD], k_s[kMaxWindow][kD], v_s[kMaxWindow][kHalf];
+    __shared__ float sq_s[kMaxWindow], sk_s[kMaxWindow], g_s[kMaxWindow], b_s[kMaxWindow];
 
     const Layer& L = p.L;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int half = lane >> 5, i4 = lane & 31;
     const int hf = blockIdx.x & 1, h = blockIdx.x >> 1, bseq = blockIdx.y;
     const int src = src_of(L, h);
+    const int K = p.K;
     // One workgroup per q/k head records its normalised key.
     const bool rec_k = hf == 0 && h == mapped_head(L, src, 0);
 
     // Conv channel pair of this thread: 0..63 q, 64..127 k, 128..159 the half tile's v.
-    int ch = 0;
-    float* dst = nullptr;
-    if (tid < 64) { ch = q_channel(L, src, 2 * tid); dst = q_s + 2 * tid; }
-    else if (tid < 128) { ch = k_channel(L, src, 2 * (tid - 64)); dst = k_s + 2 * (tid - 64); }
-    else if (tid < 128 + kHalf / 2) { ch = v_channel(L, h, hf * kHalf + 2 * (tid - 128)); dst = v_s + 2 * (tid - 128); }
+    int ch = 0, col = 0;
+    if (tid < 64) { ch = q_channel(L, src, 2 * tid); col = 2 * tid; }
+    else if (tid < 128) { ch = k_channel(L, src, 2 * (tid - 64)); col = 2 * (tid - 64); }
+    else if (tid < 128 + kHalf / 2) { ch = v_channel(L, h, hf * kHalf + 2 * (tid - 128)); col = 2 * (tid - 128); }
     const bool conv_thread = tid < 128 + kHalf / 2;
     ConvPair<DC> cp;
     if (conv_thread) {
@@ -103,7 +107,7 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(L.conv_w + (size_t)ch * DC);
 #pragma unroll
         for (int i = 0; i < DC; ++i) cp.w[i] = wp[i];
-        cp.x = *reinterpret_cast<const uint32_t*>(p.x + (size_t)bseq * p.K * L.C + ch);
+        cp.x = *reinterpret_cast<const uint32_t*>(p.x + (size_t)bseq * K * L.C + ch);
     }
 
     const v4f* tile = reinterpret_cast<const v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
@@ -112,39 +116,50 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
 #pragma unroll
     for (int u = 0; u < kPairs; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
 
-    for (int t = 0; t < p.K; ++t) {
-        const size_t row = (size_t)bseq * p.K + t;
-        float y0 = 0.0f, y1 = 0.0f;
-        if (conv_thread) {
+    // Phase 1: conv outputs, squared norms (waves 0 and 1) and gates of every token.
+    if (conv_thread) {
+        float* dst = tid < 64 ? q_s[0] : tid < 128 ? k_s[0] : v_s[0];
+        const int stride = tid < 128 ? kD : kHalf;
+        for (int t = 0; t < K; ++t) {
+            const size_t row = (size_t)bseq * K + t;
+            float y0, y1;
             uint32_t nh[DC - 1];
             conv_pair_eval<DC>(L, cp, y0, y1, nh);
-            dst[0] = y0;
-            dst[1] = y1;
+            dst[t * stride + col] = y0;
+            dst[t * stride + col + 1] = y1;
 #pragma unroll
             for (int i = 0; i < DC - 1; ++i) cp.h[i] = nh[i];
-            if (t + 1 < p.K) cp.x = *reinterpret_cast<const uint32_t*>(p.x + (row + 1) * L.C + ch);
+            if (t + 1 < K) cp.x = *reinterpret_cast<const uint32_t*>(p.x + (row + 1) * L.C + ch);
+            if (w < 2) {                                       // wave-uniform: q (wave 0), k (wave 1)
+                const float r = wave_sum(fmaf(y0, y0, y1 * y1));
+                if (lane == 0) (w == 0 ? sq_s : sk_s)[t] = r;
+            }
         }
-        if (w < 2) {
-            const float r = wave_sum(fmaf(y0, y0, y1 * y1));
-            if (lane == 0) scal_s[w] = r;
+    }
+    if (tid >= kThreads - kMaxWindow) {                       // gates: one thread per token
+        const int t = tid - (kThreads - kMaxWindow);
+        if (t < K) {
+            const size_t ab = ((size_t)bseq * K + t) * L.h_v + h;
+            g_s[t] = expf(log_gate(L, h, bf16_to_f32(p.a[ab])));
+            b_s[t] = sigmoid_f(bf16_to_f32(p.b[ab]));
         }
-        if (tid == kThreads - 1) {
-            const size_t ab = row * L.h_v + h;
-            gb_s[0] = expf(log_gate(L, h, bf16_to_f32(p.a[ab])));
-            gb_s[1] = sigmoid_f(bf16_to_f32(p.b[ab]));
-        }
-        __syncthreads();
+    }
+    lds_barrier();
 
-        const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
-        const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
-        const float kq = wave_sum(fmaf(q_s[lane], k_s[lane], q_s[lane + kWave] * k_s[lane + kWave])) * inv_q * inv_k;
+    // Phase 2: the K tokens in order, the state slab in registers.
+    for (int t = 0; t < K; ++t) {
+        const size_t row = (size_t)bseq * K + t;
+        const float inv_q = L.q_scale / sqrtf(sq_s[t] + L.l2_eps);
+        const float inv_k = 1.0f / sqrtf(sk_s[t] + L.l2_eps);
+        const float kq =
+            wave_sum(fmaf(q_s[t][lane], k_s[t][lane], q_s[t][lane + kWave] * k_s[t][lane + kWave])) * inv_q * inv_k;
         v4f kr, qr;
         {
-            const v4f kk = *reinterpret_cast<const v4f*>(k_s + 4 * i4), qq = *reinterpret_cast<const v4f*>(q_s + 4 * i4);
+            const v4f kk = *reinterpret_cast<const v4f*>(&k_s[t][4 * i4]), qq = *reinterpret_cast<const v4f*>(&q_s[t][4 * i4]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) { kr[e] = kk[e] * inv_k; qr[e] = qq[e] * inv_q; }
         }
-        const float g = gb_s[0], bt = gb_s[1];
+        const float g = g_s[t], bt = b_s[t];
         const size_t ob = (row * L.h_v + h) * kD;
 #pragma unroll
         for (int u = 0; u < kPairs; ++u) {
@@ -154,7 +169,7 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
             for (int e = 1; e < 4; ++e) { ak = fmaf(s[u][e], kr[e], ak); aq = fmaf(s[u][e], qr[e], aq); }
             ak = half_sum(ak);
             aq = half_sum(aq);
-            const float d = (v_s[j - hf * kHalf] - g * ak) * bt;
+            const float d = (v_s[t][j - hf * kHalf] - g * ak) * bt;
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[u][e] = fmaf(kr[e], d, s[u][e] * g);
             if (i4 == 0) {
@@ -164,10 +179,9 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
             }
         }
         // The record of this token.
-        if (rec_k && tid < kD) p.rec.k[(row * L.h_k + src) * kD + tid] = k_s[tid] * inv_k;
-        if (tid < kHalf) p.rec.v[(row * L.h_v + h) * kD + hf * kHalf + tid] = v_s[tid];
+        if (rec_k && tid < kD) p.rec.k[(row * L.h_k + src) * kD + tid] = k_s[t][tid] * inv_k;
+        if (tid < kHalf) p.rec.v[(row * L.h_v + h) * kD + hf * kHalf + tid] = v_s[t][tid];
         if (hf == 0 && tid == 0) { p.rec.g[row * L.h_v + h] = g; p.rec.bt[row * L.h_v + h] = bt; }
-        __syncthreads();                          // q_s, k_s, v_s, scal_s, gb_s are rewritten next token
     }
 }
 
