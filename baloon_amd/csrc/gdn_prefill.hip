@@ -21,13 +21,13 @@
 // Kernels, in stream order:
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
 //                  the chunk table (sequence and first token of each chunk)
-//   prep_kernel    per (chunk, head): conv (history from conv_state at sequence starts), L2
-//                  norm of q and k, log decay and beta; fp32 q, k, v into the workspace
+//   chunk_kernel   per (chunk, q/k head): conv (history from conv_state at sequence starts),
+//                  L2 norms of q and k; K K^T and Q K^T on fp32 MFMA (lower block triangle),
+//                  once for all the v heads mapped to the q/k head; then per v head its
+//                  decay and beta, its v rows, A and M, T = (I + A)^-1 by a blocked MFMA
+//                  inverse, W = T diag(beta Gam) K and U = T diag(beta) V as MFMA GEMMs; the
+//                  chain's operands W, M, K^T, Q written as split-bf16 MFMA fragments
 //   commit_kernel  per sequence and channel: the new rolling conv history
-//   chunk_kernel   per (chunk, v head): K K^T and Q K^T on fp32 MFMA (lower block triangle)
-//                  -> A, M; T = (I + A)^-1 by a blocked MFMA inverse; W = T diag(beta Gam) K
-//                  and U = T diag(beta) V as MFMA GEMMs; the chain's operands W, M, K^T, Q
-//                  written as split-bf16 MFMA fragments
 //   chain_kernel   per (sequence, v head, 32-column state slice): walks the chunks in order
 //                  carrying the state slice in MFMA accumulators; D, O and S' on split-bf16
 //                  MFMA (three bf16 products per fp32 product), state and output work on
@@ -57,11 +57,6 @@ struct Ws {
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int32_t* chunk_seq;  // [NC]
     int32_t* chunk_t0;   // [NC]
-    float* qn;           // [h_k][T][128] normalised (and scaled) q
-    float* kn;           // [h_k][T][128] normalised k
-    float* vv;           // [h_v][T][128] conv output v
-    float* lg;           // [h_v][T] log decay
-    float* bt;           // [h_v][T] beta
     uint16_t* Wf;        // [NC][h_v] W (64 x 128) as split-bf16 A fragments
     float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
     uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
@@ -70,7 +65,7 @@ struct Ws {
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
     float* sink;         // [16][64] target of the chain's stores for rows past a sequence end
 };
-constexpr int kWsSections = 16;
+constexpr int kWsSections = 11;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -79,9 +74,6 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
     const size_t NC = (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq;
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * NC, sizeof(int32_t) * NC,
-        sizeof(float) * c->h_k * (size_t)T * kD, sizeof(float) * c->h_k * (size_t)T * kD,
-        sizeof(float) * c->h_v * (size_t)T * kD, sizeof(float) * c->h_v * (size_t)T,
-        sizeof(float) * c->h_v * (size_t)T,
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk,
         sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
@@ -98,18 +90,13 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
     w.chunk_seq = reinterpret_cast<int32_t*>(base + off[2]);
     w.chunk_t0 = reinterpret_cast<int32_t*>(base + off[3]);
-    w.qn = reinterpret_cast<float*>(base + off[4]);
-    w.kn = reinterpret_cast<float*>(base + off[5]);
-    w.vv = reinterpret_cast<float*>(base + off[6]);
-    w.lg = reinterpret_cast<float*>(base + off[7]);
-    w.bt = reinterpret_cast<float*>(base + off[8]);
-    w.Wf = reinterpret_cast<uint16_t*>(base + off[9]);
-    w.Ut = reinterpret_cast<float*>(base + off[10]);
-    w.Mf = reinterpret_cast<uint16_t*>(base + off[11]);
-    w.G = reinterpret_cast<float*>(base + off[12]);
-    w.Ktf = reinterpret_cast<uint16_t*>(base + off[13]);
-    w.Qf = reinterpret_cast<uint16_t*>(base + off[14]);
-    w.sink = reinterpret_cast<float*>(base + off[15]);
+    w.Wf = reinterpret_cast<uint16_t*>(base + off[4]);
+    w.Ut = reinterpret_cast<float*>(base + off[5]);
+    w.Mf = reinterpret_cast<uint16_t*>(base + off[6]);
+    w.G = reinterpret_cast<float*>(base + off[7]);
+    w.Ktf = reinterpret_cast<uint16_t*>(base + off[8]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
+    w.sink = reinterpret_cast<float*>(base + off[10]);
     return w;
 }
 
@@ -211,67 +198,73 @@ __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGe
 }
 
 // ---------------------------------------------------------------------------------------
-// prep: grid (NC, 2 h_k + h_v), 256 threads; workgroup = (chunk, one q, k or v head).
-// Wave q owns tokens 16 q .. 16 q + 15 of the chunk and lane l channels 2 l, 2 l + 1 of the
-// head: every x access of a wave is one 256-byte row segment (bf16 pairs), every output
-// store 512 bytes (float pairs), and the L2 norm of a q or k row is one wave sum. The
-// history of the first token is loaded up front, then the conv runs along the tokens.
+// Conv of 16 consecutive tokens of a chunk for the channel pair (ch, ch + 1), one pair per
+// lane, so that every x access of a wave is one 256-byte row segment. Tokens tb .. tb + n - 1
+// of the chunk (n wave-uniform, 1..16); the history of the first one comes from x or, before
+// the sequence start, from the sequence's conv state ([C][dc-1] per sequence: channel ch's
+// entries, then channel ch+1's). The loads and the arithmetic are separate steps, so that a
+// wave can issue the loads well before it needs the rows (and before stores it issues in
+// between, which its later waits would otherwise include).
 // ---------------------------------------------------------------------------------------
-constexpr int kPrepTok = kChunk / 4;
+constexpr int kConvTok = 16;
+
+// The loads are unconditional and nothing touches the loaded words before conv_run: a
+// load on one path only, or any use of a loaded value, makes the wave wait for every load
+// it has in flight.
+template <int DC>
+struct ConvIn {
+    uint32_t h0[DC - 1], h1[DC - 1];    // history of the first token (one bf16 each), oldest first
+    uint32_t xs[kConvTok];              // bf16 pairs: inputs of the tokens (rows past n repeat row n-1)
+    uint32_t w[DC];                     // bf16 pairs: conv weights of channel ch, then ch + 1
+};
 
 template <int DC>
-__global__ void __launch_bounds__(256) prep_kernel(const PrefillParams p) {
-    ChunkGeo g;
-    if (!chunk_geo(p, blockIdx.x, g)) return;
+__device__ __forceinline__ void conv_load(const PrefillParams& p, const ChunkGeo& g, int lo, int ch, int tb, int n,
+                                          ConvIn<DC>& in) {
     const Layer& L = p.L;
-    const int lo = p.ws.seq_lo[g.s];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1), wq = tid / kWave;
-    const int c2 = 2 * lane;                                               // first of two channels
-    const int y = blockIdx.y;
-    const int kind = y < L.h_k ? 0 : (y < 2 * L.h_k ? 1 : 2);           // q, k, v
-    const int head = kind == 0 ? y : (kind == 1 ? y - L.h_k : y - 2 * L.h_k);
-    const int ch = kind == 0 ? q_channel(L, head, c2) : (kind == 1 ? k_channel(L, head, c2) : v_channel(L, head, c2));
-    const int tb = kPrepTok * wq;                                          // first token of this wave
-    const int n = min(max(g.len - tb, 0), kPrepTok);                      // wave-uniform
-
-    if (kind == 2 && tid < g.len) {                                       // gates of the v head's tokens
-        const size_t ab = (size_t)(g.t0 + tid) * L.h_v + head;
-        p.ws.lg[(size_t)head * p.T + g.t0 + tid] = log_gate(L, head, bf16_to_f32(p.a[ab]));
-        p.ws.bt[(size_t)head * p.T + g.t0 + tid] = sigmoid_f(bf16_to_f32(p.b[ab]));
-    }
-    if (n == 0) return;
-
-    // History of the first token: positions before the sequence start come from its conv
-    // state ([C][dc-1] per sequence: channel ch's entries, then channel ch+1's).
-    float h0[DC - 1], h1[DC - 1];
 #pragma unroll
     for (int i = 0; i < DC - 1; ++i) {
-        const int pos = g.pos0 + tb - (DC - 1) + i;
-        uint32_t u;
-        if (pos >= 0) {
-            u = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(lo + pos) * L.C + ch);
-        } else {
-            const uint16_t* cs = p.conv_state + ((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + pos;
-            u = (uint32_t)cs[0] | ((uint32_t)cs[DC - 1] << 16);
-        }
-        h0[i] = __uint_as_float(u << 16);
-        h1[i] = __uint_as_float(u & 0xffff0000u);
+        const int pos = g.pos0 + tb - (DC - 1) + i;            // wave-uniform
+        const uint16_t* xp = p.x + (size_t)(lo + max(pos, 0)) * L.C + ch;
+        const uint16_t* sp = p.conv_state + ((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + min(pos, -1);
+        in.h0[i] = *(pos >= 0 ? xp : sp);
+        in.h1[i] = *(pos >= 0 ? xp + 1 : sp + (DC - 1));
     }
-    uint32_t xs[kPrepTok];
 #pragma unroll
-    for (int t = 0; t < kPrepTok; ++t)
-        xs[t] = t < n ? *reinterpret_cast<const uint32_t*>(p.x + (size_t)(g.t0 + tb + t) * L.C + ch) : 0u;
-    float w0[DC], w1[DC];                                                  // conv_w is [C][dc]
+    for (int t = 0; t < kConvTok; ++t)
+        in.xs[t] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(g.t0 + tb + min(t, n - 1)) * L.C + ch);
+    // conv_w is [C][dc]: the two channels' 2 dc weights are dc aligned words (ch is even)
+    const uint32_t* wp = reinterpret_cast<const uint32_t*>(L.conv_w + (size_t)ch * DC);
+#pragma unroll
+    for (int i = 0; i < DC; ++i) in.w[i] = wp[i];
+}
+
+__device__ __forceinline__ float bf16_half(uint32_t word, int half) {
+    return __uint_as_float(half ? (word & 0xffff0000u) : (word << 16));
+}
+
+template <int DC>
+__device__ __forceinline__ void conv_run(const Layer& L, ConvIn<DC> in, float (&y0)[kConvTok],
+                                         float (&y1)[kConvTok]) {
+    // Pin the words here: the compiler would otherwise hoist their unpacking up to the loads,
+    // which then wait for the data right after issue.
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) { __asm__ volatile("" : "+v"(in.h0[i])); __asm__ volatile("" : "+v"(in.h1[i])); }
+#pragma unroll
+    for (int t = 0; t < kConvTok; ++t) __asm__ volatile("" : "+v"(in.xs[t]));
+#pragma unroll
+    for (int i = 0; i < DC; ++i) __asm__ volatile("" : "+v"(in.w[i]));
+    float h0[DC - 1], h1[DC - 1], w0[DC], w1[DC];
+#pragma unroll
+    for (int i = 0; i < DC - 1; ++i) { h0[i] = __uint_as_float(in.h0[i] << 16); h1[i] = __uint_as_float(in.h1[i] << 16); }
 #pragma unroll
     for (int i = 0; i < DC; ++i) {
-        w0[i] = bf16_to_f32(L.conv_w[(size_t)ch * DC + i]);
-        w1[i] = bf16_to_f32(L.conv_w[(size_t)(ch + 1) * DC + i]);
+        w0[i] = bf16_half(in.w[i >> 1], i & 1);
+        w1[i] = bf16_half(in.w[(DC + i) >> 1], (DC + i) & 1);
     }
-
-    float y0[kPrepTok], y1[kPrepTok];
 #pragma unroll
-    for (int t = 0; t < kPrepTok; ++t) {
-        const float x0 = __uint_as_float(xs[t] << 16), x1 = __uint_as_float(xs[t] & 0xffff0000u);
+    for (int t = 0; t < kConvTok; ++t) {
+        const float x0 = bf16_half(in.xs[t], 0), x1 = bf16_half(in.xs[t], 1);
         float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < DC - 1; ++i) { a0 = fmaf(h0[i], w0[i], a0); a1 = fmaf(h1[i], w1[i], a1); }
@@ -284,20 +277,6 @@ __global__ void __launch_bounds__(256) prep_kernel(const PrefillParams p) {
         for (int i = 0; i < DC - 2; ++i) { h0[i] = h0[i + 1]; h1[i] = h1[i + 1]; }
         h0[DC - 2] = x0;
         h1[DC - 2] = x1;
-    }
-
-    float* dst = (kind == 0 ? p.ws.qn : kind == 1 ? p.ws.kn : p.ws.vv) + ((size_t)head * p.T + g.t0 + tb) * kD + c2;
-    if (kind == 2) {
-#pragma unroll
-        for (int t = 0; t < kPrepTok; ++t)
-            if (t < n) *reinterpret_cast<float2*>(dst + (size_t)t * kD) = float2{y0[t], y1[t]};
-        return;
-    }
-    const float scale = kind == 0 ? L.q_scale : 1.0f;
-#pragma unroll
-    for (int t = 0; t < kPrepTok; ++t) {
-        const float inv = scale / sqrtf(wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t])) + L.l2_eps);
-        if (t < n) *reinterpret_cast<float2*>(dst + (size_t)t * kD) = float2{y0[t] * inv, y1[t] * inv};
     }
 }
 
@@ -368,9 +347,13 @@ constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (M)
 constexpr size_t kFragKt = 8 * 2 * 2 * 512;    // 128 x 64 (K^T)
 
 // ---------------------------------------------------------------------------------------
-// chunk-local: grid (NC, h_v), 256 threads; workgroup = (chunk, v head)
+// chunk-local: grid (NC, h_k), 512 threads; workgroup = (chunk, q/k head) and, one after
+// the other, the v heads mapped to that q/k head
 // ---------------------------------------------------------------------------------------
-constexpr int kKS = kD + 4;          // padded LDS row stride of the K / W tile
+constexpr int kKS = kD + 4;          // padded LDS row stride of the K / Q / V tiles
+constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
+constexpr int kChunkThreads = 512;
+constexpr int kMaxMap = 16;          // v heads per q/k head (the configuration limit)
 
 // The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
 __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
@@ -392,123 +375,166 @@ __device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, f
     for (int r = 0; r < 4; ++r) z[(4 * (lane >> 4) + r) * zs + (lane & 15)] = scale * c[r];
 }
 
-// Phases (one workgroup):
-//   stage K | K K^T and Q K^T (fp32 MFMA) -> A, M in LDS | M (and, for the first v head of a
-//   q/k head, K^T and Q) as split fragments; K rows scaled by beta Gam | T = (I + A)^-1:
-//   the four 16 x 16 diagonal blocks by substitution (one wave), then the off-diagonal
-//   blocks T_ij = -T_ii sum_k A_ik T_kj in three dependency levels of fp32 MFMA block
-//   products | W = T diag(beta Gam) K and U = T diag(beta) V as fp32 MFMA GEMMs (the zero
-//   blocks of T skipped) | W through LDS into fragments, U^T stored from the MFMA layout.
-constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
-
-__global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
-    float (*K_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);                       // K, then W
-    float* A_s = lds + kChunk * kKS;                                                 // [64][kTS]
-    float* M_s = A_s + kChunk * kTS;                                                 // M, then T
-    float* T_s = M_s;
-    float* P_s = M_s + kChunk * kTS;                                                 // [3][16][17]
-    __shared__ float G_s[kChunk], B_s[kChunk];
-
-    ChunkGeo g;
-    const int c = blockIdx.x;
-    if (!chunk_geo(p, c, g)) return;
-    const Layer& L = p.L;
-    const int h = blockIdx.y, src = src_of(L, h);
-    const bool first_head = mapped_head(L, src, 0) == h;
-    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
-    const int li = lane & 15, lg4 = lane >> 4;
-    const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
-    const float* kbase = p.ws.kn + ((size_t)src * p.T + g.t0) * kD;
-    const float* qbase = p.ws.qn + ((size_t)src * p.T + g.t0) * kD;
-    const float* vbase = p.ws.vv + ((size_t)h * p.T + g.t0) * kD;
-
-    // Stage the K rows of the chunk (zero beyond its length); wave 0 also scans the decay.
-    for (int e = tid; e < kChunk * (kD / 4); e += 256) {
-        const int t = e / (kD / 4), c4 = e % (kD / 4);
-        v4 kv = {0.f, 0.f, 0.f, 0.f};
-        if (t < g.len) kv = *reinterpret_cast<const v4*>(kbase + (size_t)t * kD + 4 * c4);
-        *reinterpret_cast<v4*>(&K_s[t][4 * c4]) = kv;
-    }
-    if (w == 0) {
-        float lgt = lane < g.len ? p.ws.lg[(size_t)h * p.T + g.t0 + lane] : 0.0f;
+// A and M of one v head from the raw products of this wave's triangle blocks (waves 0-3):
+// A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s) for s < t, M[t][s] = exp(G_t - G_s) (q_t . k_s)
+// for s <= t, zero above the diagonal inside the diagonal blocks. The blocks above the
+// diagonal are never written (nothing reads them).
+__device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], const float* G, const float* Bt,
+                                        float* A_s, float* M_s, int w, int li, int lg4) {
 #pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {          // inclusive scan over the 64 lanes
-            const float o = __shfl_up(lgt, off, kWave);
-            if (lane >= off) lgt += o;
-        }
-        G_s[lane] = lgt;
-        B_s[lane] = lane < g.len ? p.ws.bt[(size_t)h * p.T + g.t0 + lane] : 0.0f;
-        p.ws.G[ch * kChunk + lane] = lgt;
-    }
-    // The U operand rows this lane needs later (beta V, tokens s = 4 ks + lg4, columns
-    // 16 (2 w + nt) + li), loaded now so that their latency overlaps the triangle.
-    float vb[16][2];
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-        const int sr = 4 * ks + lg4;
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-            vb[ks][nt] = sr < g.len ? vbase[(size_t)sr * kD + 16 * (2 * w + nt) + li] : 0.0f;
-    }
-    __syncthreads();
-
-    // K K^T and Q K^T on the lower block triangle -> A and M (LDS; upper blocks zero).
-    // MFMA k index of (block 4m + e, lane group g) is 16 m + 4 g + e for both operands.
-    for (int i = w; i < 10; i += 4) {
+    for (int j = 0; j < 3; ++j) {
+        const int i = w + 4 * j;
+        if (i >= 10) continue;
         int br, bc;
         tri_block(i, br, bc);
-        const int arow = 16 * br + li;
-        const bool qok = arow < g.len;
-        v4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-#pragma unroll
-        for (int m = 0; m < kD / 16; ++m) {
-            const v4 ak = *reinterpret_cast<const v4*>(&K_s[arow][16 * m + 4 * lg4]);
-            const v4 aq = qok ? *reinterpret_cast<const v4*>(qbase + (size_t)arow * kD + 16 * m + 4 * lg4)
-                              : v4{0.f, 0.f, 0.f, 0.f};
-            const v4 bk = *reinterpret_cast<const v4*>(&K_s[16 * bc + li][16 * m + 4 * lg4]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kk = mfma4(ak[e], bk[e], kk);
-                qk = mfma4(aq[e], bk[e], qk);
-            }
-        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = 16 * br + 4 * lg4 + r, s = 16 * bc + li;
             float av = 0.0f, mv = 0.0f;
             if (s <= t) {
-                const float e = expf(G_s[t] - G_s[s]);
-                mv = e * qk[r];
-                if (s < t) av = B_s[t] * e * kk[r];
+                const float e = expf(G[t] - G[s]);
+                mv = e * qk[j][r];
+                if (s < t) av = Bt[t] * e * kk[j][r];
             }
             A_s[t * kTS + s] = av;
             M_s[t * kTS + s] = mv;
         }
     }
-    for (int e = tid; e < 6 * 256; e += 256) {
-        const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
-        const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
-        A_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
-        M_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
-    }
-    __syncthreads();
+}
 
-    // M as fragments (4 x 2 fragments x 64 lanes: 512 units, 2 per thread).
-    uint16_t* Mf = p.ws.Mf + ch * kFragM;
-    for (int u = tid; u < 4 * 2 * kWave; u += 256) {
-        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
-        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
-        float x[8];
+// Phases (one workgroup, 8 waves; every barrier orders LDS only, so no wave ever waits for
+// its own global stores):
+//   gate inputs of the v heads | q and k rows of the chunk: conv, L2 norm, q scale, into LDS
+//   (zero past the chunk end) | decay scan and beta of each v head | raw K K^T and Q K^T of
+//   the lower block triangle on fp32 MFMA, kept in registers, while the other waves write
+//   K^T and Q as split fragments | then, per mapped v head: M as fragments | T = (I + A)^-1:
+//   the four 16 x 16 diagonal blocks by substitution (one wave, while four others compute
+//   the next head's v rows), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj in
+//   three dependency levels of fp32 MFMA block products | W = T diag(beta Gam) K and
+//   U = T diag(beta) V as fp32 MFMA GEMMs (the zero blocks of T skipped) | U^T stored from
+//   the MFMA layout, W through LDS into fragments | A and M of the next head.
+// The v rows of even and odd heads alternate between two tiles (the odd one is the q tile,
+// free once the triangle and the Q fragments are done).
+template <int DC>
+__global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParams p) {
+    __shared__ __align__(16) float lds[3 * kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
+    float (*K_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);         // k rows
+    float (*Q_s)[kKS] = K_s + kChunk;                                  // q rows, then v rows of odd heads
+    float (*V_s)[kKS] = Q_s + kChunk;                                  // v rows of even heads
+    float* A_s = lds + 3 * kChunk * kKS;                               // [64][kTS]
+    float* M_s = A_s + kChunk * kTS;                                   // M, then T
+    float* T_s = M_s;
+    float (*W_s)[kKS] = reinterpret_cast<float (*)[kKS]>(A_s);        // W, over A and T
+    float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
+    static_assert(kChunk * kKS <= 2 * kChunk * kTS, "W fits over A and T");
+    __shared__ float G_s[kMaxMap][kChunk], B_s[kMaxMap][kChunk], BG_s[kMaxMap][kChunk];
+
+    ChunkGeo g;
+    const int c = blockIdx.x;
+    if (!chunk_geo(p, c, g)) return;
+    const Layer& L = p.L;
+    const int src = blockIdx.y, nmap = mapped_count(L, src);
+    if (nmap == 0) return;
+    const int lo = p.ws.seq_lo[g.s];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);        // wave-uniform: scalar branches
+    const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
+    const size_t cs = (size_t)c * L.h_k + src;
+    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);   // this wave's conv rows
+
+    // Gate inputs of v heads w and w + 8 (lane = token), issued first.
+    uint16_t ra[2] = {0, 0}, rb[2] = {0, 0};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = M_s[row * kTS + k0 + e];
-        store_frag(Mf, m, ks, 2, ln, x);
+    for (int j = 0; j < 2; ++j) {
+        const int hh = w + 8 * j;
+        if (hh < nmap && lane < g.len) {
+            const size_t ab = (size_t)(g.t0 + lane) * L.h_v + mapped_head(L, src, hh);
+            ra[j] = p.a[ab];
+            rb[j] = p.b[ab];
+        }
     }
-    // K^T and Q of the q/k head, once per (chunk, q/k head). K^T (rows i, k = token t):
-    // 8 x 2 fragments; Q (rows t, k = i): 4 x 4 fragments, zero rows past the chunk end.
-    if (first_head) {
+
+    // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave.
+    {
+        const bool isk = w >= 4;
+        float y0[kConvTok], y1[kConvTok];
+        if (nt > 0) {
+            ConvIn<DC> in;
+            conv_load<DC>(p, g, lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
+            conv_run<DC>(L, in, y0, y1);
+        } else {
+#pragma unroll
+            for (int t = 0; t < kConvTok; ++t) y0[t] = y1[t] = 0.0f;
+        }
+        // All 16 row sums first (independent, so their shuffle latencies overlap), then the
+        // scaled rows; rows past the chunk end are zero.
+        float ss[kConvTok];
+#pragma unroll
+        for (int t = 0; t < kConvTok; ++t) ss[t] = wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t]));
+        const float scale = isk ? 1.0f : L.q_scale;
+        float (*dst)[kKS] = isk ? K_s : Q_s;
+#pragma unroll
+        for (int t = 0; t < kConvTok; ++t) {
+            const float inv = scale / sqrtf(ss[t] + L.l2_eps);
+            *reinterpret_cast<float2*>(&dst[tb + t][c2]) = t < nt ? float2{y0[t] * inv, y1[t] * inv} : float2{0.0f, 0.0f};
+        }
+    }
+    // Decay scan and beta of v heads w and w + 8.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int hh = w + 8 * j;
+        if (hh >= nmap) continue;
+        const int h = mapped_head(L, src, hh);
+        const bool ok = lane < g.len;
+        float lgt = ok ? log_gate(L, h, bf16_to_f32(ra[j])) : 0.0f;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {          // inclusive scan over the 64 lanes
+            const float o = __shfl_up(lgt, off, kWave);
+            if (lane >= off) lgt += o;
+        }
+        const float bt = ok ? sigmoid_f(bf16_to_f32(rb[j])) : 0.0f;
+        G_s[hh][lane] = lgt;
+        B_s[hh][lane] = bt;
+        BG_s[hh][lane] = bt * expf(lgt);
+        p.ws.G[((size_t)c * L.h_v + h) * kChunk + lane] = lgt;
+    }
+    lds_barrier();
+
+    // Raw K K^T and Q K^T (waves 0-3). MFMA k index of (block 4m + e, lane group g) is
+    // 16 m + 4 g + e for both operands. Waves 4-7 first issue the loads of the first v head's
+    // rows, then write K^T (rows i, k = token t: 8 x 2 fragments) and Q (rows t, k = i:
+    // 4 x 4 fragments) as split fragments.
+    v4 kk[3], qk[3];
+    ConvIn<DC> vin;
+    if (w < 4) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int i = w + 4 * j;
+            kk[j] = v4{0.f, 0.f, 0.f, 0.f};
+            qk[j] = kk[j];
+            if (i < 10) {
+                int br, bc;
+                tri_block(i, br, bc);
+                const int arow = 16 * br + li;
+#pragma unroll
+                for (int m = 0; m < kD / 16; ++m) {
+                    const v4 ak = *reinterpret_cast<const v4*>(&K_s[arow][16 * m + 4 * lg4]);
+                    const v4 aq = *reinterpret_cast<const v4*>(&Q_s[arow][16 * m + 4 * lg4]);
+                    const v4 bk = *reinterpret_cast<const v4*>(&K_s[16 * bc + li][16 * m + 4 * lg4]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        kk[j] = mfma4(ak[e], bk[e], kk[j]);
+                        qk[j] = mfma4(aq[e], bk[e], qk[j]);
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);       // one block's operands live at a time
+        }
+    } else {
+        if (nt > 0) conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, 0), c2), tb, nt, vin);
+        const int t4 = tid - 4 * kWave;
         uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
-        for (int u = tid; u < 8 * 2 * kWave; u += 256) {
+        for (int u = t4; u < 8 * 2 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
             const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
             float x[8];
@@ -517,122 +543,145 @@ __global__ void __launch_bounds__(256) chunk_kernel(const PrefillParams p) {
             store_frag(Ktf, m, ks, 2, ln, x);
         }
         uint16_t* Qf = p.ws.Qf + cs * kFragW;
-        for (int u = tid; u < 4 * 4 * kWave; u += 256) {
+        for (int u = t4; u < 4 * 4 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
             const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
-            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (row < g.len) {
-                const v4 a = *reinterpret_cast<const v4*>(qbase + (size_t)row * kD + k0);
-                const v4 b = *reinterpret_cast<const v4*>(qbase + (size_t)row * kD + k0 + 4);
+            float x[8];
+            const v4 a = *reinterpret_cast<const v4*>(&Q_s[row][k0]), b = *reinterpret_cast<const v4*>(&Q_s[row][k0 + 4]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
-            }
+            for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
             store_frag(Qf, m, ks, 4, ln, x);
         }
     }
-    __syncthreads();                       // M_s and the raw K_s are no longer read
+    lds_barrier();
 
-    // Scale the K rows by beta Gam (the W right-hand side); wave 0 inverts the four unit
-    // lower-triangular diagonal blocks of I + A (lane = 16 b + column c), the other waves
-    // clear the upper blocks of T.
-    for (int e = tid; e < kChunk * (kD / 4); e += 256) {
-        const int t = e / (kD / 4), c4 = e % (kD / 4);
-        const float sc = B_s[t] * expf(G_s[t]);
-        v4 kv = *reinterpret_cast<const v4*>(&K_s[t][4 * c4]);
-        *reinterpret_cast<v4*>(&K_s[t][4 * c4]) = kv * sc;
-    }
-    if (w == 0) {
-        const int b = lane >> 4, cc = lane & 15;
-        const float* Ab = A_s + (16 * b) * kTS + 16 * b;
-        float x[16];
+    // v rows of the first head (waves 4-7); A and M of the first head (waves 0-3).
+    if (w >= 4) {
+        float y0[kConvTok], y1[kConvTok];
+        if (nt > 0) conv_run<DC>(L, vin, y0, y1);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float acc = r == cc ? 1.0f : 0.0f;
-#pragma unroll
-            for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
-            x[r] = acc;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
+        for (int t = 0; t < kConvTok; ++t)
+            *reinterpret_cast<float2*>(&V_s[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
     } else {
-        for (int e = tid - kWave; e < 6 * 256; e += 256 - kWave) {
-            const int i = e >> 8, r = (e >> 4) & 15, col = e & 15;
-            const int br = i < 3 ? 0 : (i < 5 ? 1 : 2), bc = i < 3 ? i + 1 : (i < 5 ? i - 1 : 3);
-            T_s[(16 * br + r) * kTS + 16 * bc + col] = 0.0f;
-        }
+        am_head(kk, qk, G_s[0], B_s[0], A_s, M_s, w, li, lg4);
     }
-    __syncthreads();
-    // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
-    // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
-#pragma unroll
-    for (int lev = 1; lev <= 3; ++lev) {
-        if (w < 4 - lev) {
-            const int j = w, i = w + lev;
-            v4 pc = {0.f, 0.f, 0.f, 0.f};
-            for (int k = j; k < i; ++k)
-                pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
-            float* Pw = P_s + w * 16 * 17;
-            put16(Pw, 17, pc, lane, 1.0f);
-            __builtin_amdgcn_s_waitcnt(0xC07F);              // lgkmcnt(0): this wave's P stores done
-            const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
-            put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
-        }
-        __syncthreads();
-    }
+    lds_barrier();
 
-    // W = T (beta Gam K) and U = T (beta V): wave w takes columns 16 (2 w + nt) .. +15 of
-    // both, all four 16-row tiles; T[t][s] = 0 for s > t, so tile mt stops at k-step 4 mt + 3.
-    v4 wacc[4][2], uacc[4][2];
+    for (int mi = 0; mi < nmap; ++mi) {
+        const int h = mapped_head(L, src, mi);
+        const size_t ch = (size_t)c * L.h_v + h;
+        float (*Vb)[kKS] = (mi & 1) ? Q_s : V_s;                        // this head's v rows
+        float (*Vn)[kKS] = (mi & 1) ? V_s : Q_s;                        // the next head's
+        const bool next = mi + 1 < nmap, conv_next = w >= 4 && next && nt > 0;
+        ConvIn<DC> nin;                    // the next head's conv inputs (waves 4-7)
+        if (conv_next) conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, mi + 1), c2), tb, nt, nin);
+
+        // M as fragments (4 x 2 fragments x 64 lanes: one unit per thread); the blocks
+        // above the diagonal are zero.
+        {
+            uint16_t* Mf = p.ws.Mf + ch * kFragM;
+            const int m = w >> 1, ks = w & 1;
+            const int row = 16 * m + li, k0 = 32 * ks + 8 * lg4;
+            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (k0 < 16 * (m + 1)) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) { wacc[mt][nt] = v4{0.f, 0.f, 0.f, 0.f}; uacc[mt][nt] = wacc[mt][nt]; }
-#pragma unroll
-    for (int ks = 0; ks < 16; ++ks) {
-        const int sr = 4 * ks + lg4;
-        const float bs = B_s[sr];
-        float bw[2], bu[2];
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-            bw[nt] = K_s[sr][16 * (2 * w + nt) + li];
-            bu[nt] = bs * vb[ks][nt];
-        }
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            if (ks > 4 * mt + 3) continue;                   // compile-time after unrolling
-            const float a = T_s[(16 * mt + li) * kTS + 4 * ks + lg4];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
-                wacc[mt][nt] = mfma4(a, bw[nt], wacc[mt][nt]);
-                uacc[mt][nt] = mfma4(a, bu[nt], uacc[mt][nt]);
+                for (int e = 0; e < 8; ++e) x[e] = M_s[row * kTS + k0 + e];
             }
+            store_frag(Mf, m, ks, 2, lane, x);
         }
-    }
-    // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
-    float* Ut = p.ws.Ut + ch * kD * kChunk;
+        lds_barrier();                     // M_s is read: T takes its place
+
+        // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane =
+        // 16 b + column c); waves 4-7 compute the next head's v rows.
+        if (w == 0) {
+            const int b = lane >> 4, cc = lane & 15;
+            const float* Ab = A_s + (16 * b) * kTS + 16 * b;
+            float x[16];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+            for (int r = 0; r < 16; ++r) {
+                float acc = r == cc ? 1.0f : 0.0f;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-            *reinterpret_cast<v4*>(Ut + (size_t)(16 * (2 * w + nt) + li) * kChunk + 16 * mt + 4 * lg4) = uacc[mt][nt];
-    __syncthreads();                       // every wave is done reading K_s: W takes its place
+                for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
+                x[r] = acc;
+                if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // loads hoisted 4 rows ahead at most
+            }
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+            for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
+        } else if (w >= 4 && next) {
+            float y0[kConvTok], y1[kConvTok];
+            if (conv_next) conv_run<DC>(L, nin, y0, y1);
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+            for (int t = 0; t < kConvTok; ++t)
+                *reinterpret_cast<float2*>(&Vn[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
+        }
+        lds_barrier();
+        // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
+        // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
 #pragma unroll
-            for (int r = 0; r < 4; ++r) K_s[16 * mt + 4 * lg4 + r][16 * (2 * w + nt) + li] = wacc[mt][nt][r];
-    __syncthreads();
-    // W as fragments (4 x 4 x 64 = 1024 units).
-    uint16_t* Wf = p.ws.Wf + ch * kFragW;
-    for (int u = tid; u < 4 * 4 * kWave; u += 256) {
-        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
-        float x[8];
-        const v4 a = *reinterpret_cast<const v4*>(&K_s[row][k0]), b = *reinterpret_cast<const v4*>(&K_s[row][k0 + 4]);
+        for (int lev = 1; lev <= 3; ++lev) {
+            if (w < 4 - lev) {
+                const int j = w, i = w + lev;
+                v4 pc = {0.f, 0.f, 0.f, 0.f};
+                for (int k = j; k < i; ++k)
+                    pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
+                float* Pw = P_s + w * 16 * 17;
+                put16(Pw, 17, pc, lane, 1.0f);
+                __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's P stores done
+                const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
+                put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
+            }
+            lds_barrier();
+        }
+
+        // W = T (beta Gam K) and U = T (beta V): wave w takes columns 16 w .. 16 w + 15 of
+        // both, all four 16-row tiles; T[t][s] = 0 for s > t, so tile mt stops at k-step
+        // 4 mt + 3.
+        v4 wacc[4], uacc[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
-        store_frag(Wf, m, ks, 4, ln, x);
+        for (int mt = 0; mt < 4; ++mt) { wacc[mt] = v4{0.f, 0.f, 0.f, 0.f}; uacc[mt] = wacc[mt]; }
+        const int col = 16 * w + li;
+#pragma unroll
+        for (int ks = 0; ks < 16; ++ks) {
+            const int sr = 4 * ks + lg4;
+            const float bw = K_s[sr][col] * BG_s[mi][sr], bu = B_s[mi][sr] * Vb[sr][col];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) {
+                if (ks > 4 * mt + 3) continue;               // compile-time after unrolling
+                const float a = T_s[(16 * mt + li) * kTS + 4 * ks + lg4];
+                wacc[mt] = mfma4(a, bw, wacc[mt]);
+                uacc[mt] = mfma4(a, bu, uacc[mt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);           // bounds the loads hoisted ahead
+        }
+        // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
+        float* Ut = p.ws.Ut + ch * kD * kChunk;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+        lds_barrier();                     // A and T are read: W takes their place
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) W_s[16 * mt + 4 * lg4 + r][col] = wacc[mt][r];
+        lds_barrier();
+        // W as fragments (4 x 4 x 64 = 1024 units, two per thread).
+        uint16_t* Wf = p.ws.Wf + ch * kFragW;
+#pragma unroll
+        for (int rep = 0; rep < 2; ++rep) {
+            const int u = tid + rep * kChunkThreads;
+            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            float x[8];
+            const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
+            store_frag(Wf, m, ks, 4, ln, x);
+        }
+        if (next) {
+            lds_barrier();                 // W is read: the next head's A and M take its place
+            if (w < 4) am_head(kk, qk, G_s[mi + 1], B_s[mi + 1], A_s, M_s, w, li, lg4);
+            lds_barrier();
+        }
     }
 }
 
@@ -1053,15 +1102,15 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const dim3 pgrid((unsigned)NC, (unsigned)(2 * cfg->h_k + cfg->h_v));
+    const dim3 kgrid((unsigned)NC, (unsigned)cfg->h_k);
     switch (cfg->d_conv) {
-        case 2: hipLaunchKernelGGL(prep_kernel<2>, pgrid, dim3(256), 0, s, p); break;
-        case 3: hipLaunchKernelGGL(prep_kernel<3>, pgrid, dim3(256), 0, s, p); break;
-        default: hipLaunchKernelGGL(prep_kernel<4>, pgrid, dim3(256), 0, s, p); break;
+        case 2: hipLaunchKernelGGL(chunk_kernel<2>, kgrid, dim3(kChunkThreads), 0, s, p); break;
+        case 3: hipLaunchKernelGGL(chunk_kernel<3>, kgrid, dim3(kChunkThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL(chunk_kernel<4>, kgrid, dim3(kChunkThreads), 0, s, p); break;
     }
+    // after the chunk kernel, which reads the old history at sequence starts
     const size_t nch = (size_t)n_seq * p.L.C;
     hipLaunchKernelGGL(commit_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, s, p);
-    hipLaunchKernelGGL(chunk_kernel, dim3((unsigned)NC, (unsigned)cfg->h_v), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kSlices));
     switch ((p.o ? 1 : 0) | (p.o_bf16 ? 2 : 0)) {
