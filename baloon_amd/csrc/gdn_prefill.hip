@@ -24,15 +24,15 @@
 //   chunk_kernel   per (chunk, q/k head): conv (history from conv_state at sequence starts),
 //                  L2 norms of q and k; K K^T and Q K^T on fp32 MFMA (lower block triangle),
 //                  once for all the v heads mapped to the q/k head; then per v head its
-//                  decay and beta, its v rows, A and M, T = (I + A)^-1 by a blocked MFMA
-//                  inverse, W = T diag(beta Gam) K and U = T diag(beta) V as MFMA GEMMs; the
-//                  chain's operands W, M, K^T, Q written as split-bf16 MFMA fragments
+//                  decay factors and beta, its v rows, A and M, T = (I + A)^-1 by a blocked
+//                  MFMA inverse, W = T diag(beta Gam) K and U = T diag(beta) V as MFMA GEMMs;
+//                  the chain's operands W, M, K^T, Q written as split-bf16 MFMA fragments
 //   commit_kernel  per sequence and channel: the new rolling conv history
-//   chain_kernel   per (sequence, v head, 32-column state slice): walks the chunks in order
-//                  carrying the state slice in MFMA accumulators; D, O and S' on split-bf16
-//                  MFMA (three bf16 products per fp32 product), state and output work on
-//                  separate waves. Columns of the state are independent, so 4 slices per
-//                  head share a head's chain.
+//   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
+//                  One wave carries the strip in MFMA accumulators (D and S' on split-bf16
+//                  MFMA, three bf16 products per fp32 product) with no barrier on its data
+//                  path; four waves compute the outputs from the S and D it hands over; one
+//                  wave copies the next chunk's W and K^T into LDS with direct loads.
 // fp32 MFMA for the chunk-local algebra and split-bf16 MFMA for the chain keep the chunked
 // result within ~1e-5 (state) of the token-by-token recurrence in double.
 #include "gdn_common.h"
@@ -60,12 +60,12 @@ struct Ws {
     uint16_t* Wf;        // [NC][h_v] W (64 x 128) as split-bf16 A fragments
     float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
     uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
-    float* G;            // [NC][h_v][64] cumulative log decay (padded rows repeat the last)
+    float* G;            // [NC][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
+                         // inclusive cumulative log decay G (padded rows repeat the last)
     uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
-    float* sink;         // [16][64] target of the chain's stores for rows past a sequence end
 };
-constexpr int kWsSections = 11;
+constexpr int kWsSections = 10;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -75,9 +75,8 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * NC, sizeof(int32_t) * NC,
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
-        sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk,
+        sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * 2 * kChunk,
         sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
-        sizeof(float) * 16 * kWave,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -96,7 +95,6 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.G = reinterpret_cast<float*>(base + off[7]);
     w.Ktf = reinterpret_cast<uint16_t*>(base + off[8]);
     w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
-    w.sink = reinterpret_cast<float*>(base + off[10]);
     return w;
 }
 
@@ -314,24 +312,36 @@ __global__ void __launch_bounds__(256) commit_kernel(const PrefillParams p) {
 // accumulators (relative error ~2^-16, against 2^-8 for one bf16 product). The chunk kernel
 // writes the chain's A operands already split, in the instruction's A layout: fragment
 // (m, ks) of a (rows x k) tile covers rows 16m..16m+15 and k = 32ks..32ks+31, and lane l of
-// it holds row 16m + l%16, k = 32ks + 8(l/16) .. +7 as 8 bf16 (16 bytes). Stored
-// [m][ks][plane hi, lo][lane][8]: one coalesced 16-byte load per lane per fragment and plane.
+// it holds row 16m + l%16 at the 8 k indices 32ks + kperm(l/16, e), e = 0..7, as 8 bf16
+// (16 bytes). Stored [m][ks][plane hi, lo][lane][8]: one coalesced 16-byte load per lane
+// per fragment and plane.
+// kperm is the row order of two stacked MFMA accumulator tiles (lane group g holds rows
+// 4g..4g+3 of each), so the chain feeds its accumulators (S, D) to the next product as B
+// operands without moving them between lanes; A and B agree on the order of the k sum.
 // ---------------------------------------------------------------------------------------
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
 
 __device__ __forceinline__ size_t frag_at(int m, int ks, int nks, int plane, int lane) {
     return ((((size_t)m * nks + ks) * 2 + plane) * kWave + lane) * 8;       // in bf16 elements
 }
 
+// Split two fp32 values into packed bf16 pairs: hi = RNE(x), lo = RNE(x - hi). The hi values
+// return to fp32 by a shift and a mask, so a pair costs one convert per plane.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16x2(x0, x1);
+    lo = pack_bf16x2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+}
+
 // Split 8 fp32 values into hi and lo bf16 vectors.
 __device__ __forceinline__ void split8(const float (&x)[8], bf8& hi, bf8& lo) {
+    uint32_t h[4], l[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        const __bf16 h = (__bf16)x[e];
-        hi[e] = h;
-        lo[e] = (__bf16)(x[e] - (float)h);
-    }
+    for (int i = 0; i < 4; ++i) split2(x[2 * i], x[2 * i + 1], h[i], l[i]);
+    hi = __builtin_bit_cast(bf8, u4x{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(bf8, u4x{l[0], l[1], l[2], l[3]});
 }
 
 __device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nks, int lane, const float (&x)[8]) {
@@ -496,7 +506,10 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         G_s[hh][lane] = lgt;
         B_s[hh][lane] = bt;
         BG_s[hh][lane] = bt * expf(lgt);
-        p.ws.G[((size_t)c * L.h_v + h) * kChunk + lane] = lgt;
+        const float glast = __shfl(lgt, kChunk - 1, kWave);
+        float* E = p.ws.G + ((size_t)c * L.h_v + h) * 2 * kChunk;
+        E[lane] = expf(glast - lgt);
+        E[kChunk + lane] = expf(lgt);
     }
     lds_barrier();
 
@@ -536,18 +549,18 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
         for (int u = t4; u < 8 * 2 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
-            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            const int row = 16 * m + (ln & 15);
             float x[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = K_s[k0 + e][row];
+            for (int e = 0; e < 8; ++e) x[e] = K_s[32 * ks + kperm(ln >> 4, e)][row];
             store_frag(Ktf, m, ks, 2, ln, x);
         }
         uint16_t* Qf = p.ws.Qf + cs * kFragW;
         for (int u = t4; u < 4 * 4 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
             float x[8];
-            const v4 a = *reinterpret_cast<const v4*>(&Q_s[row][k0]), b = *reinterpret_cast<const v4*>(&Q_s[row][k0 + 4]);
+            const v4 a = *reinterpret_cast<const v4*>(&Q_s[row][k0]), b = *reinterpret_cast<const v4*>(&Q_s[row][k0 + 16]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
             store_frag(Qf, m, ks, 4, ln, x);
@@ -581,11 +594,13 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         {
             uint16_t* Mf = p.ws.Mf + ch * kFragM;
             const int m = w >> 1, ks = w & 1;
-            const int row = 16 * m + li, k0 = 32 * ks + 8 * lg4;
+            const int row = 16 * m + li, k0 = 32 * ks + 4 * lg4;            // kperm halves
             float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (k0 < 16 * (m + 1)) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = M_s[row * kTS + k0 + e];
+            for (int hb = 0; hb < 2; ++hb) {                              // 16-column block 2 ks + hb
+                if (2 * ks + hb > m) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) x[4 * hb + e] = M_s[row * kTS + k0 + 16 * hb + e];
             }
             store_frag(Mf, m, ks, 2, lane, x);
         }
@@ -670,9 +685,9 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         for (int rep = 0; rep < 2; ++rep) {
             const int u = tid + rep * kChunkThreads;
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 8 * (ln >> 4);
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
             float x[8];
-            const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 4]);
+            const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 16]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
             store_frag(Wf, m, ks, 4, ln, x);
@@ -686,353 +701,362 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
 }
 
 // ---------------------------------------------------------------------------------------
-// chain: one workgroup per (sequence, v head, 32-column state slice), 512 threads
+// chain: one workgroup per (sequence, v head, 16-column state strip), 6 waves
 // ---------------------------------------------------------------------------------------
-// The workgroup has 8 waves in two roles that meet at two barriers per chunk:
-//   state waves (0-3): S -> LDS | W S, D = U - W S -> LDS | S' = Gam_last S + K^T (exp(G_last - G) D)
-//   output waves (4-7):          | Q S                   | O = diag(Gam) Q S + M D
-// All products are split-bf16 MFMA (16x16x32). The A operands (W, K^T, Q, M) come from the
-// chunk kernel's fragments; the B operands (S, D, Dg) are split by their producer wave into
-// LDS fragments of the B layout: fragment (ks, nt) covers k = 32ks..32ks+31 and columns
-// 16nt..16nt+15; lane l holds column 16nt + l%16, k = 32ks + 8(l/16) .. +7.
-// Lane (li = lane & 15, lg4 = lane >> 4) of role wave r: output rows 16r + 4lg4 + i in C layout;
-// state wave r owns state rows 32r .. 32r + 31 (two 16-row m-tiles) of the slice's 32 columns.
-// Each role loads the next chunk's operands (double buffer) while it computes the current one.
-constexpr int kSlice = 32;                      // state columns per chain workgroup
-constexpr int kSlices = kD / kSlice;            // 4
-constexpr int kNT = kSlice / 16;                // 16-column tiles per slice
+// Columns of the state are independent, so a head's chain splits into 8 strips of 16
+// columns, and each strip's workgroup walks its sequence's chunks in order. Roles:
+//   wave 0 (state) carries the strip S (128 x 16) in four-register MFMA accumulators and
+//     per chunk computes
+//       D  = U - W S                                   (64 x 16; W from LDS)
+//       S' = Gam_last S + K^T Dg,  Dg = diag(exp(G_last - G)) D     (K^T from LDS)
+//     The chunk kernel stores W, K^T, Q and M with their k index in accumulator row order
+//     (kperm), so the accumulator tiles of S and D, split to bf16 hi/lo, are the next
+//     product's B operands as they stand: the state path has no LDS round trip and never
+//     waits at a barrier for data. It hands the split S and D of every chunk to the output
+//     waves through a double-buffered LDS slot.
+//   waves 1-4 (output): wave 1 + r computes rows 16 r .. 16 r + 15 of
+//       O = diag(Gam) Q S + M D                        (Q, M from global, one chunk ahead)
+//     from the S and D the state wave handed over.
+//   wave 5 (copy) moves the next chunk's W and K^T fragments (64 KiB) into the other LDS
+//     slot with direct global-to-LDS loads, and waits for them before the barrier.
+// The roles meet at one barrier per chunk. Between barriers c-1 and c the state wave
+// computes chunk c from slot c&1 and writes hand-over slot c&1, the copy wave fills slot
+// (c+1)&1, and the output waves compute chunk c-1 from hand-over slot (c-1)&1. The state
+// wave's code path issues no LDS DMA, so the compiler never makes it wait for the copies.
+constexpr int kStrip = 16;                              // state columns per chain workgroup
+constexpr int kStrips = kD / kStrip;                    // 8
+constexpr int kChainWaves = 6;
+constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
+constexpr int kOpsBytes = 32 * kPlane;                  // W (4 x 4) or K^T (8 x 2) fragments, 2 planes
+constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
+constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 2 k-steps x 2 planes
+constexpr int kChainSink = kPlane;                      // target of the L2 warm-up loads
+constexpr int kChainLds = 4 * kOpsBytes + 2 * kHandBytes + kChainSink;   // 156,672 bytes
+constexpr int kWarmAhead = 2;                           // chunks warmed ahead of their copy
+constexpr int kWarmLoads = 19;                          // warm-up loads per chunk and strip
 
-typedef float f4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
-
-// B-fragment LDS tiles of the chain (bf16 elements): S (k = state row, 4 ks), D and Dg (k = token, 2 ks).
-constexpr int kBFrag = 2 * kWave * 8;                       // one (ks, nt) fragment, both planes
-__device__ __forceinline__ int bfrag_at(int ks, int nt, int plane, int ln) {
-    return ((ks * kNT + nt) * 2 + plane) * kWave * 8 + ln * 8;
+__device__ __forceinline__ bf8 lds_frag(const uint8_t* lds, int off, int lane) {
+    return *reinterpret_cast<const bf8*>(lds + off + lane * 16);
+}
+__device__ __forceinline__ void lds_put(uint8_t* lds, int off, int lane, const bf8& v) {
+    *reinterpret_cast<bf8*>(lds + off + lane * 16) = v;
 }
 
-// Write 4 consecutive k values (k = 4 q .. 4 q + 3 within the fragment's 32, q = 0..7) of
-// column n (0..15) of fragment (ks, nt), split, into a B-fragment tile.
-__device__ __forceinline__ void bfrag_put4(uint16_t* tile, int ks, int nt, int q, int n, const f4& v) {
-    const int ln = 16 * (q >> 1) + n, e0 = 4 * (q & 1);
-    uint16_t hi[4], lo[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const __bf16 hb = (__bf16)v[e];
-        hi[e] = __builtin_bit_cast(uint16_t, hb);
-        lo[e] = __builtin_bit_cast(uint16_t, (__bf16)(v[e] - (float)hb));
-    }
-    uint2 h2 = {(uint32_t)hi[0] | ((uint32_t)hi[1] << 16), (uint32_t)hi[2] | ((uint32_t)hi[3] << 16)};
-    uint2 l2 = {(uint32_t)lo[0] | ((uint32_t)lo[1] << 16), (uint32_t)lo[2] | ((uint32_t)lo[3] << 16)};
-    *reinterpret_cast<uint2*>(tile + bfrag_at(ks, nt, 0, ln) + e0) = h2;
-    *reinterpret_cast<uint2*>(tile + bfrag_at(ks, nt, 1, ln) + e0) = l2;
+// B operand of one 32-wide k-step from two stacked accumulator tiles (kperm order), split.
+__device__ __forceinline__ void split_tiles(const v4& a, const v4& b, bf8& hi, bf8& lo) {
+    uint32_t h0, h1, h2, h3, l0, l1, l2, l3;
+    split2(a[0], a[1], h0, l0);
+    split2(a[2], a[3], h1, l1);
+    split2(b[0], b[1], h2, l2);
+    split2(b[2], b[3], h3, l3);
+    hi = __builtin_bit_cast(bf8, u4x{h0, h1, h2, h3});
+    lo = __builtin_bit_cast(bf8, u4x{l0, l1, l2, l3});
 }
 
-struct StateOps {
-    bf8 w[4][2];          // W fragments (m = r, ks 0..3), planes
-    bf8 kt[2][2][2];      // K^T fragments (m = 2r + mt, ks 0..1), planes
-    f4 u[kNT];            // U rows 16r + 4lg4 + i, columns j0 + 16nt + li
-    f4 gv;                // G at those rows
-    float glast;          // G of the chunk's last row
-};
-struct OutOps {
-    bf8 q[4][2];          // Q fragments (m = r, ks 0..3), planes
-    bf8 m[2][2];          // M fragments (m = r, ks 0..1), planes
-    f4 gv;
-    int t0, len;
-};
-
-struct ChainCtx {
-    const PrefillParams* p;
-    int h, src, seq_lo, seq_hi, c_begin, j0, r, li, lg4, lane;
-};
-
-__device__ __forceinline__ size_t chain_ch(const ChainCtx& x, int c) { return (size_t)c * x.p->L.h_v + x.h; }
-
-__device__ __forceinline__ void load_state_ops(const ChainCtx& x, int c, StateOps& o) {
-    const PrefillParams& p = *x.p;
-    const size_t ch = chain_ch(x, c);
-    const uint16_t* Wf = p.ws.Wf + ch * kFragW;
-    const uint16_t* Kf = p.ws.Ktf + ((size_t)c * p.L.h_k + x.src) * kFragKt;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int pl = 0; pl < 2; ++pl) o.w[ks][pl] = *reinterpret_cast<const bf8*>(Wf + frag_at(x.r, ks, 4, pl, x.lane));
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int pl = 0; pl < 2; ++pl)
-                o.kt[mt][ks][pl] = *reinterpret_cast<const bf8*>(Kf + frag_at(2 * x.r + mt, ks, 2, pl, x.lane));
-    const int crow = 16 * x.r + 4 * x.lg4;
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
-        o.u[nt] = *reinterpret_cast<const f4*>(p.ws.Ut + (ch * kD + x.j0 + 16 * nt + x.li) * kChunk + crow);
-    const float* Gc = p.ws.G + ch * kChunk;
-    o.gv = *reinterpret_cast<const f4*>(Gc + crow);
-    o.glast = Gc[kChunk - 1];
+__device__ __forceinline__ v4 mfma_bf16(const bf8& a, const bf8& b, const v4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// c += A B with both operands split: hi hi + hi lo + lo hi.
+__device__ __forceinline__ v4 mfma_split(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, v4 c) {
+    c = mfma_bf16(ah, bh, c);
+    c = mfma_bf16(ah, bl, c);
+    return mfma_bf16(al, bh, c);
 }
 
-__device__ __forceinline__ void load_out_ops(const ChainCtx& x, int c, OutOps& o) {
-    const PrefillParams& p = *x.p;
-    const size_t ch = chain_ch(x, c);
-    o.t0 = x.seq_lo + (c - x.c_begin) * kChunk;            // chunk c of the sequence (no table lookup)
-    o.len = min(kChunk, x.seq_hi - o.t0);
-    const uint16_t* Qf = p.ws.Qf + ((size_t)c * p.L.h_k + x.src) * kFragW;
+__device__ __forceinline__ int chain_w_slot(int q) { return q * kOpsBytes; }
+__device__ __forceinline__ int chain_k_slot(int q) { return (2 + q) * kOpsBytes; }
+__device__ __forceinline__ int chain_h_slot(int q) { return 4 * kOpsBytes + q * kHandBytes; }
+
+// State role: U of chunk c at this lane's rows 16 m + 4 lg4 + i (tokens), column j, the
+// decay factors exp(G_last - G) at the same rows, and Gam_last = exp(G_last).
+__device__ __forceinline__ void chain_load_ug(const PrefillParams& p, int c, int h, int j, int lg4, v4 (&u)[4],
+                                              v4 (&e)[4], float& gam) {
+    const size_t ch = (size_t)c * p.L.h_v + h;
+    const float* Ut = p.ws.Ut + (ch * kD + j) * kChunk + 4 * lg4;
+    const float* E = p.ws.G + ch * 2 * kChunk;
+    gam = E[2 * kChunk - 1];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) e[m] = *reinterpret_cast<const v4*>(E + 16 * m + 4 * lg4);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) u[m] = *reinterpret_cast<const v4*>(Ut + 16 * m);
+}
+
+// Output role: Q and M fragments of row tile r of chunk c, and G at this lane's rows.
+__device__ __forceinline__ void chain_load_qm(const PrefillParams& p, int c, int h, int src, int r, int lane,
+                                              bf8 (&qf)[4][2], bf8 (&mf)[2][2], v4& g) {
+    const size_t ch = (size_t)c * p.L.h_v + h;
+    const uint16_t* Qf = p.ws.Qf + ((size_t)c * p.L.h_k + src) * kFragW;
     const uint16_t* Mf = p.ws.Mf + ch * kFragM;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) o.q[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(x.r, ks, 4, pl, x.lane));
+        for (int pl = 0; pl < 2; ++pl) qf[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(r, ks, 4, pl, lane));
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) o.m[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(x.r, ks, 2, pl, x.lane));
-    o.gv = *reinterpret_cast<const f4*>(p.ws.G + ch * kChunk + 16 * x.r + 4 * x.lg4);
+        for (int pl = 0; pl < 2; ++pl) mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
+    g = *reinterpret_cast<const v4*>(p.ws.G + ch * 2 * kChunk + kChunk + 16 * r + 4 * (lane >> 4));   // exp(G_t)
 }
 
-// State waves, one chunk: D = U - W S, S' = Gam_last S + K^T (exp(G_last - G) D).
-// S[mt][nt]: rows 32r + 16mt + 4lg4 + i, columns 16nt + li of the slice.
-__device__ __forceinline__ void state_step(const ChainCtx& x, const StateOps& o, f4 (&S)[2][kNT], uint16_t* S_f,
-                                           uint16_t* D_f, uint16_t* Dg_f) {
-    const int r = x.r, li = x.li, lg4 = x.lg4, lane = x.lane;
-    // S into B fragments: state row i = 32r + 16mt + 4lg4 + e -> ks = r, q = 4mt + lg4
+// Copy role: the 32 one-KiB fragment planes of W (chunk c, v head h) or K^T (chunk c, q/k
+// head src) into LDS at dst.
+__device__ __forceinline__ void chain_copy(lds_u8* dst, const uint16_t* frags, int lane) {
+    const uint8_t* g = reinterpret_cast<const uint8_t*>(frags) + lane * 16;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) bfrag_put4(S_f, r, nt, 4 * mt + lg4, li, S[mt][nt]);
-    lds_barrier();                                                    // (A) state slice visible
-
-    // W S: the three split products and the column tiles accumulate separately (six
-    // independent MFMA chains), and all B fragments of a k-step are read before its MFMAs.
-    f4 ws[kNT][3];
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-        for (int q = 0; q < 3; ++q) ws[nt][q] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        bf8 bh[kNT], bl[kNT];
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            bh[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 0, lane));
-            bl[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 1, lane));
-        }
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            ws[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][0], bh[nt], ws[nt][0], 0, 0, 0);
-            ws[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][0], bl[nt], ws[nt][1], 0, 0, 0);
-            ws[nt][2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.w[ks][1], bh[nt], ws[nt][2], 0, 0, 0);
-        }
-    }
-    f4 d[kNT], dg[kNT];
-    f4 eg;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) eg[i] = expf(o.glast - o.gv[i]);
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            d[nt][i] = o.u[nt][i] - (ws[nt][0][i] + (ws[nt][1][i] + ws[nt][2][i]));
-            dg[nt][i] = eg[i] * d[nt][i];
-        }
-    }
-    // D, Dg into B fragments: token t = 16r + 4lg4 + e -> ks = r >> 1, q = 4 (r & 1) + lg4
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-        bfrag_put4(D_f, r >> 1, nt, 4 * (r & 1) + lg4, li, d[nt]);
-        bfrag_put4(Dg_f, r >> 1, nt, 4 * (r & 1) + lg4, li, dg[nt]);
-    }
-    lds_barrier();                                                    // (B) D visible
-
-    // S' = Gam_last S + K^T Dg: the state tile takes the hi*hi products; hi*lo and lo*hi
-    // go to a second accumulator per tile, added at the end.
-    const float gl = expf(o.glast);
-    f4 sx[2][kNT];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) { S[mt][nt] *= gl; sx[mt][nt] = f4{0.f, 0.f, 0.f, 0.f}; }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        bf8 bh[kNT], bl[kNT];
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            bh[nt] = *reinterpret_cast<const bf8*>(Dg_f + bfrag_at(ks, nt, 0, lane));
-            bl[nt] = *reinterpret_cast<const bf8*>(Dg_f + bfrag_at(ks, nt, 1, lane));
-        }
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < kNT; ++nt) {
-                S[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][0], bh[nt], S[mt][nt], 0, 0, 0);
-                sx[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][0], bl[nt], sx[mt][nt], 0, 0, 0);
-                sx[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.kt[mt][ks][1], bh[nt], sx[mt][nt], 0, 0, 0);
-            }
-    }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) S[mt][nt] += sx[mt][nt];
+    for (int i = 0; i < 32; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, dst + i * kPlane, 16, 0, 0);
 }
 
-// Output waves, one chunk: O = diag(Gam) Q S + M D for rows 16r..16r+15. OUT: bit 0 fp32 o,
-// bit 1 bf16 o. Every store is issued (rows past the sequence end go to the sink), so the
-// number of memory operations per chunk is fixed and the next chunk's operand loads never
-// have to wait for this chunk's stores.
-template <int OUT>
-__device__ __forceinline__ void out_step(const ChainCtx& x, const OutOps& o, const uint16_t* S_f, const uint16_t* D_f) {
-    const PrefillParams& p = *x.p;
-    const int r = x.r, li = x.li, lg4 = x.lg4, lane = x.lane, crow = 16 * r + 4 * lg4;
-    lds_barrier();                                                    // (A)
-    f4 qs[kNT][3];
+// W fragments (row tiles m = 0..3, both planes) of k-step ks from slot q.
+__device__ __forceinline__ void chain_w_frags(const uint8_t* lds, int q, int ks, int lane, bf8 (&f)[4][2]) {
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt)
-#pragma unroll
-        for (int q = 0; q < 3; ++q) qs[nt][q] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        bf8 bh[kNT], bl[kNT];
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            bh[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 0, lane));
-            bl[nt] = *reinterpret_cast<const bf8*>(S_f + bfrag_at(ks, nt, 1, lane));
-        }
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            qs[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][0], bh[nt], qs[nt][0], 0, 0, 0);
-            qs[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][0], bl[nt], qs[nt][1], 0, 0, 0);
-            qs[nt][2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.q[ks][1], bh[nt], qs[nt][2], 0, 0, 0);
-        }
+    for (int m = 0; m < 4; ++m) {
+        const int o = chain_w_slot(q) + (m * 4 + ks) * 2 * kPlane;
+        f[m][0] = lds_frag(lds, o, lane);
+        f[m][1] = lds_frag(lds, o + kPlane, lane);
     }
-    lds_barrier();                                                    // (B)
-    f4 eg;
+}
+// K^T fragments (row tiles 4 g .. 4 g + 3, both planes) of k-step ks from slot q.
+__device__ __forceinline__ void chain_kt_frags(const uint8_t* lds, int q, int ks, int g, int lane, bf8 (&f)[4][2]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) eg[i] = expf(o.gv[i]);
-    f4 md[kNT][2];
+    for (int j = 0; j < 4; ++j) {
+        const int o = chain_k_slot(q) + ((4 * g + j) * 2 + ks) * 2 * kPlane;
+        f[j][0] = lds_frag(lds, o, lane);
+        f[j][1] = lds_frag(lds, o + kPlane, lane);
+    }
+}
+// acc[j] += A_j B for four row tiles, split products; the products go tile by tile within
+// each of hi hi, hi lo, lo hi, so consecutive MFMAs never share an accumulator.
+__device__ __forceinline__ void mfma4_split(const bf8 (&a)[4][2], const bf8& bh, const bf8& bl, v4* acc) {
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
+    for (int j = 0; j < 4; ++j) acc[j] = mfma_bf16(a[j][0], bh, acc[j]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) md[nt][0][i] = eg[i] * (qs[nt][0][i] + (qs[nt][1][i] + qs[nt][2][i]));
-        md[nt][1] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 4; ++j) acc[j] = mfma_bf16(a[j][0], bl, acc[j]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = mfma_bf16(a[j][1], bh, acc[j]);
+}
+
+// State role, one chunk from slot q, in two parts around the chunk's barrier:
+//   chain_state_a: D = U - W S (S handed over on the way), D handed over, Dg split;
+//   barrier (the output waves take the hand-over);
+//   chain_state_b: S' = Gam_last S + K^T Dg with Dg = diag(exp(G_last - G)) D.
+// Part b of one chunk and part a of the next run back to back with no barrier between
+// them. The fragments of the next k-step (or row-tile group) are read while the current
+// one's MFMAs run.
+__device__ __forceinline__ void chain_state_a(uint8_t* lds, int q, int lane, const v4 (&S)[8], const v4 (&U)[4],
+                                              const v4 (&E)[4], bf8 (&dh)[2], bf8 (&dl)[2]) {
+    v4 acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = v4{0.f, 0.f, 0.f, 0.f};
+    bf8 fa[4][2], fb[4][2], sh[4], sl[4];
+    auto split_s = [&](int ks) {
+        split_tiles(S[2 * ks], S[2 * ks + 1], sh[ks], sl[ks]);
+        lds_put(lds, chain_h_slot(q) + (2 * ks) * kPlane, lane, sh[ks]);
+        lds_put(lds, chain_h_slot(q) + (2 * ks + 1) * kPlane, lane, sl[ks]);
+    };
+    chain_w_frags(lds, q, 0, lane, fa);
+    split_s(0);
+    chain_w_frags(lds, q, 1, lane, fb);
+    split_s(1);
+    mfma4_split(fa, sh[0], sl[0], acc);
+    chain_w_frags(lds, q, 2, lane, fa);
+    split_s(2);
+    mfma4_split(fb, sh[1], sl[1], acc);
+    chain_w_frags(lds, q, 3, lane, fb);
+    split_s(3);
+    mfma4_split(fa, sh[2], sl[2], acc);
+    mfma4_split(fb, sh[3], sl[3], acc);
+    v4 D[4], Dg[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        D[m] = U[m] - acc[m];
+        Dg[m] = E[m] * D[m];
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-        bf8 bh[kNT], bl[kNT];
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            bh[nt] = *reinterpret_cast<const bf8*>(D_f + bfrag_at(ks, nt, 0, lane));
-            bl[nt] = *reinterpret_cast<const bf8*>(D_f + bfrag_at(ks, nt, 1, lane));
-        }
-#pragma unroll
-        for (int nt = 0; nt < kNT; ++nt) {
-            md[nt][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][0], bh[nt], md[nt][0], 0, 0, 0);
-            md[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][0], bl[nt], md[nt][1], 0, 0, 0);
-            md[nt][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(o.m[ks][1], bh[nt], md[nt][1], 0, 0, 0);
-        }
+        bf8 a, b;
+        split_tiles(D[2 * ks], D[2 * ks + 1], a, b);
+        lds_put(lds, chain_h_slot(q) + kHandS + (2 * ks) * kPlane, lane, a);
+        lds_put(lds, chain_h_slot(q) + kHandS + (2 * ks + 1) * kPlane, lane, b);
+        split_tiles(Dg[2 * ks], Dg[2 * ks + 1], dh[ks], dl[ks]);
     }
+}
+__device__ __forceinline__ void chain_state_b(const uint8_t* lds, int q, int lane, v4 (&S)[8], float gam,
+                                              const bf8 (&dh)[2], const bf8 (&dl)[2]) {
+    bf8 fa[4][2], fb[4][2];
+    chain_kt_frags(lds, q, 0, 0, lane, fa);
+    chain_kt_frags(lds, q, 1, 0, lane, fb);
 #pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-        const f4 ov = md[nt][0] + md[nt][1];
+    for (int mt = 0; mt < 8; ++mt) S[mt] *= gam;
+    mfma4_split(fa, dh[0], dl[0], S);
+    chain_kt_frags(lds, q, 0, 1, lane, fa);
+    mfma4_split(fb, dh[1], dl[1], S);                             // row tiles 0-3 done first
+    chain_kt_frags(lds, q, 1, 1, lane, fb);
+    mfma4_split(fa, dh[0], dl[0], S + 4);
+    mfma4_split(fb, dh[1], dl[1], S + 4);
+}
+
+struct ChainOut {
+    bf8 qf[4][2], mf[2][2];
+    v4 g;                 // exp(G_t) at this lane's rows
+};
+
+// Output role, one chunk: rows 16 r .. 16 r + 15 of O = diag(Gam) Q S + M D from hand-over
+// slot q. Rows at or past len are not stored.
+template <int OUT>
+__device__ __forceinline__ void chain_out_step(const PrefillParams& p, const uint8_t* lds, int q, int lane, int r,
+                                               const ChainOut& x, size_t o_base, int len) {
+    lds_barrier();                                                // the chunk has been handed over
+    bf8 sb[4][2], db[2][2];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = crow + i;
-            const size_t oo = ((size_t)(o.t0 + t) * p.L.h_v + x.h) * kD + x.j0 + 16 * nt + li;
-            const bool in = t < o.len;
-            if constexpr ((OUT & 1) != 0) *(in ? p.o + oo : p.ws.sink + lane) = ov[i];
-            if constexpr ((OUT & 2) != 0)
-                *(in ? p.o_bf16 + oo : reinterpret_cast<uint16_t*>(p.ws.sink) + lane) = f32_to_bf16(ov[i]);
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) sb[ks][pl] = lds_frag(lds, chain_h_slot(q) + (2 * ks + pl) * kPlane, lane);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) db[ks][pl] = lds_frag(lds, chain_h_slot(q) + kHandS + (2 * ks + pl) * kPlane, lane);
+    v4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) o = mfma_split(x.qf[ks][0], x.qf[ks][1], sb[ks][0], sb[ks][1], o);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] *= x.g[i];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) o = mfma_split(x.mf[ks][0], x.mf[ks][1], db[ks][0], db[ks][1], o);
+    const size_t row = (size_t)p.L.h_v * kD;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 16 * r + 4 * (lane >> 4) + i;
+        if (t < len) {
+            const size_t oo = o_base + (size_t)t * row;
+            if constexpr ((OUT & 1) != 0) p.o[oo] = o[i];
+            if constexpr ((OUT & 2) != 0) p.o_bf16[oo] = f32_to_bf16(o[i]);
         }
     }
 }
 
-// As many stores as one out_step issues, all to the sink: issued once before the loop so
-// that the memory operations in flight at the loop head are the same on entry as around the
-// loop, and the compiler's wait for the next operands does not cover the last stores.
-template <int OUT>
-__device__ __forceinline__ void sink_stores(const PrefillParams& p, int lane) {
+// Copy role: bring this strip's share of chunk c's operands into L2 ahead of their use: an
+// eighth of W, K^T, Q and M (the 8 strips of a head share one XCD and its L2), its own U
+// rows, and G. Direct loads into a sink in LDS, so no register waits for them; always
+// kWarmLoads loads, which the wait before each barrier leaves in flight.
+__device__ __forceinline__ void chain_warm(const PrefillParams& p, lds_u8* sink, int c, int h, int src, int strip,
+                                           int lane) {
+    const size_t ch = (size_t)c * p.L.h_v + h, cs = (size_t)c * p.L.h_k + src;
+    const uint8_t* W = reinterpret_cast<const uint8_t*>(p.ws.Wf + ch * kFragW) + strip * 4 * kPlane + lane * 16;
+    const uint8_t* K = reinterpret_cast<const uint8_t*>(p.ws.Ktf + cs * kFragKt) + strip * 4 * kPlane + lane * 16;
+    const uint8_t* Q = reinterpret_cast<const uint8_t*>(p.ws.Qf + cs * kFragW) + strip * 4 * kPlane + lane * 16;
+    const uint8_t* M = reinterpret_cast<const uint8_t*>(p.ws.Mf + ch * kFragM) + strip * 2 * kPlane + lane * 16;
+    const uint8_t* U = reinterpret_cast<const uint8_t*>(p.ws.Ut + (ch * kD + strip * kStrip) * kChunk) + lane * 16;
+    const uint8_t* G = reinterpret_cast<const uint8_t*>(p.ws.G + ch * 2 * kChunk) + (lane & 31) * 16;
 #pragma unroll
-    for (int i = 0; i < kNT * 4; ++i) {            // distinct addresses: none of them is redundant
-        if constexpr ((OUT & 1) != 0) p.ws.sink[i * kWave + lane] = 0.0f;
-        if constexpr ((OUT & 2) != 0) reinterpret_cast<uint16_t*>(p.ws.sink + 8 * kWave)[i * kWave + lane] = 0;
+    for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_global_load_lds(W + i * kPlane, sink, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(K + i * kPlane, sink, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(Q + i * kPlane, sink, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(U + i * kPlane, sink, 16, 0, 0);
     }
+    __builtin_amdgcn_global_load_lds(M, sink, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(M + kPlane, sink, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(G, sink, 16, 0, 0);
+}
+
+// s_waitcnt that waits until at most N vector memory operations are outstanding (gfx9
+// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 template <int OUT>
-__global__ void __launch_bounds__(512) chain_kernel(const PrefillParams p) {
-    __shared__ __align__(16) uint16_t S_f[4 * kNT * kBFrag];
-    __shared__ __align__(16) uint16_t D_f[2 * kNT * kBFrag];
-    __shared__ __align__(16) uint16_t Dg_f[2 * kNT * kBFrag];
+__global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const PrefillParams p) {
+    __shared__ __align__(16) uint8_t lds[kChainLds];
 
     const Layer& L = p.L;
-    // XCD-aware mapping: the 4 slices of one (sequence, head) pair share an XCD (and its L2).
+    // XCD-aware mapping: the 8 strips of one (sequence, head) pair share an XCD, so its L2
+    // serves the pair's chunk operands to all of them.
     const int lin = blockIdx.x, xcd = lin & 7, k = lin >> 3;
-    const int slice = k & (kSlices - 1);
-    const int pair = (k / kSlices) * 8 + xcd;
+    const int strip = k & (kStrips - 1);
+    const int pair = (k / kStrips) * 8 + xcd;
     if (pair >= p.n_seq * L.h_v) return;
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
     const int c_begin = p.ws.chunk_off[s], c_end = p.ws.chunk_off[s + 1];
     if (c_begin >= c_end) return;
-    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
+    const int j0 = strip * kStrip;
 
-    ChainCtx x;
-    x.p = &p;
-    x.h = h;
-    x.src = src;
-    x.seq_lo = p.ws.seq_lo[s];
-    x.seq_hi = p.ws.seq_lo[s + 1];
-    x.c_begin = c_begin;
-    x.j0 = slice * kSlice;
-    x.r = w & 3;
-    x.li = lane & 15;
-    x.lg4 = lane >> 4;
-    x.lane = lane;
-
-    if (w < 4) {
-        // State slice: rows 32 r + 16 mt + 4 lg4 + i (k index), columns j0 + 16 nt + li (v
-        // index); the state is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
-        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD;
-        f4 S[2][kNT];
+    if (w == 0) {
+        // State strip: rows 16 mt + 4 lg4 + i (k index), column j0 + li (v index); the state
+        // is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
+        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD + (size_t)(j0 + li) * kD + 4 * lg4;
+        v4 S[8];
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < kNT; ++nt)
-                S[mt][nt] = *reinterpret_cast<const f4*>(st + (size_t)(x.j0 + 16 * nt + x.li) * kD + 32 * x.r + 16 * mt + 4 * x.lg4);
-        __builtin_amdgcn_s_waitcnt(0);             // the state is in registers before the loop
-        // Prefetches are unconditional (past the last chunk they re-read it): a load that is
-        // skipped on one path forces the compiler to wait for every load in flight.
-        StateOps A, B;
-        load_state_ops(x, c_begin, A);
+        for (int mt = 0; mt < 8; ++mt) S[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
+        v4 U[4], E[4];
+        float gam;
+        bf8 dh[2], dl[2];
+        chain_load_ug(p, c_begin, h, j0 + li, lg4, U, E, gam);
+        lds_barrier();                                            // W of the first chunk in LDS
+        // Chunk c: part a, barrier c, part b. U and E of chunk c+1 are loaded as soon as part
+        // a of chunk c has used them (unconditionally: past the last chunk they re-read it).
+        // Two chunks per loop trip, so that part b of the first and part a of the second
+        // share a basic block and can overlap.
+        auto chunk = [&](int c) {
+            const int q = (c - c_begin) & 1;
+            chain_state_a(lds, q, lane, S, U, E, dh, dl);
+            const float g = gam;
+            __builtin_amdgcn_sched_barrier(0);
+            chain_load_ug(p, min(c + 1, c_end - 1), h, j0 + li, lg4, U, E, gam);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();                                        // barrier c
+            chain_state_b(lds, q, lane, S, g, dh, dl);
+        };
         int c = c_begin;
         for (; c + 1 < c_end; c += 2) {
-            load_state_ops(x, c + 1, B);
-            state_step(x, A, S, S_f, D_f, Dg_f);
-            __builtin_amdgcn_sched_barrier(0);     // keep A's reload after A's last use
-            load_state_ops(x, min(c + 2, c_end - 1), A);
-            state_step(x, B, S, S_f, D_f, Dg_f);
+            chunk(c);
+            chunk(c + 1);
+        }
+        if (c < c_end) chunk(c);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
+    } else if (w <= 4) {
+        const int r = w - 1;
+        const int seq_lo = p.ws.seq_lo[s], seq_hi = p.ws.seq_lo[s + 1];
+        ChainOut x;
+        chain_load_qm(p, c_begin, h, src, r, lane, x.qf, x.mf, x.g);
+        lds_barrier();
+        for (int c = c_begin; c < c_end; ++c) {
+            const int t0 = seq_lo + (c - c_begin) * kChunk;
+            chain_out_step<OUT>(p, lds, (c - c_begin) & 1, lane, r, x, ((size_t)t0 * L.h_v + h) * kD + j0 + li,
+                                min(kChunk, seq_hi - t0));
+            __builtin_amdgcn_sched_barrier(0);                    // the reload after the last use
+            chain_load_qm(p, min(c + 1, c_end - 1), h, src, r, lane, x.qf, x.mf, x.g);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (c < c_end) state_step(x, A, S, S_f, D_f, Dg_f);
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < kNT; ++nt)
-                *reinterpret_cast<f4*>(st + (size_t)(x.j0 + 16 * nt + x.li) * kD + 32 * x.r + 16 * mt + 4 * x.lg4) = S[mt][nt];
     } else {
-        OutOps A, B;                               // same schedule as the state waves
-        load_out_ops(x, c_begin, A);
-        sink_stores<OUT>(p, lane);
-        int c = c_begin;
-        for (; c + 1 < c_end; c += 2) {
-            load_out_ops(x, c + 1, B);
-            out_step<OUT>(x, A, S_f, D_f);
-            __builtin_amdgcn_sched_barrier(0);
-            load_out_ops(x, min(c + 2, c_end - 1), A);
-            out_step<OUT>(x, B, S_f, D_f);
-            __builtin_amdgcn_sched_barrier(0);
+        lds_u8* lds3 = (lds_u8*)lds;                              // the copies address LDS directly
+        lds_u8* sink = lds3 + 4 * kOpsBytes + 2 * kHandBytes;
+        auto w_of = [&](int cc) { return p.ws.Wf + ((size_t)cc * L.h_v + h) * kFragW; };
+        auto kt_of = [&](int cc) { return p.ws.Ktf + ((size_t)cc * L.h_k + src) * kFragKt; };
+        // Before the first barrier: W of the first chunk. Between barriers c-1 and c: W of
+        // chunk c+1 (used before barrier c+1) and K^T of chunk c (used after barrier c); the
+        // slots they replace were last read before barrier c-1.
+        chain_copy(lds3 + chain_w_slot(0), w_of(c_begin), lane);
+#pragma unroll
+        for (int a = 1; a <= kWarmAhead; ++a) chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane);
+        wait_vmcnt<kWarmAhead * kWarmLoads>();                   // the copies have landed in LDS
+        lds_barrier();
+        for (int c = c_begin; c < c_end; ++c) {
+            const int q = (c - c_begin) & 1;
+            if (c + 1 < c_end) chain_copy(lds3 + chain_w_slot(q ^ 1), w_of(c + 1), lane);
+            chain_copy(lds3 + chain_k_slot(q), kt_of(c), lane);
+            chain_warm(p, sink, min(c + 1 + kWarmAhead, c_end - 1), h, src, strip, lane);
+            wait_vmcnt<kWarmLoads>();                            // this trip's copies done, its warm-ups may not be
+            lds_barrier();                                        // barrier c
         }
-        if (c < c_end) out_step<OUT>(x, A, S_f, D_f);
+        __builtin_amdgcn_s_waitcnt(0);
     }
 }
 
@@ -1089,7 +1113,7 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
         return hipErrorInvalidValue;
     const long long NC = (total_T + kChunk - 1) / kChunk + (long long)n_seq;
     const long long pairs = (long long)n_seq * cfg->h_v;
-    if (NC > 0x7fffffffLL || pairs * kSlices > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (NC > 0x7fffffffLL || ((pairs + 7) / 8) * 8 * kStrips > 0x7fffffffLL) return hipErrorInvalidValue;
     const long long rows = (long long)total_T * cfg->h_v;
     if (gate && (rows + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidValue;
 
@@ -1112,12 +1136,12 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     const size_t nch = (size_t)n_seq * p.L.C;
     hipLaunchKernelGGL(commit_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
-    const dim3 cgrid((unsigned)(groups * 8 * kSlices));
+    const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
     switch ((p.o ? 1 : 0) | (p.o_bf16 ? 2 : 0)) {
-        case 0: hipLaunchKernelGGL(chain_kernel<0>, cgrid, dim3(512), 0, s, p); break;
-        case 1: hipLaunchKernelGGL(chain_kernel<1>, cgrid, dim3(512), 0, s, p); break;
-        case 2: hipLaunchKernelGGL(chain_kernel<2>, cgrid, dim3(512), 0, s, p); break;
-        default: hipLaunchKernelGGL(chain_kernel<3>, cgrid, dim3(512), 0, s, p); break;
+        case 0: hipLaunchKernelGGL(chain_kernel<0>, cgrid, cblock, 0, s, p); break;
+        case 1: hipLaunchKernelGGL(chain_kernel<1>, cgrid, cblock, 0, s, p); break;
+        case 2: hipLaunchKernelGGL(chain_kernel<2>, cgrid, cblock, 0, s, p); break;
+        default: hipLaunchKernelGGL(chain_kernel<3>, cgrid, cblock, 0, s, p); break;
     }
     if (gate)
         hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o,
