@@ -729,7 +729,7 @@ constexpr int kChainWaves = 6;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
 constexpr int kOpsBytes = 32 * kPlane;                  // W (4 x 4) or K^T (8 x 2) fragments, 2 planes
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
-constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 2 k-steps x 2 planes
+constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in fp32
 constexpr int kChainSink = kPlane;                      // target of the L2 warm-up loads
 constexpr int kChainLds = 4 * kOpsBytes + 2 * kHandBytes + kChainSink;   // 156,672 bytes
 constexpr int kWarmAhead = 2;                           // chunks warmed ahead of their copy
@@ -873,28 +873,33 @@ __device__ __forceinline__ void chain_state_a(uint8_t* lds, int q, int lane, con
         D[m] = U[m] - acc[m];
         Dg[m] = E[m] * D[m];
     }
+    // D goes over in fp32 (the output waves split it); Dg is split here for part b.
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        bf8 a, b;
-        split_tiles(D[2 * ks], D[2 * ks + 1], a, b);
-        lds_put(lds, chain_h_slot(q) + kHandS + (2 * ks) * kPlane, lane, a);
-        lds_put(lds, chain_h_slot(q) + kHandS + (2 * ks + 1) * kPlane, lane, b);
-        split_tiles(Dg[2 * ks], Dg[2 * ks + 1], dh[ks], dl[ks]);
-    }
+    for (int m = 0; m < 4; ++m) *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = D[m];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) split_tiles(Dg[2 * ks], Dg[2 * ks + 1], dh[ks], dl[ks]);
 }
 __device__ __forceinline__ void chain_state_b(const uint8_t* lds, int q, int lane, v4 (&S)[8], float gam,
                                               const bf8 (&dh)[2], const bf8 (&dl)[2]) {
-    bf8 fa[4][2], fb[4][2];
-    chain_kt_frags(lds, q, 0, 0, lane, fa);
-    chain_kt_frags(lds, q, 1, 0, lane, fb);
+    // The reads of the next fragment group are pinned ahead of the current group's MFMAs,
+    // so LDS latency hides under them.
+    bf8 f0[4][2], f1[4][2], f2[4][2], f3[4][2];
+    chain_kt_frags(lds, q, 0, 0, lane, f0);
+    chain_kt_frags(lds, q, 1, 0, lane, f1);
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) S[mt] *= gam;
-    mfma4_split(fa, dh[0], dl[0], S);
-    chain_kt_frags(lds, q, 0, 1, lane, fa);
-    mfma4_split(fb, dh[1], dl[1], S);                             // row tiles 0-3 done first
-    chain_kt_frags(lds, q, 1, 1, lane, fb);
-    mfma4_split(fa, dh[0], dl[0], S + 4);
-    mfma4_split(fb, dh[1], dl[1], S + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    chain_kt_frags(lds, q, 0, 1, lane, f2);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma4_split(f0, dh[0], dl[0], S);
+    __builtin_amdgcn_sched_barrier(0);
+    chain_kt_frags(lds, q, 1, 1, lane, f3);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma4_split(f1, dh[1], dl[1], S);                             // row tiles 0-3 done first
+    __builtin_amdgcn_sched_barrier(0);
+    mfma4_split(f2, dh[0], dl[0], S + 4);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma4_split(f3, dh[1], dl[1], S + 4);
 }
 
 struct ChainOut {
@@ -913,10 +918,11 @@ __device__ __forceinline__ void chain_out_step(const PrefillParams& p, const uin
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) sb[ks][pl] = lds_frag(lds, chain_h_slot(q) + (2 * ks + pl) * kPlane, lane);
+    v4 D[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int m = 0; m < 4; ++m) D[m] = *reinterpret_cast<const v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16);
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) db[ks][pl] = lds_frag(lds, chain_h_slot(q) + kHandS + (2 * ks + pl) * kPlane, lane);
+    for (int ks = 0; ks < 2; ++ks) split_tiles(D[2 * ks], D[2 * ks + 1], db[ks][0], db[ks][1]);
     v4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) o = mfma_split(x.qf[ks][0], x.qf[ks][1], sb[ks][0], sb[ks][1], o);
@@ -1047,14 +1053,16 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
 #pragma unroll
         for (int a = 1; a <= kWarmAhead; ++a) chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane);
         wait_vmcnt<kWarmAhead * kWarmLoads>();                   // the copies have landed in LDS
-        lds_barrier();
+        // Bare barriers in this role: the explicit waits cover the copies, and a release
+        // fence would also wait for the warm-up loads (LDS DMA counts as LDS writes).
+        __builtin_amdgcn_s_barrier();
         for (int c = c_begin; c < c_end; ++c) {
             const int q = (c - c_begin) & 1;
             if (c + 1 < c_end) chain_copy(lds3 + chain_w_slot(q ^ 1), w_of(c + 1), lane);
             chain_copy(lds3 + chain_k_slot(q), kt_of(c), lane);
             chain_warm(p, sink, min(c + 1 + kWarmAhead, c_end - 1), h, src, strip, lane);
             wait_vmcnt<kWarmLoads>();                            // this trip's copies done, its warm-ups may not be
-            lds_barrier();                                        // barrier c
+            __builtin_amdgcn_s_barrier();                         // barrier c
         }
         __builtin_amdgcn_s_waitcnt(0);
     }
