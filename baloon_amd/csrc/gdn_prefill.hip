@@ -55,8 +55,7 @@ __device__ __forceinline__ v4 mfma4(float a, float b, v4 c) {
 struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
-    int32_t* chunk_seq;  // [NC]
-    int32_t* chunk_t0;   // [NC]
+    int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
     uint16_t* Wf;        // [NC][h_v] W (64 x 128) as split-bf16 A fragments
     float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
     uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
@@ -65,7 +64,7 @@ struct Ws {
     uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
 };
-constexpr int kWsSections = 10;
+constexpr int kWsSections = 9;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -73,7 +72,7 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSections]) {
     const size_t NC = (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq;
     const size_t sz[kWsSections] = {
-        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * NC, sizeof(int32_t) * NC,
+        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * 2 * kChunk,
         sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
@@ -87,14 +86,13 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     Ws w;
     w.seq_lo = reinterpret_cast<int32_t*>(base + off[0]);
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
-    w.chunk_seq = reinterpret_cast<int32_t*>(base + off[2]);
-    w.chunk_t0 = reinterpret_cast<int32_t*>(base + off[3]);
-    w.Wf = reinterpret_cast<uint16_t*>(base + off[4]);
-    w.Ut = reinterpret_cast<float*>(base + off[5]);
-    w.Mf = reinterpret_cast<uint16_t*>(base + off[6]);
-    w.G = reinterpret_cast<float*>(base + off[7]);
-    w.Ktf = reinterpret_cast<uint16_t*>(base + off[8]);
-    w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
+    w.chunk_rec = reinterpret_cast<int4*>(base + off[2]);
+    w.Wf = reinterpret_cast<uint16_t*>(base + off[3]);
+    w.Ut = reinterpret_cast<float*>(base + off[4]);
+    w.Mf = reinterpret_cast<uint16_t*>(base + off[5]);
+    w.G = reinterpret_cast<float*>(base + off[6]);
+    w.Ktf = reinterpret_cast<uint16_t*>(base + off[7]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[8]);
     return w;
 }
 
@@ -177,21 +175,24 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const PrefillParams 
             const int mid = (lo + hi + 1) >> 1;
             if (p.ws.chunk_off[mid] <= c) lo = mid; else hi = mid - 1;
         }
-        p.ws.chunk_seq[c] = lo;
-        p.ws.chunk_t0[c] = p.ws.seq_lo[lo] + (c - p.ws.chunk_off[lo]) * kChunk;
+        const int s0 = p.ws.seq_lo[lo];
+        p.ws.chunk_rec[c] = int4{lo, s0 + (c - p.ws.chunk_off[lo]) * kChunk, s0, p.ws.seq_lo[lo + 1]};
     }
 }
 
 // Chunk geometry: sequence, first token, tokens in the chunk, position of the first token
 // within its sequence. Returns false for grid slots beyond the chunk count.
-struct ChunkGeo { int s, t0, len, pos0; };
+// One load for the whole geometry (the chunk count is read alongside, independently).
+struct ChunkGeo { int s, t0, len, pos0, lo; };
 __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGeo& g) {
-    if (c >= p.ws.chunk_off[p.n_seq]) return false;
-    g.s = p.ws.chunk_seq[c];
-    g.t0 = p.ws.chunk_t0[c];
-    const int lo = p.ws.seq_lo[g.s], hi = p.ws.seq_lo[g.s + 1];
-    g.len = min(kChunk, hi - g.t0);
-    g.pos0 = g.t0 - lo;
+    const int nc = p.ws.chunk_off[p.n_seq];
+    const int4 r = p.ws.chunk_rec[min(c, p.NC - 1)];
+    if (c >= nc) return false;
+    g.s = r.x;
+    g.t0 = r.y;
+    g.lo = r.z;
+    g.len = min(kChunk, r.w - g.t0);
+    g.pos0 = g.t0 - g.lo;
     return true;
 }
 
@@ -208,7 +209,8 @@ constexpr int kConvTok = 16;
 
 // The loads are unconditional and nothing touches the loaded words before conv_run: a
 // load on one path only, or any use of a loaded value, makes the wave wait for every load
-// it has in flight.
+// it has in flight. Every row index is clamped into the chunk's tokens, so a wave whose
+// rows all lie past the chunk end (n = 0) reads valid rows, whose results are discarded.
 template <int DC>
 struct ConvIn {
     uint32_t h0[DC - 1], h1[DC - 1];    // history of the first token (one bf16 each), oldest first
@@ -222,7 +224,7 @@ __device__ __forceinline__ void conv_load(const PrefillParams& p, const ChunkGeo
     const Layer& L = p.L;
 #pragma unroll
     for (int i = 0; i < DC - 1; ++i) {
-        const int pos = g.pos0 + tb - (DC - 1) + i;            // wave-uniform
+        const int pos = min(g.pos0 + tb - (DC - 1) + i, g.pos0 + g.len - 1);   // wave-uniform
         const uint16_t* xp = p.x + (size_t)(lo + max(pos, 0)) * L.C + ch;
         const uint16_t* sp = p.conv_state + ((size_t)g.s * L.C + ch) * (DC - 1) + (DC - 1) + min(pos, -1);
         in.h0[i] = *(pos >= 0 ? xp : sp);
@@ -230,7 +232,7 @@ __device__ __forceinline__ void conv_load(const PrefillParams& p, const ChunkGeo
     }
 #pragma unroll
     for (int t = 0; t < kConvTok; ++t)
-        in.xs[t] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(g.t0 + tb + min(t, n - 1)) * L.C + ch);
+        in.xs[t] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(g.t0 + min(tb + min(t, n - 1), g.len - 1)) * L.C + ch);
     // conv_w is [C][dc]: the two channels' 2 dc weights are dc aligned words (ch is even)
     const uint32_t* wp = reinterpret_cast<const uint32_t*>(L.conv_w + (size_t)ch * DC);
 #pragma unroll
@@ -351,6 +353,19 @@ __device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nk
     *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 1, lane)) = lo;
 }
 
+// A fragment whose planes are already split (hi and lo bf16 bit patterns).
+__device__ __forceinline__ void store_frag_planes(uint16_t* base, int m, int ks, int nks, int lane,
+                                                  const uint16_t (&h)[8], const uint16_t (&l)[8]) {
+    u4x hv, lv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hv[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
+        lv[i] = (uint32_t)l[2 * i] | ((uint32_t)l[2 * i + 1] << 16);
+    }
+    *reinterpret_cast<u4x*>(base + frag_at(m, ks, nks, 0, lane)) = hv;
+    *reinterpret_cast<u4x*>(base + frag_at(m, ks, nks, 1, lane)) = lv;
+}
+
 // Fragment sizes in bf16 elements: (rows/16) x (k/32) fragments x 2 planes x 512.
 constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (W, Q)
 constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (M)
@@ -364,6 +379,20 @@ constexpr int kKS = kD + 4;          // padded LDS row stride of the K / Q / V t
 constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
 constexpr int kChunkThreads = 512;
 constexpr int kMaxMap = 16;          // v heads per q/k head (the configuration limit)
+
+// Normalised k and q rows in LDS as split-bf16 planes (hi, then lo; hi + lo is the fp32 value
+// to ~2^-17): [64 tokens][128 channels] bf16, 256-byte rows whose 16-byte chunks are
+// XOR-swizzled by (token & 15), so that a chunk read by 16 consecutive tokens (an MFMA
+// operand) touches 16 different bank groups. Byte offset of (token t, channel ch) in a plane:
+constexpr int kQKPlane = kChunk * 256;                   // bytes per plane
+__device__ __forceinline__ int qk_off(int t, int ch) {
+    return t * 256 + ((((ch >> 3) ^ (t & 15))) << 4) + ((ch & 7) << 1);
+}
+__device__ __forceinline__ float qk_f32(const uint8_t* planes, int t, int ch) {
+    const int o = qk_off(t, ch);
+    return bf16_to_f32(*reinterpret_cast<const uint16_t*>(planes + o)) +
+           bf16_to_f32(*reinterpret_cast<const uint16_t*>(planes + kQKPlane + o));
+}
 
 // The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
 __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
@@ -388,7 +417,8 @@ __device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, f
 // A and M of one v head from the raw products of this wave's triangle blocks (waves 0-3):
 // A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s) for s < t, M[t][s] = exp(G_t - G_s) (q_t . k_s)
 // for s <= t, zero above the diagonal inside the diagonal blocks. The blocks above the
-// diagonal are never written (nothing reads them).
+// diagonal are never written (nothing reads them). Branch-free; the decay uses the hardware
+// exp (relative error <= 4e-6 down to the fp32 underflow of exp(G_t - G_s)).
 __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], const float* G, const float* Bt,
                                         float* A_s, float* M_s, int w, int li, int lg4) {
 #pragma unroll
@@ -397,17 +427,15 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
         if (i >= 10) continue;
         int br, bc;
         tri_block(i, br, bc);
+        const int t0 = 16 * br + 4 * lg4, s = 16 * bc + li;
+        const v4 gt = *reinterpret_cast<const v4*>(G + t0), bt = *reinterpret_cast<const v4*>(Bt + t0);
+        const float gs = G[s];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = 16 * br + 4 * lg4 + r, s = 16 * bc + li;
-            float av = 0.0f, mv = 0.0f;
-            if (s <= t) {
-                const float e = expf(G[t] - G[s]);
-                mv = e * qk[j][r];
-                if (s < t) av = Bt[t] * e * kk[j][r];
-            }
-            A_s[t * kTS + s] = av;
-            M_s[t * kTS + s] = mv;
+            const int t = t0 + r;
+            const float e = __expf(fminf(gt[r] - gs, 0.0f));    // used for s <= t only
+            M_s[t * kTS + s] = s <= t ? e * qk[j][r] : 0.0f;
+            A_s[t * kTS + s] = s < t ? bt[r] * e * kk[j][r] : 0.0f;
         }
     }
 }
@@ -437,6 +465,9 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
     float (*W_s)[kKS] = reinterpret_cast<float (*)[kKS]>(A_s);        // W, over A and T
     float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
     static_assert(kChunk * kKS <= 2 * kChunk * kTS, "W fits over A and T");
+    static_assert(2 * kQKPlane <= kChunk * kKS * 4, "k and q planes fit their tiles");
+    uint8_t* Kp = reinterpret_cast<uint8_t*>(K_s);                     // k rows as split planes
+    uint8_t* Qp = reinterpret_cast<uint8_t*>(Q_s);                     // q rows as split planes
     __shared__ float G_s[kMaxMap][kChunk], B_s[kMaxMap][kChunk], BG_s[kMaxMap][kChunk];
 
     ChunkGeo g;
@@ -445,7 +476,7 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
     const Layer& L = p.L;
     const int src = blockIdx.y, nmap = mapped_count(L, src);
     if (nmap == 0) return;
-    const int lo = p.ws.seq_lo[g.s];
+    const int lo = g.lo;
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);        // wave-uniform: scalar branches
     const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
@@ -464,31 +495,11 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         }
     }
 
-    // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave.
-    {
-        const bool isk = w >= 4;
-        float y0[kConvTok], y1[kConvTok];
-        if (nt > 0) {
-            ConvIn<DC> in;
-            conv_load<DC>(p, g, lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
-            conv_run<DC>(L, in, y0, y1);
-        } else {
-#pragma unroll
-            for (int t = 0; t < kConvTok; ++t) y0[t] = y1[t] = 0.0f;
-        }
-        // All 16 row sums first (independent, so their shuffle latencies overlap), then the
-        // scaled rows; rows past the chunk end are zero.
-        float ss[kConvTok];
-#pragma unroll
-        for (int t = 0; t < kConvTok; ++t) ss[t] = wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t]));
-        const float scale = isk ? 1.0f : L.q_scale;
-        float (*dst)[kKS] = isk ? K_s : Q_s;
-#pragma unroll
-        for (int t = 0; t < kConvTok; ++t) {
-            const float inv = scale / sqrtf(ss[t] + L.l2_eps);
-            *reinterpret_cast<float2*>(&dst[tb + t][c2]) = t < nt ? float2{y0[t] * inv, y1[t] * inv} : float2{0.0f, 0.0f};
-        }
-    }
+    // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave: the loads are issued
+    // first, the decay scan (which needs only the gate inputs) runs while they are in flight.
+    const bool isk = w >= 4;
+    ConvIn<DC> in;
+    conv_load<DC>(p, g, lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
     // Decay scan and beta of v heads w and w + 8.
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -511,12 +522,33 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         E[lane] = expf(glast - lgt);
         E[kChunk + lane] = expf(lgt);
     }
+    {
+        float y0[kConvTok], y1[kConvTok];
+        conv_run<DC>(L, in, y0, y1);
+        // All 16 row sums first (independent, so their shuffle latencies overlap), then the
+        // scaled rows; rows past the chunk end are zero.
+        float ss[kConvTok];
+#pragma unroll
+        for (int t = 0; t < kConvTok; ++t) ss[t] = wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t]));
+        const float scale = isk ? 1.0f : L.q_scale;
+        uint8_t* dst = isk ? Kp : Qp;
+#pragma unroll
+        for (int t = 0; t < kConvTok; ++t) {
+            const float inv = scale * rsqrtf(ss[t] + L.l2_eps);
+            uint32_t hi = 0, lo = 0;
+            if (t < nt) split2(y0[t] * inv, y1[t] * inv, hi, lo);
+            const int o = qk_off(tb + t, c2);
+            *reinterpret_cast<uint32_t*>(dst + o) = hi;
+            *reinterpret_cast<uint32_t*>(dst + kQKPlane + o) = lo;
+        }
+    }
     lds_barrier();
 
-    // Raw K K^T and Q K^T (waves 0-3). MFMA k index of (block 4m + e, lane group g) is
-    // 16 m + 4 g + e for both operands. Waves 4-7 first issue the loads of the first v head's
-    // rows, then write K^T (rows i, k = token t: 8 x 2 fragments) and Q (rows t, k = i:
-    // 4 x 4 fragments) as split fragments.
+    // Raw K K^T and Q K^T (waves 0-3) on split-bf16 MFMA (16x16x32, three bf16 products per
+    // fp32 product), operands straight from the planes: lane (li, lg4) supplies channels
+    // 32 ks + 8 lg4 .. +7 of token row li for both operands. Waves 4-7 first issue the
+    // loads of the first v head's rows, then copy K^T (rows i, k = token t: 8 x 2 fragments)
+    // and Q (rows t, k = i: 4 x 4 fragments) from the planes into split fragments.
     v4 kk[3], qk[3];
     ConvIn<DC> vin;
     if (w < 4) {
@@ -528,17 +560,22 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
             if (i < 10) {
                 int br, bc;
                 tri_block(i, br, bc);
-                const int arow = 16 * br + li;
+                const int arow = 16 * br + li, brow = 16 * bc + li;
 #pragma unroll
-                for (int m = 0; m < kD / 16; ++m) {
-                    const v4 ak = *reinterpret_cast<const v4*>(&K_s[arow][16 * m + 4 * lg4]);
-                    const v4 aq = *reinterpret_cast<const v4*>(&Q_s[arow][16 * m + 4 * lg4]);
-                    const v4 bk = *reinterpret_cast<const v4*>(&K_s[16 * bc + li][16 * m + 4 * lg4]);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        kk[j] = mfma4(ak[e], bk[e], kk[j]);
-                        qk[j] = mfma4(aq[e], bk[e], qk[j]);
-                    }
+                for (int ks = 0; ks < kD / 32; ++ks) {
+                    const int ch = 32 * ks + 8 * lg4, oa = qk_off(arow, ch), ob = qk_off(brow, ch);
+                    const bf8 akh = *reinterpret_cast<const bf8*>(Kp + oa);
+                    const bf8 akl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + oa);
+                    const bf8 aqh = *reinterpret_cast<const bf8*>(Qp + oa);
+                    const bf8 aql = *reinterpret_cast<const bf8*>(Qp + kQKPlane + oa);
+                    const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
+                    const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
+                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akh, bkh, kk[j], 0, 0, 0);
+                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aqh, bkh, qk[j], 0, 0, 0);
+                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akh, bkl, kk[j], 0, 0, 0);
+                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aqh, bkl, qk[j], 0, 0, 0);
+                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akl, bkh, kk[j], 0, 0, 0);
+                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aql, bkh, qk[j], 0, 0, 0);
                 }
             }
             __builtin_amdgcn_sched_barrier(0);       // one block's operands live at a time
@@ -550,20 +587,25 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         for (int u = t4; u < 8 * 2 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
             const int row = 16 * m + (ln & 15);
-            float x[8];
+            uint16_t xh[8], xl[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = K_s[32 * ks + kperm(ln >> 4, e)][row];
-            store_frag(Ktf, m, ks, 2, ln, x);
+            for (int e = 0; e < 8; ++e) {
+                const int o = qk_off(32 * ks + kperm(ln >> 4, e), row);
+                xh[e] = *reinterpret_cast<const uint16_t*>(Kp + o);
+                xl[e] = *reinterpret_cast<const uint16_t*>(Kp + kQKPlane + o);
+            }
+            store_frag_planes(Ktf, m, ks, 2, ln, xh, xl);
         }
         uint16_t* Qf = p.ws.Qf + cs * kFragW;
         for (int u = t4; u < 4 * 4 * kWave; u += 4 * kWave) {
             const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
             const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
-            float x[8];
-            const v4 a = *reinterpret_cast<const v4*>(&Q_s[row][k0]), b = *reinterpret_cast<const v4*>(&Q_s[row][k0 + 16]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
-            store_frag(Qf, m, ks, 4, ln, x);
+            const int oa = qk_off(row, k0), ob = qk_off(row, k0 + 16);
+            const uint2 ah = *reinterpret_cast<const uint2*>(Qp + oa), bh = *reinterpret_cast<const uint2*>(Qp + ob);
+            const uint2 al = *reinterpret_cast<const uint2*>(Qp + kQKPlane + oa);
+            const uint2 bl = *reinterpret_cast<const uint2*>(Qp + kQKPlane + ob);
+            *reinterpret_cast<u4x*>(Qf + frag_at(m, ks, 4, 0, ln)) = u4x{ah.x, ah.y, bh.x, bh.y};
+            *reinterpret_cast<u4x*>(Qf + frag_at(m, ks, 4, 1, ln)) = u4x{al.x, al.y, bl.x, bl.y};
         }
     }
     lds_barrier();
@@ -586,8 +628,6 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         float (*Vb)[kKS] = (mi & 1) ? Q_s : V_s;                        // this head's v rows
         float (*Vn)[kKS] = (mi & 1) ? V_s : Q_s;                        // the next head's
         const bool next = mi + 1 < nmap, conv_next = w >= 4 && next && nt > 0;
-        ConvIn<DC> nin;                    // the next head's conv inputs (waves 4-7)
-        if (conv_next) conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, mi + 1), c2), tb, nt, nin);
 
         // M as fragments (4 x 2 fragments x 64 lanes: one unit per thread); the blocks
         // above the diagonal are zero.
@@ -607,7 +647,7 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
         lds_barrier();                     // M_s is read: T takes its place
 
         // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane =
-        // 16 b + column c); waves 4-7 compute the next head's v rows.
+        // 16 b + column c); waves 4-7 load and compute the next head's v rows.
         if (w == 0) {
             const int b = lane >> 4, cc = lane & 15;
             const float* Ab = A_s + (16 * b) * kTS + 16 * b;
@@ -623,8 +663,14 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
 #pragma unroll
             for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
         } else if (w >= 4 && next) {
+            // The next head's conv inputs are loaded here, where wave 0's substitution
+            // covers their latency (loading them earlier holds ~26 registers longer).
             float y0[kConvTok], y1[kConvTok];
-            if (conv_next) conv_run<DC>(L, nin, y0, y1);
+            if (conv_next) {
+                ConvIn<DC> nin;
+                conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, mi + 1), c2), tb, nt, nin);
+                conv_run<DC>(L, nin, y0, y1);
+            }
 #pragma unroll
             for (int t = 0; t < kConvTok; ++t)
                 *reinterpret_cast<float2*>(&Vn[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
@@ -648,31 +694,53 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
             lds_barrier();
         }
 
-        // W = T (beta Gam K) and U = T (beta V): wave w takes columns 16 w .. 16 w + 15 of
-        // both, all four 16-row tiles; T[t][s] = 0 for s > t, so tile mt stops at k-step
-        // 4 mt + 3.
-        v4 wacc[4], uacc[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) { wacc[mt] = v4{0.f, 0.f, 0.f, 0.f}; uacc[mt] = wacc[mt]; }
+        // U = T (beta V), then W = T (beta Gam K), on split-bf16 MFMA (16x16x32, three bf16
+        // products per fp32 product; one accumulator set live at a time): wave w takes
+        // columns 16 w .. 16 w + 15, all four 16-row tiles. T[t][s] = 0 for s > t, so tile
+        // mt needs the 32-token k-steps up to mt / 2, and the blocks of T above the block
+        // diagonal (never written) are read as zeros. Lane (li, lg4) supplies k = 32 ks +
+        // 8 lg4 .. +7 of row / column li.
         const int col = 16 * w + li;
+        auto t_gemm = [&](bool is_w, v4 (&acc)[4]) {
 #pragma unroll
-        for (int ks = 0; ks < 16; ++ks) {
-            const int sr = 4 * ks + lg4;
-            const float bw = K_s[sr][col] * BG_s[mi][sr], bu = B_s[mi][sr] * Vb[sr][col];
+            for (int mt = 0; mt < 4; ++mt) acc[mt] = v4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) {
-                if (ks > 4 * mt + 3) continue;               // compile-time after unrolling
-                const float a = T_s[(16 * mt + li) * kTS + 4 * ks + lg4];
-                wacc[mt] = mfma4(a, bw, wacc[mt]);
-                uacc[mt] = mfma4(a, bu, uacc[mt]);
+            for (int ks = 0; ks < 2; ++ks) {
+                float bv[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int sr = 32 * ks + 8 * lg4 + e;
+                    bv[e] = is_w ? qk_f32(Kp, sr, col) * BG_s[mi][sr] : B_s[mi][sr] * Vb[sr][col];
+                }
+                bf8 bh, bl;
+                split8(bv, bh, bl);
+#pragma unroll
+                for (int mt = 2 * ks; mt < 4; ++mt) {
+                    const bool live = 2 * ks + (lg4 >> 1) <= mt;    // this lane's 16-token block of T
+                    const float* tr = T_s + (16 * mt + li) * kTS + 32 * ks + 8 * lg4;
+                    const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 4);
+                    float av[8];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) { av[e] = live ? t0[e] : 0.0f; av[e + 4] = live ? t1[e] : 0.0f; }
+                    bf8 ah, al;
+                    split8(av, ah, al);
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[mt], 0, 0, 0);
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[mt], 0, 0, 0);
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[mt], 0, 0, 0);
+                }
             }
-            __builtin_amdgcn_sched_barrier(0);           // bounds the loads hoisted ahead
-        }
-        // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
-        float* Ut = p.ws.Ut + ch * kD * kChunk;
+        };
+        {
+            v4 uacc[4];
+            t_gemm(false, uacc);
+            // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
+            float* Ut = p.ws.Ut + ch * kD * kChunk;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+            for (int mt = 0; mt < 4; ++mt)
+                *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+        }
+        v4 wacc[4];
+        t_gemm(true, wacc);
         lds_barrier();                     // A and T are read: W takes their place
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
