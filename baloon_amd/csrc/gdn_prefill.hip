@@ -56,7 +56,7 @@ struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
-    uint16_t* Wf;        // [NC][h_v] W (64 x 128) as split-bf16 A fragments
+    uint16_t* Wf;        // [NC][h_v] -W (64 x 128) as split-bf16 A fragments
     float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
     uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
     float* G;            // [NC][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
@@ -747,7 +747,8 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
 #pragma unroll
             for (int r = 0; r < 4; ++r) W_s[16 * mt + 4 * lg4 + r][col] = wacc[mt][r];
         lds_barrier();
-        // W as fragments (4 x 4 x 64 = 1024 units, two per thread).
+        // -W as fragments (4 x 4 x 64 = 1024 units, two per thread): negated, so the chain's
+        // D = U - W S accumulates from U.
         uint16_t* Wf = p.ws.Wf + ch * kFragW;
 #pragma unroll
         for (int rep = 0; rep < 2; ++rep) {
@@ -757,7 +758,7 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
             float x[8];
             const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 16]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { x[e] = a[e]; x[e + 4] = b[e]; }
+            for (int e = 0; e < 4; ++e) { x[e] = -a[e]; x[e + 4] = -b[e]; }
             store_frag(Wf, m, ks, 4, ln, x);
         }
         if (next) {
@@ -769,7 +770,7 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
 }
 
 // ---------------------------------------------------------------------------------------
-// chain: one workgroup per (sequence, v head, 16-column state strip), 6 waves
+// chain: one workgroup per (sequence, v head, 16-column state strip), 7 waves
 // ---------------------------------------------------------------------------------------
 // Columns of the state are independent, so a head's chain splits into 8 strips of 16
 // columns, and each strip's workgroup walks its sequence's chunks in order. Roles:
@@ -785,15 +786,17 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
 //   waves 1-4 (output): wave 1 + r computes rows 16 r .. 16 r + 15 of
 //       O = diag(Gam) Q S + M D                        (Q, M from global, one chunk ahead)
 //     from the S and D the state wave handed over.
-//   wave 5 (copy) moves the next chunk's W and K^T fragments (64 KiB) into the other LDS
-//     slot with direct global-to-LDS loads, and waits for them before the barrier.
+//   waves 5, 6 (copy) move the next chunk's W and this chunk's K^T fragments (32 KiB each,
+//     one wave each, so twice the loads are in flight) into LDS with direct global-to-LDS
+//     loads, and wait for them before the barrier.
 // The roles meet at one barrier per chunk. Between barriers c-1 and c the state wave
-// computes chunk c from slot c&1 and writes hand-over slot c&1, the copy wave fills slot
-// (c+1)&1, and the output waves compute chunk c-1 from hand-over slot (c-1)&1. The state
-// wave's code path issues no LDS DMA, so the compiler never makes it wait for the copies.
+// finishes chunk c-1 (K^T from slot (c-1)&1) interleaved with the start of chunk c (W from
+// slot c&1, hand-over slot c&1), the copy waves fill W slot (c+1)&1 and K^T slot c&1, and
+// the output waves compute chunk c-1 from hand-over slot (c-1)&1. The state wave's code
+// path issues no LDS DMA, so the compiler never makes it wait for the copies.
 constexpr int kStrip = 16;                              // state columns per chain workgroup
 constexpr int kStrips = kD / kStrip;                    // 8
-constexpr int kChainWaves = 6;
+constexpr int kChainWaves = 7;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
 constexpr int kOpsBytes = 32 * kPlane;                  // W (4 x 4) or K^T (8 x 2) fragments, 2 planes
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
@@ -801,7 +804,8 @@ constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in f
 constexpr int kChainSink = kPlane;                      // target of the L2 warm-up loads
 constexpr int kChainLds = 4 * kOpsBytes + 2 * kHandBytes + kChainSink;   // 156,672 bytes
 constexpr int kWarmAhead = 2;                           // chunks warmed ahead of their copy
-constexpr int kWarmLoads = 19;                          // warm-up loads per chunk and strip
+constexpr int kWarmLoadsW = 9;                          // warm-up loads per chunk: W-copy wave
+constexpr int kWarmLoadsK = 10;                         //                          K^T-copy wave
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
@@ -905,69 +909,164 @@ __device__ __forceinline__ void mfma4_split(const bf8 (&a)[4][2], const bf8& bh,
     for (int j = 0; j < 4; ++j) acc[j] = mfma_bf16(a[j][1], bh, acc[j]);
 }
 
-// State role, one chunk from slot q, in two parts around the chunk's barrier:
-//   chain_state_a: D = U - W S (S handed over on the way), D handed over, Dg split;
-//   barrier (the output waves take the hand-over);
-//   chain_state_b: S' = Gam_last S + K^T Dg with Dg = diag(exp(G_last - G)) D.
-// Part b of one chunk and part a of the next run back to back with no barrier between
-// them. The fragments of the next k-step (or row-tile group) are read while the current
-// one's MFMAs run.
-__device__ __forceinline__ void chain_state_a(uint8_t* lds, int q, int lane, const v4 (&S)[8], const v4 (&U)[4],
-                                              const v4 (&E)[4], bf8 (&dh)[2], bf8 (&dl)[2]) {
-    v4 acc[4];
+// Interleaves two independent four-tile split products, MFMA by MFMA, so that the pipe
+// always has an accumulator that is not waiting for its previous product.
+__device__ __forceinline__ void mfma4x2_split(const bf8 (&a)[4][2], const bf8& ah, const bf8& al, v4* acc_a,
+                                              const bf8 (&b)[4][2], const bf8& bh, const bf8& bl, v4* acc_b) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = v4{0.f, 0.f, 0.f, 0.f};
-    bf8 fa[4][2], fb[4][2], sh[4], sl[4];
-    auto split_s = [&](int ks) {
-        split_tiles(S[2 * ks], S[2 * ks + 1], sh[ks], sl[ks]);
+    for (int j = 0; j < 4; ++j) {
+        acc_a[j] = mfma_bf16(a[j][0], ah, acc_a[j]);
+        acc_b[j] = mfma_bf16(b[j][0], bh, acc_b[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc_a[j] = mfma_bf16(a[j][0], al, acc_a[j]);
+        acc_b[j] = mfma_bf16(b[j][0], bl, acc_b[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        acc_a[j] = mfma_bf16(a[j][1], ah, acc_a[j]);
+        acc_b[j] = mfma_bf16(b[j][1], bh, acc_b[j]);
+    }
+}
+
+// acc[t] += A_t B for row tiles t = 0, 1 only, split products.
+__device__ __forceinline__ void mfma2_split(const bf8 (&a)[4][2], const bf8& bh, const bf8& bl, v4* acc) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[t] = mfma_bf16(a[t][0], bh, acc[t]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[t] = mfma_bf16(a[t][0], bl, acc[t]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) acc[t] = mfma_bf16(a[t][1], bh, acc[t]);
+}
+
+// State role (wave 0): the strip's whole chunk loop, S (128 x 16) in accumulators.
+// Between barriers c-1 and c (c > c_begin) it finishes chunk c-1,
+//     S <- Gam_{c-1} S + K^T Dg_{c-1}          (K^T from slot (c-1)&1; S arrives scaled)
+// and runs chunk c:
+//     S handed over (split), D = U - W S, D handed over, Dg = E D split, S *= Gam_c.
+// W is stored negated, so the D accumulators start from U. The work is cut into regions
+// of 12 MFMAs, each holding the VALU work (splits, scalings) that can overlap them. Three
+// fragment groups (R0..R2) rotate through the K^T and W fragments, each refilled as soon
+// as its last MFMA has issued.
+__device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t* lds, int lane, int c_begin,
+                                                 int c_end, int h, int j, int lg4, v4 (&S)[8]) {
+    v4 U[4], E[4];
+    float gam;
+    bf8 dh[2], dl[2], sh[4], sl[4];
+    v4 dg2, dg3;                       // Dg row tiles 2, 3, split at the start of part b
+    bf8 R0[4][2], R1[4][2], R2[4][2];
+
+    auto put_s = [&](int q, int ks) {
         lds_put(lds, chain_h_slot(q) + (2 * ks) * kPlane, lane, sh[ks]);
         lds_put(lds, chain_h_slot(q) + (2 * ks + 1) * kPlane, lane, sl[ks]);
     };
-    chain_w_frags(lds, q, 0, lane, fa);
-    split_s(0);
-    chain_w_frags(lds, q, 1, lane, fb);
-    split_s(1);
-    mfma4_split(fa, sh[0], sl[0], acc);
-    chain_w_frags(lds, q, 2, lane, fa);
-    split_s(2);
-    mfma4_split(fb, sh[1], sl[1], acc);
-    chain_w_frags(lds, q, 3, lane, fb);
-    split_s(3);
-    mfma4_split(fa, sh[2], sl[2], acc);
-    mfma4_split(fb, sh[3], sl[3], acc);
-    v4 D[4], Dg[4];
+    // Part b, row tiles 0-3 (K^T k-steps 0, 1 of slot qp in R0, R1); R2 and then R0 take
+    // the row tiles 4-7.
+    auto part_b_lo = [&](int qp) {
+        chain_kt_frags(lds, qp, 0, 0, lane, R0);
+        chain_kt_frags(lds, qp, 1, 0, lane, R1);
+        split_tiles(dg2, dg3, dh[1], dl[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma4_split(R0, dh[0], dl[0], S);
+        __builtin_amdgcn_sched_barrier(0);
+        chain_kt_frags(lds, qp, 0, 1, lane, R2);
+        __builtin_amdgcn_sched_barrier(0);
+        mfma4_split(R1, dh[1], dl[1], S);
+        __builtin_amdgcn_sched_barrier(0);
+        chain_kt_frags(lds, qp, 1, 1, lane, R0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Part b, row tiles 4-7; with A, the split and hand-over of S row tiles 0-3 (final
+    // after part_b_lo) and the reads of W k-steps 0, 1 (slot q) into R1, R2.
+    auto part_b_hi = [&](int q, bool A) {
+        mfma4_split(R2, dh[0], dl[0], S + 4);
+        if (A) {
+            split_tiles(S[0], S[1], sh[0], sl[0]);
+            put_s(q, 0);
+            chain_w_frags(lds, q, 0, lane, R1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma4_split(R0, dh[1], dl[1], S + 4);
+        if (A) {
+            split_tiles(S[2], S[3], sh[1], sl[1]);
+            put_s(q, 1);
+            chain_w_frags(lds, q, 1, lane, R2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Part a from the W products on: D = U + (-W) S, hand-overs, Dg split, S *= Gam.
+    auto part_a = [&](int q) {
+        // W k-step 0 (R1); S row tiles 4, 5 split; S row tiles 0, 1 scaled; W k-step 2 -> R0.
+        mfma4_split(R1, sh[0], sl[0], U);
+        split_tiles(S[4], S[5], sh[2], sl[2]);
+        put_s(q, 2);
+        S[0] *= gam;
+        S[1] *= gam;
+        chain_w_frags(lds, q, 2, lane, R0);
+        __builtin_amdgcn_sched_barrier(0);
+        // W k-step 1 (R2); S row tiles 6, 7 split; S row tiles 2, 3 scaled; W k-step 3 -> R1.
+        mfma4_split(R2, sh[1], sl[1], U);
+        split_tiles(S[6], S[7], sh[3], sl[3]);
+        put_s(q, 3);
+        S[2] *= gam;
+        S[3] *= gam;
+        chain_w_frags(lds, q, 3, lane, R1);
+        __builtin_amdgcn_sched_barrier(0);
+        // W k-steps 2, 3 of row tiles 0, 1 (final after this); S row tiles 4-7 scaled.
+        mfma2_split(R0, sh[2], sl[2], U);
+        mfma2_split(R1, sh[3], sl[3], U);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        D[m] = U[m] - acc[m];
-        Dg[m] = E[m] * D[m];
+        for (int mt = 4; mt < 8; ++mt) S[mt] *= gam;
+        __builtin_amdgcn_sched_barrier(0);
+        // W k-steps 2, 3 of row tiles 2, 3; D tiles 0, 1 handed over (fp32, the output
+        // waves split it) and Dg tiles 0, 1 split.
+        {
+            bf8 a2[4][2], a3[4][2];
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) {
+                a2[0][pl] = R0[2][pl]; a2[1][pl] = R0[3][pl];
+                a3[0][pl] = R1[2][pl]; a3[1][pl] = R1[3][pl];
+            }
+            mfma2_split(a2, sh[2], sl[2], U + 2);
+            mfma2_split(a3, sh[3], sl[3], U + 2);
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = U[m];
+        split_tiles(E[0] * U[0], E[1] * U[1], dh[0], dl[0]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 2; m < 4; ++m)
+            *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = U[m];
+        dg2 = E[2] * U[2];
+        dg3 = E[3] * U[3];
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    chain_load_ug(p, c_begin, h, j, lg4, U, E, gam);
+    lds_barrier();                                            // W of the first chunk in LDS
+    // Chunk c_begin: part a only.
+    split_tiles(S[0], S[1], sh[0], sl[0]);
+    put_s(0, 0);
+    split_tiles(S[2], S[3], sh[1], sl[1]);
+    put_s(0, 1);
+    chain_w_frags(lds, 0, 0, lane, R1);
+    chain_w_frags(lds, 0, 1, lane, R2);
+    __builtin_amdgcn_sched_barrier(0);
+    part_a(0);
+    for (int c = c_begin + 1; c < c_end; ++c) {
+        chain_load_ug(p, c, h, j, lg4, U, E, gam);
+        __builtin_amdgcn_sched_barrier(0);
+        lds_barrier();                                        // barrier c-1
+        const int q = (c - c_begin) & 1;
+        part_b_lo(q ^ 1);
+        part_b_hi(q, true);
+        part_a(q);
     }
-    // D goes over in fp32 (the output waves split it); Dg is split here for part b.
-#pragma unroll
-    for (int m = 0; m < 4; ++m) *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = D[m];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) split_tiles(Dg[2 * ks], Dg[2 * ks + 1], dh[ks], dl[ks]);
-}
-__device__ __forceinline__ void chain_state_b(const uint8_t* lds, int q, int lane, v4 (&S)[8], float gam,
-                                              const bf8 (&dh)[2], const bf8 (&dl)[2]) {
-    // The reads of the next fragment group are pinned ahead of the current group's MFMAs,
-    // so LDS latency hides under them.
-    bf8 f0[4][2], f1[4][2], f2[4][2], f3[4][2];
-    chain_kt_frags(lds, q, 0, 0, lane, f0);
-    chain_kt_frags(lds, q, 1, 0, lane, f1);
-#pragma unroll
-    for (int mt = 0; mt < 8; ++mt) S[mt] *= gam;
-    __builtin_amdgcn_sched_barrier(0);
-    chain_kt_frags(lds, q, 0, 1, lane, f2);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma4_split(f0, dh[0], dl[0], S);
-    __builtin_amdgcn_sched_barrier(0);
-    chain_kt_frags(lds, q, 1, 1, lane, f3);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma4_split(f1, dh[1], dl[1], S);                             // row tiles 0-3 done first
-    __builtin_amdgcn_sched_barrier(0);
-    mfma4_split(f2, dh[0], dl[0], S + 4);
-    __builtin_amdgcn_sched_barrier(0);
-    mfma4_split(f3, dh[1], dl[1], S + 4);
+    lds_barrier();                                            // barrier c_end-1
+    part_b_lo((c_end - 1 - c_begin) & 1);
+    part_b_hi(0, false);
 }
 
 struct ChainOut {
@@ -1010,29 +1109,36 @@ __device__ __forceinline__ void chain_out_step(const PrefillParams& p, const uin
     }
 }
 
-// Copy role: bring this strip's share of chunk c's operands into L2 ahead of their use: an
-// eighth of W, K^T, Q and M (the 8 strips of a head share one XCD and its L2), its own U
-// rows, and G. Direct loads into a sink in LDS, so no register waits for them; always
-// kWarmLoads loads, which the wait before each barrier leaves in flight.
+// Copy role: bring this strip's share of chunk c's operands into L2 ahead of their use (the
+// 8 strips of a head share one XCD and its L2). Direct loads into a sink in LDS, so no
+// register waits for them. The W-copy wave (kWarmLoadsW loads) takes an eighth of W and Q,
+// and the decay factors; the K^T-copy wave (kWarmLoadsK loads) an eighth of K^T and M, and
+// the strip's U rows.
 __device__ __forceinline__ void chain_warm(const PrefillParams& p, lds_u8* sink, int c, int h, int src, int strip,
-                                           int lane) {
+                                           int lane, bool w_wave) {
     const size_t ch = (size_t)c * p.L.h_v + h, cs = (size_t)c * p.L.h_k + src;
-    const uint8_t* W = reinterpret_cast<const uint8_t*>(p.ws.Wf + ch * kFragW) + strip * 4 * kPlane + lane * 16;
-    const uint8_t* K = reinterpret_cast<const uint8_t*>(p.ws.Ktf + cs * kFragKt) + strip * 4 * kPlane + lane * 16;
-    const uint8_t* Q = reinterpret_cast<const uint8_t*>(p.ws.Qf + cs * kFragW) + strip * 4 * kPlane + lane * 16;
-    const uint8_t* M = reinterpret_cast<const uint8_t*>(p.ws.Mf + ch * kFragM) + strip * 2 * kPlane + lane * 16;
-    const uint8_t* U = reinterpret_cast<const uint8_t*>(p.ws.Ut + (ch * kD + strip * kStrip) * kChunk) + lane * 16;
-    const uint8_t* G = reinterpret_cast<const uint8_t*>(p.ws.G + ch * 2 * kChunk) + (lane & 31) * 16;
+    if (w_wave) {
+        const uint8_t* W = reinterpret_cast<const uint8_t*>(p.ws.Wf + ch * kFragW) + strip * 4 * kPlane + lane * 16;
+        const uint8_t* Q = reinterpret_cast<const uint8_t*>(p.ws.Qf + cs * kFragW) + strip * 4 * kPlane + lane * 16;
+        const uint8_t* G = reinterpret_cast<const uint8_t*>(p.ws.G + ch * 2 * kChunk) + (lane & 31) * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        __builtin_amdgcn_global_load_lds(W + i * kPlane, sink, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(K + i * kPlane, sink, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(Q + i * kPlane, sink, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(U + i * kPlane, sink, 16, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(W + i * kPlane, sink, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(Q + i * kPlane, sink, 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(G, sink, 16, 0, 0);
+    } else {
+        const uint8_t* K = reinterpret_cast<const uint8_t*>(p.ws.Ktf + cs * kFragKt) + strip * 4 * kPlane + lane * 16;
+        const uint8_t* M = reinterpret_cast<const uint8_t*>(p.ws.Mf + ch * kFragM) + strip * 2 * kPlane + lane * 16;
+        const uint8_t* U = reinterpret_cast<const uint8_t*>(p.ws.Ut + (ch * kD + strip * kStrip) * kChunk) + lane * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_global_load_lds(K + i * kPlane, sink, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(U + i * kPlane, sink, 16, 0, 0);
+        }
+        __builtin_amdgcn_global_load_lds(M, sink, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(M + kPlane, sink, 16, 0, 0);
     }
-    __builtin_amdgcn_global_load_lds(M, sink, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(M + kPlane, sink, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(G, sink, 16, 0, 0);
 }
 
 // s_waitcnt that waits until at most N vector memory operations are outstanding (gfx9
@@ -1068,31 +1174,7 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
         v4 S[8];
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) S[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
-        v4 U[4], E[4];
-        float gam;
-        bf8 dh[2], dl[2];
-        chain_load_ug(p, c_begin, h, j0 + li, lg4, U, E, gam);
-        lds_barrier();                                            // W of the first chunk in LDS
-        // Chunk c: part a, barrier c, part b. U and E of chunk c+1 are loaded as soon as part
-        // a of chunk c has used them (unconditionally: past the last chunk they re-read it).
-        // Two chunks per loop trip, so that part b of the first and part a of the second
-        // share a basic block and can overlap.
-        auto chunk = [&](int c) {
-            const int q = (c - c_begin) & 1;
-            chain_state_a(lds, q, lane, S, U, E, dh, dl);
-            const float g = gam;
-            __builtin_amdgcn_sched_barrier(0);
-            chain_load_ug(p, min(c + 1, c_end - 1), h, j0 + li, lg4, U, E, gam);
-            __builtin_amdgcn_sched_barrier(0);
-            lds_barrier();                                        // barrier c
-            chain_state_b(lds, q, lane, S, g, dh, dl);
-        };
-        int c = c_begin;
-        for (; c + 1 < c_end; c += 2) {
-            chunk(c);
-            chunk(c + 1);
-        }
-        if (c < c_end) chunk(c);
+        chain_state_role(p, lds, lane, c_begin, c_end, h, j0 + li, lg4, S);
 #pragma unroll
         for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
     } else if (w <= 4) {
@@ -1110,26 +1192,32 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
             __builtin_amdgcn_sched_barrier(0);
         }
     } else {
+        const bool w_wave = w == 5;                               // wave 5: W; wave 6: K^T
         lds_u8* lds3 = (lds_u8*)lds;                              // the copies address LDS directly
         lds_u8* sink = lds3 + 4 * kOpsBytes + 2 * kHandBytes;
         auto w_of = [&](int cc) { return p.ws.Wf + ((size_t)cc * L.h_v + h) * kFragW; };
         auto kt_of = [&](int cc) { return p.ws.Ktf + ((size_t)cc * L.h_k + src) * kFragKt; };
         // Before the first barrier: W of the first chunk. Between barriers c-1 and c: W of
-        // chunk c+1 (used before barrier c+1) and K^T of chunk c (used after barrier c); the
+        // chunk c+1 (used after barrier c) and K^T of chunk c (used after barrier c); the
         // slots they replace were last read before barrier c-1.
-        chain_copy(lds3 + chain_w_slot(0), w_of(c_begin), lane);
+        if (w_wave) chain_copy(lds3 + chain_w_slot(0), w_of(c_begin), lane);
 #pragma unroll
-        for (int a = 1; a <= kWarmAhead; ++a) chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane);
-        wait_vmcnt<kWarmAhead * kWarmLoads>();                   // the copies have landed in LDS
-        // Bare barriers in this role: the explicit waits cover the copies, and a release
-        // fence would also wait for the warm-up loads (LDS DMA counts as LDS writes).
+        for (int a = 1; a <= kWarmAhead; ++a)
+            chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane, w_wave);
+        // The copies have landed in LDS; the warm-ups may still be in flight. Bare barriers
+        // in this role: a release fence would also wait for the warm-up loads (LDS DMA counts
+        // as LDS writes).
+        if (w_wave) wait_vmcnt<kWarmAhead * kWarmLoadsW>();
         __builtin_amdgcn_s_barrier();
         for (int c = c_begin; c < c_end; ++c) {
             const int q = (c - c_begin) & 1;
-            if (c + 1 < c_end) chain_copy(lds3 + chain_w_slot(q ^ 1), w_of(c + 1), lane);
-            chain_copy(lds3 + chain_k_slot(q), kt_of(c), lane);
-            chain_warm(p, sink, min(c + 1 + kWarmAhead, c_end - 1), h, src, strip, lane);
-            wait_vmcnt<kWarmLoads>();                            // this trip's copies done, its warm-ups may not be
+            if (w_wave) {
+                if (c + 1 < c_end) chain_copy(lds3 + chain_w_slot(q ^ 1), w_of(c + 1), lane);
+            } else {
+                chain_copy(lds3 + chain_k_slot(q), kt_of(c), lane);
+            }
+            chain_warm(p, sink, min(c + 1 + kWarmAhead, c_end - 1), h, src, strip, lane, w_wave);
+            if (w_wave) wait_vmcnt<kWarmLoadsW>(); else wait_vmcnt<kWarmLoadsK>();   // this trip's copies done
             __builtin_amdgcn_s_barrier();                         // barrier c
         }
         __builtin_amdgcn_s_waitcnt(0);
