@@ -100,6 +100,9 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
     else if (tid < 128 + kHalf / 2) { ch = v_channel(L, h, hf * kHalf + 2 * (tid - 128)); col = 2 * (tid - 128); }
     const bool conv_thread = tid < 128 + kHalf / 2;
     ConvPair<DC> cp;
+    // The inputs of all K tokens are loaded at once (rows past K repeat row K-1), so the
+    // token loop below never waits for a load it issued itself.
+    uint32_t xk[kMaxWindow];
     if (conv_thread) {
         const uint32_t* hp = reinterpret_cast<const uint32_t*>(p.conv_state + ((size_t)bseq * L.C + ch) * (DC - 1));
 #pragma unroll
@@ -107,7 +110,9 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
         const uint32_t* wp = reinterpret_cast<const uint32_t*>(L.conv_w + (size_t)ch * DC);
 #pragma unroll
         for (int i = 0; i < DC; ++i) cp.w[i] = wp[i];
-        cp.x = *reinterpret_cast<const uint32_t*>(p.x + (size_t)bseq * K * L.C + ch);
+#pragma unroll
+        for (int t = 0; t < kMaxWindow; ++t)
+            xk[t] = *reinterpret_cast<const uint32_t*>(p.x + ((size_t)bseq * K + min(t, K - 1)) * L.C + ch);
     }
 
     const v4f* tile = reinterpret_cast<const v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
@@ -120,16 +125,17 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
     if (conv_thread) {
         float* dst = tid < 64 ? q_s[0] : tid < 128 ? k_s[0] : v_s[0];
         const int stride = tid < 128 ? kD : kHalf;
-        for (int t = 0; t < K; ++t) {
-            const size_t row = (size_t)bseq * K + t;
+#pragma unroll
+        for (int t = 0; t < kMaxWindow; ++t) {
+            if (t >= K) break;
             float y0, y1;
             uint32_t nh[DC - 1];
+            cp.x = xk[t];
             conv_pair_eval<DC>(L, cp, y0, y1, nh);
             dst[t * stride + col] = y0;
             dst[t * stride + col + 1] = y1;
 #pragma unroll
             for (int i = 0; i < DC - 1; ++i) cp.h[i] = nh[i];
-            if (t + 1 < K) cp.x = *reinterpret_cast<const uint32_t*>(p.x + (row + 1) * L.C + ch);
             if (w < 2) {                                       // wave-uniform: q (wave 0), k (wave 1)
                 const float r = wave_sum(fmaf(y0, y0, y1 * y1));
                 if (lane == 0) (w == 0 ? sq_s : sk_s)[t] = r;
