@@ -22,19 +22,21 @@
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
 //                  the chunk table (sequence and first token of each chunk)
 //   chunk_kernel   per (chunk, q/k head): conv (history from conv_state at sequence starts),
-//                  L2 norms of q and k; K K^T and Q K^T on fp32 MFMA (lower block triangle),
-//                  once for all the v heads mapped to the q/k head; then per v head its
-//                  decay factors and beta, its v rows, A and M, T = (I + A)^-1 by a blocked
-//                  MFMA inverse, W = T diag(beta Gam) K and U = T diag(beta) V as MFMA GEMMs;
-//                  the chain's operands W, M, K^T, Q written as split-bf16 MFMA fragments
+//                  L2 norms of q and k; K K^T and Q K^T (lower block triangle) once for all
+//                  the v heads mapped to the q/k head; then per v head its decay factors and
+//                  beta, its v rows, A and M, T = (I + A)^-1 by a blocked inverse (fp32
+//                  MFMA block products), W = T diag(beta Gam) K and U = T diag(beta) V; the
+//                  chain's operands W (negated, so the chain's D accumulates from U), M,
+//                  K^T and Q written as split-bf16 MFMA fragments, U^T in fp32
 //   commit_kernel  per sequence and channel: the new rolling conv history
 //   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
-//                  One wave carries the strip in MFMA accumulators (D and S' on split-bf16
-//                  MFMA, three bf16 products per fp32 product) with no barrier on its data
-//                  path; four waves compute the outputs from the S and D it hands over; one
-//                  wave copies the next chunk's W and K^T into LDS with direct loads.
-// fp32 MFMA for the chunk-local algebra and split-bf16 MFMA for the chain keep the chunked
-// result within ~1e-5 (state) of the token-by-token recurrence in double.
+//                  One wave carries the strip in MFMA accumulators with no barrier on its
+//                  data path; four waves compute the outputs from the S and D it hands over;
+//                  two waves copy the next chunk's W and the current chunk's K^T into LDS
+//                  with direct loads and warm L2 ahead.
+// Every dense product except the inverse's block products runs on split-bf16 MFMA (three
+// bf16 products per fp32 product, ~2^-16 relative error); the chunked result stays within
+// ~1e-5 (state) of the token-by-token recurrence in double.
 #include "gdn_common.h"
 
 namespace ixg {
@@ -444,13 +446,14 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
 // its own global stores):
 //   gate inputs of the v heads | q and k rows of the chunk: conv, L2 norm, q scale, into LDS
 //   (zero past the chunk end) | decay scan and beta of each v head | raw K K^T and Q K^T of
-//   the lower block triangle on fp32 MFMA, kept in registers, while the other waves write
-//   K^T and Q as split fragments | then, per mapped v head: M as fragments | T = (I + A)^-1:
-//   the four 16 x 16 diagonal blocks by substitution (one wave, while four others compute
-//   the next head's v rows), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj in
-//   three dependency levels of fp32 MFMA block products | W = T diag(beta Gam) K and
-//   U = T diag(beta) V as fp32 MFMA GEMMs (the zero blocks of T skipped) | U^T stored from
-//   the MFMA layout, W through LDS into fragments | A and M of the next head.
+//   the lower block triangle on split-bf16 MFMA, kept in registers, while the other waves
+//   write K^T and Q as split fragments | then, per mapped v head: M as fragments |
+//   T = (I + A)^-1: the four 16 x 16 diagonal blocks by substitution (one wave, while four
+//   others compute the next head's v rows), then the off-diagonal blocks
+//   T_ij = -T_ii sum_k A_ik T_kj in three dependency levels of fp32 MFMA block products |
+//   U = T diag(beta) V and W = T diag(beta Gam) K as split-bf16 MFMA GEMMs (the zero blocks
+//   of T skipped) | U^T stored from the MFMA layout, W through LDS into fragments | A and M
+//   of the next head.
 // The v rows of even and odd heads alternate between two tiles (the odd one is the q tile,
 // free once the triangle and the Q fragments are done).
 template <int DC>
