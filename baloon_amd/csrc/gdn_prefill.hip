@@ -28,12 +28,12 @@
 //                  MFMA block products), W = T diag(beta Gam) K and U = T diag(beta) V; the
 //                  chain's operands W (negated, so the chain's D accumulates from U), M,
 //                  K^T and Q written as split-bf16 MFMA fragments, U^T in fp32
-//   commit_kernel  per sequence and channel: the new rolling conv history
 //   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
 //                  One wave carries the strip in MFMA accumulators with no barrier on its
 //                  data path; four waves compute the outputs from the S and D it hands over;
 //                  two waves copy the next chunk's W and the current chunk's K^T into LDS
-//                  with direct loads and warm L2 ahead.
+//                  with direct loads and warm L2 ahead; before the first chunk the K^T
+//                  wave writes the new rolling conv history of the pair's share of channels.
 // Every dense product except the inverse's block products runs on split-bf16 MFMA (three
 // bf16 products per fp32 product, ~2^-16 relative error); the chunked result stays within
 // ~1e-5 (state) of the token-by-token recurrence in double.
@@ -283,16 +283,13 @@ __device__ __forceinline__ void conv_run(const Layer& L, ConvIn<DC> in, float (&
 }
 
 // ---------------------------------------------------------------------------------------
-// commit: the rolling conv history after each sequence, one thread per (sequence, channel)
+// commit: the rolling conv history of channel ch after sequence s, tokens lo .. lo+len-1
+// (len > 0); run by the chain kernel, which starts after the chunk kernel has read the old
+// history
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(256) commit_kernel(const PrefillParams p) {
+__device__ __forceinline__ void commit_history(const PrefillParams& p, int ch, int lo, int len, int s) {
     const Layer& L = p.L;
-    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (idx >= (size_t)p.n_seq * L.C) return;
-    const int s = (int)(idx / L.C), ch = (int)(idx % L.C);
-    const int lo = p.ws.seq_lo[s], len = p.ws.seq_lo[s + 1] - lo;
-    if (len == 0) return;
-    uint16_t* st = p.conv_state + idx * (L.dc - 1);
+    uint16_t* st = p.conv_state + ((size_t)s * L.C + ch) * (L.dc - 1);
     // extended history [old (dc-1 values) | the sequence's inputs]; the new history is its
     // last dc-1 entries, i.e. entries len .. len+dc-2. An entry below dc-1 is old history.
     const uint16_t o0 = st[0], o1 = L.dc > 2 ? st[1] : (uint16_t)0, o2 = L.dc > 3 ? st[2] : (uint16_t)0;
@@ -1165,6 +1162,7 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     if (pair >= p.n_seq * L.h_v) return;
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
     const int c_begin = p.ws.chunk_off[s], c_end = p.ws.chunk_off[s + 1];
+    const int seq_lo = p.ws.seq_lo[s], seq_hi = p.ws.seq_lo[s + 1];
     if (c_begin >= c_end) return;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
@@ -1182,7 +1180,6 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
         for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
     } else if (w <= 4) {
         const int r = w - 1;
-        const int seq_lo = p.ws.seq_lo[s], seq_hi = p.ws.seq_lo[s + 1];
         ChainOut x;
         chain_load_qm(p, c_begin, h, src, r, lane, x.qf, x.mf, x.g);
         lds_barrier();
@@ -1207,6 +1204,14 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
 #pragma unroll
         for (int a = 1; a <= kWarmAhead; ++a)
             chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane, w_wave);
+        if (!w_wave) {
+            // The new rolling conv history (nothing in this kernel reads conv_state, and the
+            // chunk kernel has read the old history): the sequence's h_v * 8 workgroups split
+            // its C channels into contiguous ranges. Its round trip overlaps the W copy.
+            const int G = L.h_v * kStrips, g = h * kStrips + strip, per = (L.C + G - 1) / G;
+            const int ch_hi = min(L.C, (g + 1) * per);
+            for (int ch = g * per + lane; ch < ch_hi; ch += kWave) commit_history(p, ch, seq_lo, seq_hi - seq_lo, s);
+        }
         // The copies have landed in LDS; the warm-ups may still be in flight. Bare barriers
         // in this role: a release fence would also wait for the warm-up loads (LDS DMA counts
         // as LDS writes).
@@ -1299,9 +1304,6 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
         case 3: hipLaunchKernelGGL(chunk_kernel<3>, kgrid, dim3(kChunkThreads), 0, s, p); break;
         default: hipLaunchKernelGGL(chunk_kernel<4>, kgrid, dim3(kChunkThreads), 0, s, p); break;
     }
-    // after the chunk kernel, which reads the old history at sequence starts
-    const size_t nch = (size_t)n_seq * p.L.C;
-    hipLaunchKernelGGL(commit_kernel, dim3((unsigned)((nch + 255) / 256)), dim3(256), 0, s, p);
     const long long groups = (pairs + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
     switch ((p.o ? 1 : 0) | (p.o_bf16 ? 2 : 0)) {
