@@ -10,14 +10,18 @@
 //
 // At decode batch sizes the product is a skinny GEMM that streams W once from HBM (about 2
 // FLOP per weight byte at B = 64), so the work is moving bytes, not MFMA throughput. One
-// workgroup owns 64 output columns and 64 rows; its 8 waves split K into contiguous ranges,
-// and each wave runs v_mfma_f32_16x16x32_bf16 on all 4 x 4 tiles of the 64 x 64 output with
-// operands loaded straight from memory. The k-slots of the instruction are filled so that a
-// lane's two consecutive k-steps are adjacent in memory: for a 64-k super-step, lanes
-// 16 g .. 16 g + 15 hold k = 16 g .. 16 g + 15 of their row (8 for each of two MFMAs), so four
-// lanes read one full 128-byte line of each row per super-step. A and B use the same slot
-// assignment, so the products are unchanged. The 8 partial tiles are added in wave order
-// through LDS, so the result does not depend on timing.
+// workgroup owns a 64 x 64 output tile over the whole of K. Two producer waves copy 64-k
+// stages of the tile's 64 activation rows (one wave) and 64 weight rows (the other) into a
+// ring of LDS stages with direct global-to-LDS loads: every load instruction moves 1 KiB =
+// 8 whole 128-byte row segments, and the loads of three stages are in flight at once.
+// Four consumer waves each own a 32 x 32 quarter of the tile and run
+// v_mfma_f32_16x16x32_bf16 on operands read from the ring; they issue no LDS DMA, so the
+// compiler never makes their LDS reads wait for the copies in flight. Producers and
+// consumers meet at one barrier per stage. In LDS the 16-byte chunk c of tile row r sits
+// at position c ^ (r & 7) of the row's 128 bytes, so the eight rows an operand read touches
+// at once fall in different banks; the producers apply the swizzle by choosing which chunk
+// each lane fetches. The summation order over K is fixed, so results do not depend on
+// timing.
 #include "gdn_common.h"
 
 namespace ixg {
@@ -25,11 +29,18 @@ namespace {
 
 constexpr int kNt = 64;                 // output columns per workgroup (4 MFMA n-tiles)
 constexpr int kMt = 64;                 // rows per workgroup (4 MFMA m-tiles)
-constexpr int kWaves = 8;               // contiguous K ranges
-constexpr int kSuper = 64;              // k per super-step (two MFMA k-steps)
+constexpr int kKd = 64;                 // k per stage (two MFMA k-steps)
+constexpr int kRowB = 2 * kKd;          // bytes of one tile row per stage
+constexpr int kRowsPerCopy = 1024 / kRowB;          // tile rows per 1 KiB load instruction
+constexpr int kHalf = 64 * kRowB;       // bytes of one operand tile per stage
+constexpr int kStage = 2 * kHalf;       // activation tile, then weight tile
+constexpr int kRing = 4;                // stages in the LDS ring (64 KiB)
+constexpr int kCons = 4, kProd = 2;     // consumer and producer waves
+constexpr int kCopies = 2 * (64 / kRowsPerCopy) / kProd;   // load instructions per producer and stage
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 struct InProj {
     const uint16_t* h;          // [B][K]
@@ -51,71 +62,114 @@ __device__ __forceinline__ void store_out(const InProj& p, int row, int col, flo
     if (p.y) p.y[(size_t)row * p.N + col] = v;
 }
 
-__global__ void __launch_bounds__(kWaves * kWave) in_proj_kernel(const InProj p) {
-    __shared__ float red[kWaves][kMt][kNt + 1];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 
-    const int tid = threadIdx.x, wv = tid / kWave, lane = tid & (kWave - 1);
-    const int r16 = lane & 15, kg = lane >> 4;
+// Byte offset in an operand tile of 16-byte chunk c of row r.
+__device__ __forceinline__ int ring_off(int r, int c) { return r * kRowB + ((c ^ (r & 7)) << 4); }
+
+__global__ void __launch_bounds__((kCons + kProd) * kWave) in_proj_kernel(const InProj p) {
+    __shared__ __align__(16) uint8_t lds[kRing * kStage];
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int n0 = blockIdx.x * kNt, m0 = blockIdx.y * kMt;
-    const int nsup = p.K / kSuper;                                   // super-steps in K
-    const int s_lo = wv * nsup / kWaves, s_hi = (wv + 1) * nsup / kWaves;
+    const int nst = p.K / kKd;
 
-    // Operand rows of this lane (clamped into range: rows and columns past the end compute
-    // values that are never stored).
-    const bf16x8* ap[4];
-    const bf16x8* bp[4];
+    if (w >= kCons) {
+        // Producer: the first half of the producer waves copy activation rows, the second
+        // half weight rows, kCopies load instructions each. Instruction g of a tile covers
+        // rows kRowsPerCopy g .. +kRowsPerCopy-1; lane l writes position l % (kRowB / 16) of
+        // row kRowsPerCopy g + l / (kRowB / 16), so it fetches chunk position ^ (row & 7) of
+        // that row. Rows past the end are clamped (their results are never stored).
+        const int pw = w - kCons;
+        const bool act = pw < kProd / 2;
+        const int g0 = (pw % (kProd / 2)) * kCopies;          // first load instruction of this wave
+        const int rr = lane / (kRowB / 16), pos = lane % (kRowB / 16);
+        const uint8_t* src[kCopies];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = min(m0 + 16 * i + r16, p.B - 1), c = min(n0 + 16 * i + r16, p.N - 1);
-        ap[i] = reinterpret_cast<const bf16x8*>(p.h + (size_t)r * p.K + 16 * kg);
-        bp[i] = reinterpret_cast<const bf16x8*>(p.w + (size_t)c * p.K + 16 * kg);
-    }
-
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-#pragma unroll 2
-    for (int sp = s_lo; sp < s_hi; ++sp) {
-        bf16x8 av[4][2], bv[4][2];
-        const int o = sp * (kSuper / 8);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int q = 0; q < 2; ++q) { bv[i][q] = bp[i][o + q]; av[i][q] = ap[i][o + q]; }
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-                for (int ni = 0; ni < 4; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mi][q], bv[ni][q], acc[mi][ni], 0, 0, 0);
-    }
-
-    // acc[mi][ni][r] is output (row 16 mi + 4 kg + r, column 16 ni + r16) of this wave's K range.
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) red[wv][16 * mi + 4 * kg + r][16 * ni + r16] = acc[mi][ni][r];
-    __syncthreads();
-    // 4096 outputs, 8 per thread: row tid / 8, columns 8 (tid % 8) .. +7.
-    const int row = tid >> 3, c0 = 8 * (tid & 7);
-    if (m0 + row < p.B) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int col = n0 + c0 + e;
-            if (col < p.N) {
-                float v = red[0][row][c0 + e];
-#pragma unroll
-                for (int q = 1; q < kWaves; ++q) v += red[q][row][c0 + e];
-                store_out(p, m0 + row, col, v);
-            }
+        for (int j = 0; j < kCopies; ++j) {
+            const int r = kRowsPerCopy * (g0 + j) + rr;
+            const int chunk = pos ^ (r & 7);
+            const int row = act ? min(m0 + r, p.B - 1) : min(n0 + r, p.N - 1);
+            src[j] = reinterpret_cast<const uint8_t*>(act ? p.h : p.w) + (size_t)row * p.K * 2 + chunk * 16;
         }
+        lds_u8* dst = (lds_u8*)lds + (act ? 0 : kHalf) + g0 * 1024;
+        // Virtual stage v goes to ring slot v % kRing; stages past the end repeat the last one,
+        // so every trip issues the same number of loads.
+        auto issue = [&](int v) {
+            const int sv = min(v, nst - 1);
+            lds_u8* d = dst + (v % kRing) * kStage;
+#pragma unroll
+            for (int j = 0; j < kCopies; ++j) __builtin_amdgcn_global_load_lds(src[j] + sv * kRowB, d + j * 1024, 16, 0, 0);
+        };
+#pragma unroll
+        for (int v = 0; v < kRing - 1; ++v) issue(v);
+        wait_vmcnt<kCopies * (kRing - 2)>();                   // stage 0 landed
+        __builtin_amdgcn_s_barrier();
+        for (int st = 0; st < nst; ++st) {
+            // The slot of stage st + kRing - 1 held stage st - 1, read before this barrier.
+            issue(st + kRing - 1);
+            wait_vmcnt<kCopies * (kRing - 2)>();               // stage st + 1 landed
+            __builtin_amdgcn_s_barrier();
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
     }
+
+    // Consumer wave w: rows 32 (w & 1) .., columns 32 (w >> 1) .. of the tile.
+    const int li = lane & 15, lg = lane >> 4;
+    const int rbase = 32 * (w & 1), cbase = 32 * (w >> 1);
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // Operand offsets inside a stage: lane (li, lg) of k-step ks holds k = 32 ks + 8 lg .. +7
+    // of its row (chunk 4 ks + lg).
+    constexpr int kSteps = kKd / 32;
+    int ao[2][kSteps], bo[2][kSteps];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < kSteps; ++ks) {
+            ao[t][ks] = ring_off(rbase + 16 * t + li, 4 * ks + lg);
+            bo[t][ks] = kHalf + ring_off(cbase + 16 * t + li, 4 * ks + lg);
+        }
+    lds_barrier();
+    for (int st = 0; st < nst; ++st) {
+        const uint8_t* sp = lds + (st % kRing) * kStage;
+        bf16x8 av[2][kSteps], bv[2][kSteps];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ks = 0; ks < kSteps; ++ks) {
+                av[t][ks] = *reinterpret_cast<const bf16x8*>(sp + ao[t][ks]);
+                bv[t][ks] = *reinterpret_cast<const bf16x8*>(sp + bo[t][ks]);
+            }
+#pragma unroll
+        for (int ks = 0; ks < kSteps; ++ks)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < 2; ++nt)
+                    acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][ks], bv[nt][ks], acc[mt][nt], 0, 0, 0);
+        lds_barrier();                                          // this slot may be refilled
+    }
+
+    // acc[mt][nt][r] is output (row rbase + 16 mt + 4 lg + r, column cbase + 16 nt + li).
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + rbase + 16 * mt + 4 * lg + r, col = n0 + cbase + 16 * nt + li;
+                if (row < p.B && col < p.N) store_out(p, row, col, acc[mt][nt][r]);
+            }
 }
 
 }  // namespace
@@ -133,7 +187,7 @@ extern "C" hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, c
     using namespace ixg;
     const hipError_t e = ix_gdn_check_cfg_(cfg);
     if (e != hipSuccess) return e;
-    if (B <= 0 || B > 65535 * kMt || hidden <= 0 || hidden % kSuper != 0) return hipErrorInvalidValue;
+    if (B <= 0 || B > 65535 * kMt || hidden <= 0 || hidden % kKd != 0) return hipErrorInvalidValue;
     if (!h || !w || !x || !z || !a || !b) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(h) | reinterpret_cast<uintptr_t>(w)) & 15) return hipErrorInvalidValue;
     if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(a) |
@@ -147,6 +201,6 @@ extern "C" hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, c
     p.hv = cfg->h_v;
     p.N = p.C + p.Z + 2 * p.hv;
     const dim3 grid((unsigned)((p.N + kNt - 1) / kNt), (unsigned)((B + kMt - 1) / kMt));
-    hipLaunchKernelGGL(in_proj_kernel, grid, dim3(kWaves * kWave), 0, s, p);
+    hipLaunchKernelGGL(in_proj_kernel, grid, dim3((kCons + kProd) * kWave), 0, s, p);
     return hipGetLastError();
 }

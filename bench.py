@@ -200,7 +200,7 @@ def in_proj_bench(args, hidden=2048, iters=100):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(0x6D4E0006)
-    nw = 4                                                    # rotated weight copies (MALL defeated)
+    nw = 8                                                    # rotated weight copies: 8 x 50.6 MB exceeds the 256 MB MALL
     ws = [(torch.randn(N, hidden, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(nw)]
     h = torch.randn(B, hidden, generator=g, device=dev).to(torch.bfloat16)
     x = torch.empty(B, cfg.channels, dtype=torch.bfloat16, device=dev)

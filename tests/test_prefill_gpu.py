@@ -76,6 +76,19 @@ def test_varlen_with_empty_and_short_sequences():
     check(oracle.make_cfg(), [0, 0, 1, 65, 195, 198, 198, 260], inputs.seed_for(4))
 
 
+@pytest.mark.parametrize("n", [1100, 4400])
+def test_more_sequences_than_one_plan_pass(n):
+    # The offsets are scanned in passes of 1024 threads, the running maximum and chunk count
+    # carried between passes (two and five passes here). Most sequences are empty or a few
+    # tokens long; a few span several chunks around pass boundaries.
+    lens = np.floor(inputs.Gen(inputs.seed_for(4) + n).uniform(0x51, (n,)) * 5).astype(np.int64)
+    for b in (1024, 4096):
+        if b < n:
+            lens[b - 4:b + 3] = [70, 0, 130, 1, 64, 0, 65]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    check(oracle.make_cfg(h_k=1, h_v=1), cu, inputs.seed_for(4) + n, state_std=0.0)
+
+
 @pytest.mark.parametrize("kw", [
     dict(head_map=1),
     dict(conv_act=1),
