@@ -85,6 +85,7 @@ def window_case(cfg, B, K, accepted, seed):
     (4, [0, 1, 2, 3, 4, 4]),
     (1, [1, 0, -2, 7, 1, 1]),
     (8, [8, 5, 0, 13, 3, -1]),
+    (16, [16, 3, 0, 16, 15, 7]),                      # the largest window
 ])
 def test_window_verify_and_commit(K, accepted):
     window_case(bx.make_cfg(), 6, K, accepted, inputs.seed_for(2) + 50 + K)
