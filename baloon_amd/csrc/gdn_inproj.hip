@@ -14,7 +14,7 @@
 // stages of the tile's 64 activation rows (one wave) and 64 weight rows (the other) into a
 // ring of LDS stages with direct global-to-LDS loads: every load instruction moves 1 KiB =
 // 8 whole 128-byte row segments, and the loads of three stages are in flight at once.
-// Four consumer waves each own a 32 x 32 quarter of the tile and run
+// Eight consumer waves each own a 32 x 16 eighth of the tile and run
 // v_mfma_f32_16x16x32_bf16 on operands read from the ring; they issue no LDS DMA, so the
 // compiler never makes their LDS reads wait for the copies in flight. Producers and
 // consumers meet at one barrier per stage. In LDS the 16-byte chunk c of tile row r sits
@@ -35,7 +35,9 @@ constexpr int kRowsPerCopy = 1024 / kRowB;          // tile rows per 1 KiB load 
 constexpr int kHalf = 64 * kRowB;       // bytes of one operand tile per stage
 constexpr int kStage = 2 * kHalf;       // activation tile, then weight tile
 constexpr int kRing = 4;                // stages in the LDS ring (64 KiB)
-constexpr int kCons = 4, kProd = 2;     // consumer and producer waves
+constexpr int kCons = 8, kProd = 2;     // consumer and producer waves
+constexpr int kTM = 2, kTN = 1;         // 16 x 16 output tiles per consumer wave (rows, columns)
+static_assert(2 * 16 * kTM == kMt && (kCons / 2) * 16 * kTN == kNt, "the consumer waves cover the tile");
 constexpr int kCopies = 2 * (64 / kRowsPerCopy) / kProd;   // load instructions per producer and stage
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -120,51 +122,51 @@ __global__ void __launch_bounds__((kCons + kProd) * kWave) in_proj_kernel(const 
         return;
     }
 
-    // Consumer wave w: rows 32 (w & 1) .., columns 32 (w >> 1) .. of the tile.
+    // Consumer wave w: rows 32 (w & 1) .. +31, columns 16 (w >> 1) .. +15 of the tile.
     const int li = lane & 15, lg = lane >> 4;
-    const int rbase = 32 * (w & 1), cbase = 32 * (w >> 1);
-    f32x4 acc[2][2];
+    const int rbase = 16 * kTM * (w & 1), cbase = 16 * kTN * (w >> 1);
+    f32x4 acc[kTM][kTN];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < kTM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nt = 0; nt < kTN; ++nt) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // Operand offsets inside a stage: lane (li, lg) of k-step ks holds k = 32 ks + 8 lg .. +7
     // of its row (chunk 4 ks + lg).
     constexpr int kSteps = kKd / 32;
-    int ao[2][kSteps], bo[2][kSteps];
+    int ao[kTM][kSteps], bo[kTN][kSteps];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int ks = 0; ks < kSteps; ++ks) {
 #pragma unroll
-        for (int ks = 0; ks < kSteps; ++ks) {
-            ao[t][ks] = ring_off(rbase + 16 * t + li, 4 * ks + lg);
-            bo[t][ks] = kHalf + ring_off(cbase + 16 * t + li, 4 * ks + lg);
-        }
+        for (int t = 0; t < kTM; ++t) ao[t][ks] = ring_off(rbase + 16 * t + li, 4 * ks + lg);
+#pragma unroll
+        for (int t = 0; t < kTN; ++t) bo[t][ks] = kHalf + ring_off(cbase + 16 * t + li, 4 * ks + lg);
+    }
     lds_barrier();
     for (int st = 0; st < nst; ++st) {
         const uint8_t* sp = lds + (st % kRing) * kStage;
-        bf16x8 av[2][kSteps], bv[2][kSteps];
+        bf16x8 av[kTM][kSteps], bv[kTN][kSteps];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int ks = 0; ks < kSteps; ++ks) {
 #pragma unroll
-            for (int ks = 0; ks < kSteps; ++ks) {
-                av[t][ks] = *reinterpret_cast<const bf16x8*>(sp + ao[t][ks]);
-                bv[t][ks] = *reinterpret_cast<const bf16x8*>(sp + bo[t][ks]);
-            }
+            for (int t = 0; t < kTM; ++t) av[t][ks] = *reinterpret_cast<const bf16x8*>(sp + ao[t][ks]);
+#pragma unroll
+            for (int t = 0; t < kTN; ++t) bv[t][ks] = *reinterpret_cast<const bf16x8*>(sp + bo[t][ks]);
+        }
 #pragma unroll
         for (int ks = 0; ks < kSteps; ++ks)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt)
+            for (int mt = 0; mt < kTM; ++mt)
 #pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
+                for (int nt = 0; nt < kTN; ++nt)
                     acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[mt][ks], bv[nt][ks], acc[mt][nt], 0, 0, 0);
         lds_barrier();                                          // this slot may be refilled
     }
 
     // acc[mt][nt][r] is output (row rbase + 16 mt + 4 lg + r, column cbase + 16 nt + li).
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < kTM; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < kTN; ++nt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + rbase + 16 * mt + 4 * lg + r, col = n0 + cbase + 16 * nt + li;

@@ -87,6 +87,8 @@ def test_mmvq_q8_0(n_in):
     ({}, 70, 128),                                   # a second, partial row tile
     (dict(h_k=2, h_v=4), 5, 384),                    # N = 1544: a partial column tile
     (dict(h_k=4, h_v=12, head_map=1), 17, 512),
+    ({}, 3, 64),                                     # one k stage (fewer than the ring holds)
+    ({}, 9, 192),                                    # three k stages
 ])
 def test_in_proj(kw, B, hidden):
     torch = _torch()
