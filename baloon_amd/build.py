@@ -4,7 +4,9 @@
 
 Each translation unit is compiled for gfx950 only, with packed-FP32 instruction selection
 disabled (-packed-fp32-ops), and with kernel resource-usage remarks captured to
-``_build/resource_usage.txt`` so tests can assert that no hot kernel spills to scratch.
+``_build/resource_usage.txt`` (one line per kernel: ``name=... VGPRs=.. AGPRs=.. ScratchSize=..
+Occupancy=.. SGPRsSpill=.. VGPRsSpill=.. LDSSize=..``) so tests can assert that no hot kernel
+spills to scratch and report SGPR spills, which land in VGPR lanes (v_writelane/v_readlane).
 """
 from __future__ import annotations
 
@@ -67,7 +69,7 @@ def _resource_summary(remarks: str) -> str:
             cur = {"name": val}
             lines.append(cur)
         elif cur is not None:
-            cur[key.split(" [")[0]] = val
+            cur[key.split(" [")[0].replace(" ", "")] = val      # e.g. "SGPRs Spill" -> SGPRsSpill
     out = []
     for d in lines:
         out.append(" ".join(f"{k}={v}" for k, v in d.items()))

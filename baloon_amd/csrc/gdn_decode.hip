@@ -155,6 +155,13 @@ __device__ __forceinline__ void column_store(const v4f& s, v4f* dst, const v4f& 
 // back and invalidate the whole L2, full of this kernel's state lines, per workgroup). The
 // stores are complete (vmcnt 0) before the counting atomic is issued, and the reads are
 // issued only after it has returned the partner's count.
+// This ordering is a gfx950 contract, not a HIP memory-model guarantee: the accesses are
+// relaxed, and what orders them is gfx950's code generation (agent-scope atomic stores and
+// loads bypass the non-coherent caches, and s_waitcnt vmcnt(0) retires the stores before the
+// counting atomic issues). A port to another target must replace it with release/acquire.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "head_gate_exchange relies on gfx950 ordering of relaxed agent-scope atomics"
+#endif
 __device__ __forceinline__ void head_gate_exchange(const DecodeParams& p, const DecodeWs& ws, int bseq, int h,
                                                    int hf, float v, int lane) {
     const size_t hd = (size_t)bseq * p.L.h_v + h;

@@ -1,6 +1,8 @@
 """Shared helpers for the GDN tests: numpy <-> device tensors and the comparison norms."""
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 import oracle
@@ -8,6 +10,36 @@ from oracle import bf16, inputs
 
 TOL_O_ABS = 1e-3       # fp32 outputs vs the double oracle, absolute
 TOL_STATE_REL = 1e-4   # fp32 state vs the double oracle, max|d| / max|ref|
+# Oracle threads: the GPU box's CPU share is 16 whatever os.cpu_count() reports there.
+NT = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)))
+
+
+def extreme_gates(cfg, tok, seed, frac=0.2):
+    """Drive the gate and beta logits of token inputs past the reference's thresholds.
+
+    In each of a and b, a fraction ``frac`` of the entries is set to a large positive value
+    and another ``frac`` to a large negative one, at seeded positions: a = +25 puts
+    a + dt_bias above softplus's threshold 20 (softplus(x) = x there, src/ix_gdn.cu:22) and,
+    with A_log up to ln 16, a log decay near -400 whose exp underflows to 0 in fp32;
+    a = -25 puts it below -20 (softplus ~ e^x, decay ~1); b = +-30 gives beta = 1 and
+    beta ~ 1e-13. Returns a copy of tok with a and b replaced (bf16 bits)."""
+    g = inputs.Gen(seed ^ 0x5EED)
+    out = dict(tok)
+    for name, big, tid in (("a", 25.0, 0x401), ("b", 30.0, 0x402)):
+        v = bf16.to_f32(tok[name]).astype(np.float32)
+        u = g.uniform(tid, v.shape)
+        v = np.where(u < frac, np.float32(big), np.where(u < 2 * frac, np.float32(-big), v)).astype(np.float32)
+        out[name] = bf16.from_f32(v)
+    return out
+
+
+def extreme_params(p):
+    """Layer parameters with A_log = ln 16 (the top of its range) on every other v head."""
+    q = dict(p)
+    al = np.array(p["A_log"], dtype=np.float32, copy=True)
+    al[::2] = np.float32(np.log(16.0))
+    q["A_log"] = al
+    return q
 
 
 def dev(a, dtype=None):
@@ -62,4 +94,5 @@ def bf16_ulp_diff(got_bits: np.ndarray, ref_f64: np.ndarray) -> int:
     return int(np.max(np.abs(ordered(g) - ordered(ref_bits)))) if g.size else 0
 
 
-__all__ = ["oracle", "bf16", "inputs", "dev", "host", "state_to_dev", "state_from_dev", "bf16_ulp_diff", "bf16_excess_err", "TOL_O_ABS", "TOL_STATE_REL"]
+__all__ = ["oracle", "bf16", "inputs", "dev", "host", "state_to_dev", "state_from_dev", "bf16_ulp_diff", "bf16_excess_err",
+           "extreme_gates", "extreme_params", "NT", "TOL_O_ABS", "TOL_STATE_REL"]

@@ -14,7 +14,7 @@ import pytest
 import baloon_amd as bx
 import oracle
 from oracle import bf16, inputs
-from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
+from tests.common import NT, TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-6
@@ -65,7 +65,7 @@ class Layer:
     def oracle_step(self, t):
         cfg, B = self.cfg, self.B
         self.cs, self.st, ro = oracle.decode(cfg, B, t["x"], self.cs, self.p["w"], t["a"], t["b"], self.p["A_log"],
-                                             self.p["dt_bias"], self.st, nthreads=8)
+                                             self.p["dt_bias"], self.st, nthreads=NT)
         return ro
 
 
@@ -74,7 +74,7 @@ WS = [pytest.param(True, id="workspace"), pytest.param(False, id="no_workspace")
 
 @pytest.mark.parametrize("ws", WS)
 @pytest.mark.parametrize("kw,B", [({}, 16), ({}, 1), (dict(h_k=4, h_v=12, head_map=1), 3),
-                                  (dict(h_k=3, h_v=8), 2)])
+                                  (dict(h_k=3, h_v=8), 2), (dict(h_k=1, h_v=16), 2), (dict(h_k=2, h_v=18), 2)])
 def test_decode_gated_matches_out_norm(kw, B, ws):
     cfg = bx.make_cfg(**kw)
     seed = inputs.seed_for(2) + 31 + B
@@ -154,5 +154,5 @@ def test_prefill_gated_matches_out_norm():
     np.testing.assert_array_equal(yb, bf16.from_f32(y))
     assert oracle.rel_err(y, oracle.gated_out(o, g["z"], g["nrm"], EPS)) <= TOL_Y_OWN
     _, _, ro = oracle.prefill(cfg, cu, tok["x"], st["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
-                              p["dt_bias"], st["state"], nthreads=8)
+                              p["dt_bias"], st["state"], nthreads=NT)
     assert oracle.rel_err(y, oracle.gated_out(ro, g["z"], g["nrm"], EPS)) <= TOL_Y_E2E

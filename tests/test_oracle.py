@@ -278,6 +278,72 @@ def test_decode_composes_legacy_functions(head_map):
         np.testing.assert_allclose(ro.reshape(hv, dk), o_o[b], rtol=1e-5, atol=1e-7)
 
 
+def _identity_conv_case(cfg, B, seed):
+    """Inputs whose conv output is x itself: every tap weight 0 except the current input's,
+    which is 1 (both exact in bf16), and a zero recurrent state."""
+    p, t, s = _fused_inputs(cfg, B, seed)
+    w = np.zeros((cfg.channels, cfg.d_conv), np.float32)
+    w[:, -1] = 1.0
+    p["w"] = bf16.from_f32(w)
+    s["state"] = np.zeros_like(s["state"])
+    return p, t, s
+
+
+@pytest.mark.parametrize("act", [0, 1])
+def test_decode_activation_closed_form(act):
+    # With a zero state the step gives S' = beta k^ v^T and o = beta (k^ . q^) v, where v is
+    # the conv output after the activation and q^, k^ the normalised activated q, k rows. An
+    # identity conv makes that output act(x): x itself, or SiLU(x) = x / (1 + e^-x). The x
+    # rows include 0 (SiLU(0) = 0) and +-12 (SiLU(12) = 12 - 7.4e-5, SiLU(-12) = -7.4e-5).
+    cfg = _small_cfg(conv_act=act, h_k=2, h_v=4)
+    B = 2
+    p, t, s = _identity_conv_case(cfg, B, 61)
+    xf = bf16.to_f32(t["x"]).astype(np.float64)
+    xf[:, 3] = 0.0
+    xf[:, 5] = 12.0
+    xf[:, -2] = -12.0
+    t["x"] = bf16.from_f32(xf.astype(np.float32))
+    xf = bf16.to_f32(t["x"]).astype(np.float64)
+    _, st, o = oracle.decode(cfg, B, t["x"], s["conv_state"], p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"],
+                             s["state"])
+    y = xf / (1.0 + np.exp(-xf)) if act else xf
+    if act:
+        assert y[0, 3] == 0.0 and abs(y[0, 5] - (12.0 - 12.0 * math.exp(-12.0) / (1 + math.exp(-12.0)))) < 1e-12
+    dk, hk = cfg.d_k, cfg.h_k
+    for b in range(B):
+        q = y[b, :hk * dk].reshape(hk, dk)
+        k = y[b, hk * dk:2 * hk * dk].reshape(hk, dk)
+        v = y[b, 2 * hk * dk:].reshape(cfg.h_v, cfg.d_v)
+        qn = q / np.sqrt((q * q).sum(1, keepdims=True) + cfg.l2_eps)
+        kn = k / np.sqrt((k * k).sum(1, keepdims=True) + cfg.l2_eps)
+        beta = 1.0 / (1.0 + np.exp(-bf16.to_f32(t["b"][b]).astype(np.float64)))
+        for h in range(cfg.h_v):
+            src = h % hk
+            np.testing.assert_allclose(st[b, h], beta[h] * np.outer(kn[src], v[h]), rtol=1e-12, atol=1e-15)
+            np.testing.assert_allclose(o[b, h], beta[h] * (kn[src] @ qn[src]) * v[h], rtol=1e-10, atol=1e-14)
+
+
+def test_decode_q_scale_is_linear_in_o_only():
+    # q_scale multiplies the normalised q (1 in the reference): the outputs scale by it and
+    # the states do not move. A power of two scales exactly; 1/sqrt(128) within rounding.
+    cfg1 = _small_cfg()
+    B = 3
+    p, t, s = _fused_inputs(cfg1, B, 71)
+    ref = oracle.decode(cfg1, B, t["x"], s["conv_state"], p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"],
+                        s["state"])
+    for qs, exact in ((0.25, True), (128 ** -0.5, False), (-2.0, True)):
+        cfg = _small_cfg(q_scale=qs)
+        cs, st, o = oracle.decode(cfg, B, t["x"], s["conv_state"], p["w"], t["a"], t["b"], p["A_log"],
+                                  p["dt_bias"], s["state"])
+        np.testing.assert_array_equal(cs, ref[0])
+        np.testing.assert_array_equal(st, ref[1])
+        want = np.float64(np.float32(qs)) * ref[2]
+        if exact:
+            np.testing.assert_array_equal(o, want)
+        else:
+            np.testing.assert_allclose(o, want, rtol=1e-13, atol=1e-16)
+
+
 def test_decode_batch_rows_independent():
     cfg = _small_cfg()
     B = 4

@@ -6,18 +6,16 @@ the oracle; bf16 outputs exactly RNE of the kernel's own fp32 outputs; fp32 stat
 max|d|/max|ref| <= 1e-4 after the sequence (the reference's norm, tests/test_gdn.cu:10-13);
 conv state bit-exact. Inputs come from the portable generator (oracle/inputs.py).
 """
-import os
-
 import numpy as np
 import pytest
 
 import baloon_amd as bx
 import oracle
 from oracle import bf16, inputs
-from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
+from tests.common import (NT, TOL_O_ABS, TOL_STATE_REL, dev, extreme_gates, extreme_params, host, state_from_dev,
+                          state_to_dev)
 
 pytestmark = pytest.mark.gpu
-NT = min(16, os.cpu_count() or 1)
 
 
 def _torch():
@@ -48,12 +46,14 @@ def oracle_prefill(cfg, cu, tok, p, st):
                           p["dt_bias"], st["state"], nthreads=NT)
 
 
-def check(cfg, cu, seed, state_std=0.02, conv_std=1.0):
+def check(cfg, cu, seed, state_std=0.02, conv_std=1.0, extreme=False):
     cu = np.asarray(cu, np.int32)
     n, T = cu.size - 1, int(cu[-1])
     p = inputs.layer_params(cfg, seed)
     tok = inputs.token_inputs(cfg, seed, max(T, 1))
     tok = {k: v[:T] for k, v in tok.items()}
+    if extreme:
+        p, tok = extreme_params(p), extreme_gates(cfg, tok, seed)
     st = inputs.initial_states(cfg, seed, n, state_std=state_std, conv_std=conv_std)
     cs, s, o, ob = gpu_prefill(cfg, cu, tok, p, st)
     rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
@@ -99,9 +99,33 @@ def test_more_sequences_than_one_plan_pass(n):
     dict(h_k=4, h_v=2),
     dict(h_k=2, h_v=6, head_map=1),
     dict(h_k=1, h_v=1),
+    dict(h_k=1, h_v=16),             # 16 v heads on one q/k head: the configuration limit
+    dict(h_k=2, h_v=32, head_map=1), # 16 per source with the contiguous map
+    dict(h_k=2, h_v=18),             # 9 per source (more than 8) with modulo pairing
 ])
 def test_variants(kw):
     check(oracle.make_cfg(**kw), [0, 70, 71, 150], inputs.seed_for(3) + 11 * len(kw))
+
+
+@pytest.mark.parametrize("frac", [0.05, 0.2])
+def test_extreme_gates(frac):
+    # Gate logits past softplus's threshold on both sides and beta logits at +-30 at seeded
+    # positions (tests/common.py extreme_gates), A_log = ln 16 on every other head: decays
+    # that underflow to 0 next to decays of ~1 inside one chunk, over several chunks.
+    cfg = oracle.make_cfg()
+    seed = inputs.seed_for(3) + int(frac * 100)
+    cu = np.asarray([0, 260, 333], np.int32)
+    p = extreme_params(inputs.layer_params(cfg, seed))
+    tok = extreme_gates(cfg, inputs.token_inputs(cfg, seed, 333), seed, frac)
+    st = inputs.initial_states(cfg, seed, 2)
+    cs, s, o, ob = gpu_prefill(cfg, cu, tok, p, st)
+    rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    rel = oracle.rel_err(s, rs)
+    assert rel <= TOL_STATE_REL, f"state rel err {rel}"
+    err = float(np.max(np.abs(o - ro)))
+    assert err <= TOL_O_ABS, f"o abs err {err}"
+    np.testing.assert_array_equal(ob, bf16.from_f32(o))
 
 
 def test_zero_initial_state_config3_shape_short():
@@ -139,13 +163,13 @@ def test_prefill_matches_gpu_decode_loop():
 
 
 def test_config4_varlen_prefill_then_decode():
-    # configuration 4: 32 sequences, lengths ~ U[1, L], initial states N(0, 0.02), then 32
-    # decode steps per sequence from the carried conv and recurrent states. The full
-    # configuration draws lengths up to 2048; 512 keeps the double oracle to seconds.
+    # configuration 4 as stated: 32 sequences with lengths ~ U[1, 2048] packed by cu_seqlens,
+    # initial states N(0, 0.02), then 32 decode steps per sequence from the carried conv and
+    # recurrent states; outputs of every decode step checked, states at the end.
     torch = _torch()
     cfg = bx.make_cfg()
     seed, n, steps = inputs.seed_for(4), 32, 32
-    cu = inputs.varlen(seed, n, 1, 512)
+    cu = inputs.varlen(seed, n, 1, 2048)
     T = int(cu[-1])
     p = inputs.layer_params(cfg, seed)
     tok = inputs.token_inputs(cfg, seed, T)

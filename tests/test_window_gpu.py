@@ -12,7 +12,8 @@ import pytest
 import baloon_amd as bx
 import oracle
 from oracle import inputs
-from tests.common import TOL_O_ABS, TOL_STATE_REL, dev, host, state_from_dev, state_to_dev
+from tests.common import (NT, TOL_O_ABS, TOL_STATE_REL, dev, extreme_gates, extreme_params, host, state_from_dev,
+                          state_to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -22,11 +23,13 @@ def _torch():
     return torch
 
 
-def window_case(cfg, B, K, accepted, seed):
+def window_case(cfg, B, K, accepted, seed, extreme=False):
     torch = _torch()
     p = inputs.layer_params(cfg, seed)
     st = inputs.initial_states(cfg, seed, B)
     tok = inputs.token_inputs(cfg, seed, B * K)                      # row b*K + t
+    if extreme:
+        p, tok = extreme_params(p), extreme_gates(cfg, tok, seed)
     x = tok["x"].reshape(B, K, -1)
     a = tok["a"].reshape(B, K, -1)
     b = tok["b"].reshape(B, K, -1)
@@ -71,7 +74,7 @@ def window_case(cfg, B, K, accepted, seed):
     ref = [(rcs, rst)]
     for t in range(K):
         rcs, rst, ro = oracle.decode(cfg, B, x[:, t], rcs, p["w"], a[:, t], b[:, t], p["A_log"], p["dt_bias"], rst,
-                                     nthreads=8)
+                                     nthreads=NT)
         assert float(np.max(np.abs(o_win[:, t] - ro))) <= TOL_O_ABS
         ref.append((rcs, rst))
     for bi in range(B):
@@ -92,9 +95,15 @@ def test_window_verify_and_commit(K, accepted):
 
 
 @pytest.mark.parametrize("kw", [dict(head_map=1, h_k=4, h_v=12), dict(d_conv=2), dict(d_conv=3, conv_act=1),
-                                dict(h_k=3, h_v=8, q_scale=0.125)])
+                                dict(h_k=3, h_v=8, q_scale=0.125), dict(h_k=1, h_v=16), dict(h_k=2, h_v=18),
+                                dict(h_k=2, h_v=32, head_map=1)])
 def test_window_variants(kw):
-    window_case(bx.make_cfg(**kw), 3, 3, [3, 1, 2], inputs.seed_for(2) + 60 + len(kw))
+    window_case(bx.make_cfg(**kw), 3, 3, [3, 1, 2], inputs.seed_for(2) + 60 + len(kw) + kw.get("h_v", 0))
+
+
+def test_window_extreme_gates():
+    # gate logits past softplus's threshold on both sides, beta logits at +-30, A_log = ln 16
+    window_case(bx.make_cfg(), 6, 8, [8, 5, 0, 3, 7, 1], inputs.seed_for(2) + 90, extreme=True)
 
 
 def test_window_then_decode_continues():
@@ -126,7 +135,7 @@ def test_window_then_decode_continues():
         assert bx.ix_gdn_decode(cfg, B, dev(t["x"]), d_cs, d_w, dev(t["a"]), dev(t["b"]), d_A, d_dt, d_st, od, None,
                                 ws) == 0
         rcs, rst, ro = oracle.decode(cfg, B, t["x"], rcs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], rst,
-                                     nthreads=8)
+                                     nthreads=NT)
         torch.cuda.synchronize()
         assert float(np.max(np.abs(host(od) - ro))) <= TOL_O_ABS
     np.testing.assert_array_equal(host(d_cs), rcs)
