@@ -75,6 +75,8 @@ def lib():
             fn = getattr(_lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_int if name == "ixo_src_head" else None
+        _lib.ixo_mix_counter.argtypes = [ctypes.c_uint64, ctypes.c_uint64, P]
+        _lib.ixo_mix_counter.restype = None
         for name in ("ixo_gate", "ixo_sigmoid", "ixo_softplus"):
             getattr(_lib, name).restype = ctypes.c_double
         _lib.ixo_gate.argtypes = [F, ctypes.c_double, F]

@@ -217,3 +217,20 @@ void ixo_prefill(const ixo_cfg* c, int n_seq, const int32_t* cu, const uint16_t*
     }
     free(y);
 }
+
+/* ------------------------------------------------------------------------------------------
+ * Input generator support (oracle/inputs.py): out[i] = mix(i + key) for i < n, with mix the
+ * splitmix64 finaliser. Exact integer arithmetic, so it equals the numpy formulation bit for
+ * bit; it only makes large seeded tensors cheap to generate.
+ * ------------------------------------------------------------------------------------------ */
+static inline uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void ixo_mix_counter(uint64_t key, uint64_t n, uint64_t* out) {
+#pragma omp parallel for schedule(static) num_threads(8)
+    for (long long i = 0; i < (long long)n; ++i) out[i] = splitmix64((uint64_t)i + key);
+}

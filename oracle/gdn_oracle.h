@@ -53,6 +53,9 @@ void ixo_prefill(const ixo_cfg* c, int n_seq, const int32_t* cu_seqlens, const u
                  uint16_t* conv_state, const uint16_t* w, const uint16_t* a, const uint16_t* b,
                  const float* A_log, const float* dt_bias, double* state, double* o, int nthreads);
 
+/* Input generator support: out[i] = splitmix64(i + key), i < n (oracle/inputs.py). */
+void ixo_mix_counter(uint64_t key, uint64_t n, uint64_t* out);
+
 #ifdef __cplusplus
 }
 #endif
