@@ -34,7 +34,7 @@ EXPORTS = (
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
     "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_commit_window",
     "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
-    "ix_gdn_version",
+    "ix_gdn_version", "ix_gdn_decode_noalloc",
 )
 
 
@@ -110,6 +110,7 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_in_proj_width": ([P], I),
         "ix_gdn_in_proj": ([P, I, I, P, P, P, P, P, P, P, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
+        "ix_gdn_decode_noalloc": ([P, I, P, P, P, P, P, P, P, P, P, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -181,6 +182,16 @@ def ix_gdn_decode(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, stat
     return lib().ix_gdn_decode(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a), _ptr(b),
                                _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16), _ptr(workspace),
                                _stream(s))
+
+
+def ix_gdn_decode_noalloc(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
+                          s=None) -> int:
+    """ix_gdn_decode without a workspace and without any allocation: the group counters live
+    in a library-owned static device array (B * h_k <= 65536). Calls on one GPU must be
+    ordered (they share the array)."""
+    return lib().ix_gdn_decode_noalloc(ctypes.byref(cfg), B, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a),
+                                       _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16),
+                                       _stream(s))
 
 
 def ix_gdn_prefill_workspace_size(cfg: Cfg, n_seq: int, total_T: int) -> int:

@@ -35,6 +35,8 @@
 // HBM latency overlaps the conv; the state is streamed once per token.
 #include "gdn_common.h"
 
+#include <mutex>
+
 namespace ixg {
 namespace {
 
@@ -399,24 +401,32 @@ group_kernel(const DecodeParams p) {
     }
 }
 
+// The slab kernel needs every q/k head to feed at least one v head (its history is written
+// by the group's last member); otherwise, and without counters, one workgroup owns each
+// group.
+inline bool every_src_used(const ix_gdn_cfg* cfg) {
+    return cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
+}
+
+inline DecodeWs bind_decode_ws(void* workspace, int B, const ix_gdn_cfg* cfg) {
+    size_t off[4];
+    decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
+    char* base = static_cast<char*>(workspace);
+    return DecodeWs{reinterpret_cast<int*>(base + off[0]), reinterpret_cast<int*>(base + off[1]),
+                    reinterpret_cast<float*>(base + off[2]), reinterpret_cast<float*>(base + off[3])};
+}
+
+// ws: the workspace sections (group counters at least; the gated kernel also uses the head
+// counters and exchange slots), or null for the group kernel.
 template <bool GATED>
-void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, void* workspace, hipStream_t s) {
-    // The slab kernel needs every q/k head to feed at least one v head (its history is
-    // written by the group's last member); otherwise, and without a workspace, one
-    // workgroup owns each group.
-    const bool every_src_used = cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
+void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, const DecodeWs* ws, hipStream_t s) {
     const dim3 block(kThreads);
-    if (workspace && every_src_used) {
-        size_t off[4];
-        decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
-        char* base = static_cast<char*>(workspace);
-        const DecodeWs ws{reinterpret_cast<int*>(base + off[0]), reinterpret_cast<int*>(base + off[1]),
-                          reinterpret_cast<float*>(base + off[2]), reinterpret_cast<float*>(base + off[3])};
+    if (ws && every_src_used(cfg)) {
         const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
         switch (cfg->d_conv) {
-            case 2: hipLaunchKernelGGL((slab_kernel<2, GATED>), grid, block, 0, s, p, ws); break;
-            case 3: hipLaunchKernelGGL((slab_kernel<3, GATED>), grid, block, 0, s, p, ws); break;
-            default: hipLaunchKernelGGL((slab_kernel<4, GATED>), grid, block, 0, s, p, ws); break;
+            case 2: hipLaunchKernelGGL((slab_kernel<2, GATED>), grid, block, 0, s, p, *ws); break;
+            case 3: hipLaunchKernelGGL((slab_kernel<3, GATED>), grid, block, 0, s, p, *ws); break;
+            default: hipLaunchKernelGGL((slab_kernel<4, GATED>), grid, block, 0, s, p, *ws); break;
         }
     } else {
         const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
@@ -497,7 +507,12 @@ extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t
     const hipError_t e = decode_params(cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16,
                                        workspace, p);
     if (e != hipSuccess) return e;
-    ixg::launch_decode<false>(cfg, B, p, workspace, s);
+    if (workspace) {
+        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace, B, cfg);
+        ixg::launch_decode<false>(cfg, B, p, &ws, s);
+    } else {
+        ixg::launch_decode<false>(cfg, B, p, nullptr, s);
+    }
     return hipGetLastError();
 }
 
@@ -512,6 +527,69 @@ extern "C" hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const ui
     if (e != hipSuccess) return e;
     if ((e = ix_gdn_check_gate_(gate)) != hipSuccess) return e;
     p.og = ixg::make_out_gate(gate);
-    ixg::launch_decode<true>(cfg, B, p, workspace, s);
+    if (workspace) {
+        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace, B, cfg);
+        ixg::launch_decode<true>(cfg, B, p, &ws, s);
+    } else {
+        ixg::launch_decode<true>(cfg, B, p, nullptr, s);
+    }
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------
+// ix_gdn_decode_noalloc: ix_gdn_decode's counter-workspace kernel with the group counters in
+// a library-owned static device array instead of a caller workspace, so the call allocates
+// nothing. Each GPU holds its own copy of the array (256 KiB) until the process ends.
+// ---------------------------------------------------------------------------------------
+constexpr int kNoAllocMaxGroups = 65536;                 // B * h_k counters
+static __device__ __align__(256) int scratch[kNoAllocMaxGroups];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int* g_scratch_dev[kMaxDevices];                         // device address of `scratch`, per GPU
+
+__global__ void __launch_bounds__(256) scratch_clear_kernel(int* p, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
+// The current device's copy of `scratch`. On the first call on a device: its address (the
+// host-side name is only a stand-in for it), then a fill kernel on stream s that zeroes it
+// (it also starts zeroed at load; the kernels leave every counter at zero again).
+hipError_t noalloc_counters(hipStream_t s, int** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, s, static_cast<int*>(ptr), kNoAllocMaxGroups);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+        g_scratch_dev[dev] = static_cast<int*>(ptr);
+    }
+    *out = g_scratch_dev[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" hipError_t ix_gdn_decode_noalloc(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                                            const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
+                                            const float* A_log, const float* dt_bias, float* state, float* o,
+                                            uint16_t* o_bf16, hipStream_t s) {
+    ixg::DecodeParams p;
+    hipError_t e = decode_params(cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16, nullptr, p);
+    if (e != hipSuccess) return e;
+    if ((long long)B * cfg->h_k > kNoAllocMaxGroups) return hipErrorInvalidValue;   // beyond the static array
+    if (!ixg::every_src_used(cfg)) {                     // the group kernel needs no counters
+        ixg::launch_decode<false>(cfg, B, p, nullptr, s);
+        return hipGetLastError();
+    }
+    int* counters = nullptr;
+    if ((e = noalloc_counters(s, &counters)) != hipSuccess) return e;
+    const ixg::DecodeWs ws{counters, nullptr, nullptr, nullptr};   // the ungated kernel uses the counters only
+    ixg::launch_decode<false>(cfg, B, p, &ws, s);
     return hipGetLastError();
 }

@@ -131,6 +131,21 @@ hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16
                          const float* dt_bias, float* state, float* o, uint16_t* o_bf16, void* workspace,
                          hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* ix_gdn_decode for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. It runs the kernel ix_gdn_decode runs with a workspace, with the group counters
+ * in a library-owned static device array (one copy per GPU, 256 KiB, held until the process
+ * ends; found and cleared on the first call on each device) instead of a caller workspace,
+ * and calls no allocating routine. Requires B * h_k <= 65536 (else hipErrorInvalidValue,
+ * before any launch). Every call in this process on one GPU shares that GPU's array, which
+ * each call leaves all zero: calls that overlap on one GPU (on two streams, or from two host
+ * threads) race, so the caller must order them, e.g. on one stream. Arguments otherwise as
+ * ix_gdn_decode. */
+hipError_t ix_gdn_decode_noalloc(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
+                                 const uint16_t* conv_w, const uint16_t* a, const uint16_t* b, const float* A_log,
+                                 const float* dt_bias, float* state, float* o, uint16_t* o_bf16,
+                                 hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* ix_gdn_decode followed by the gated output norm of each (sequence, v head), in the same
  * launch: gate->z, gate->y, gate->y_bf16 are [B][h_v][d_v]. o and o_bf16 may both be NULL.
  * gate must be non-NULL with z, ssm_norm and at least one of y, y_bf16 set. With a workspace
