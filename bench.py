@@ -8,27 +8,46 @@ independent sequences, 16 q/k heads and 32 v heads, d_k = d_v = 128, fp32 state 
 layer, fused conv (4 taps over 8192 channels), one ix_gdn_decode launch per step. A "step" is
 one decode token for all B sequences of one layer; steps rotate over --layers independent
 layers (state, conv state, weights), so the working set (4 x 128 MiB) exceeds the 256 MB
-Infinity Cache and the state really streams from HBM. Inputs are synthetic and resident in
-HBM before the timed region, which is bracketed by HIP events on the launch stream.
+Infinity Cache and the state really streams from HBM. Inputs are resident in HBM before the
+timed region, which is bracketed by HIP events on the launch stream.
 
-Also reported on the same line: decode latency at B = 1 (configuration 1), chunked prefill
-of one 4096-token sequence (configuration 3) with its MFMA roofline fraction, the measured
-in-place HBM ceiling of the box, and the CPU oracle (a C port of the reference's recurrence)
-timed on this host over bounded samples of the same workloads.
+Also reported on the same line: decode latency at B = 1 (configuration 1), eager and as a
+captured HIP graph; the gated decode, the speculative window and the input projection at the
+decode batch; chunked prefill of one 4096-token sequence (configuration 3) with its MFMA
+roofline fraction; the measured in-place HBM ceiling of the box.
+
+The cpu_baseline leg is the only code here that uses oracle/ (the CPU restatement of the
+reference's recurrence, test infrastructure). It generates the seeded inputs every GPU leg
+runs on (oracle/inputs.py, the generator the tests use), replays each timed decode and
+prefill sequence on this host's cores -- those replays are the CPU baseline -- and checks the
+GPU's results against them: the states after the timed region and the last outputs of every
+decode leg, the prefill's outputs and final state, one window and one projection call. A
+mismatch is a failed gate: the bench then prints no JSON line and exits with status 3.
+Nothing from oracle/ runs inside a timed GPU region.
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E spec
+MFMA_BF16_PEAK_TFLOPS = 2500.0 # MI355X dense bf16 spec
 STATE_TILE = 128 * 128 * 4     # bytes per (sequence, v head)
+PREFILL_FLOP_PER_TOKEN = 5_767_168     # 2C^2(3d_k+2d_v) + 6 C d_k d_v per (v head, chunk of 64) / 64, x 32 heads
+TOL_O_ABS = 1e-3               # fp32 outputs vs the double oracle (bf16 outputs: beyond their own rounding)
+TOL_STATE_REL = 1e-4           # fp32 state: max|d| / max|ref|
+TOL_Y_REL = 1e-4               # gated output norm, end to end
+TOL_PROJ = 2e-5                # projection: |y - ref| <= 2e-5 * sum |h w| per output
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_traffic.json")
 
 
 def parse():
@@ -38,50 +57,282 @@ def parse():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--layers", type=int, default=4)
-    ap.add_argument("--inputs", type=int, default=8, help="distinct input sets cycled through")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget per CPU baseline leg")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--inputs", type=int, default=8, help="distinct token input sets cycled through")
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the single-core CPU samples (the multi-core replays, which gate the run, always run)")
     return ap.parse_args()
 
 
-def decode_bench(args, gated=False):
+def cpu_share() -> int:
+    """Host threads for the CPU legs: the GPU box's CPU share is 16 whatever nproc shows."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+# ---------------------------------------------------------------------------------------------
+# host <-> device plumbing
+# ---------------------------------------------------------------------------------------------
+
+def to_dev(a):
+    import torch
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+    return torch.from_numpy(a.copy()).cuda()
+
+
+def to_host(t) -> np.ndarray:
+    import torch
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def state_dev(st):
+    """[..][h_v][d_k][d_v] -> the library's [..][h_v][d_v][d_k] layout on the device."""
+    return to_dev(np.ascontiguousarray(np.swapaxes(np.asarray(st, np.float32), -1, -2)))
+
+
+def state_host(t) -> np.ndarray:
+    return np.ascontiguousarray(np.swapaxes(to_host(t), -1, -2))
+
+
+def bf16_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def timed(stream, fn, n):
+    """n calls of fn(i) between HIP events recorded on `stream`; every status checked after."""
+    import torch
+
+    import baloon_amd as bx
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    rcs = [fn(i) for i in range(n)]
+    e1.record(stream)
+    torch.cuda.synchronize()
+    for rc in rcs:
+        bx.check("launch", rc)
+    return e0.elapsed_time(e1) / 1e3          # seconds
+
+
+# ---------------------------------------------------------------------------------------------
+# cpu_baseline leg: the only user of oracle/ (inputs, CPU replays, the correctness gate)
+# ---------------------------------------------------------------------------------------------
+
+class CpuBaselineLeg:
+    def __init__(self):
+        import oracle
+        from oracle import bf16, inputs, proj
+        self.oracle, self.inputs, self.bf16, self.proj = oracle, inputs, bf16, proj
+        self.nt = cpu_share()
+        self.cfg = oracle.make_cfg()
+        self.failures = []
+        self.record = {}
+
+    # ---- inputs ----
+    def decode_data(self, B, L, P):
+        """Per-layer parameters, the initial states (shared by the layers) and P token input
+        sets for configuration 2, from seed 0x6D4E0002 (layer l: + l)."""
+        inp, cfg = self.inputs, self.cfg
+        seed = inp.seed_for(2)
+        st = inp.initial_states(cfg, seed, B)
+        return dict(
+            params=[inp.layer_params(cfg, seed + l) for l in range(L)],
+            state0=st["state"], cs0=st["conv_state"],
+            tokens=[inp.token_inputs(cfg, seed, B, step=i) for i in range(P)],
+            gate=inp.out_gate_inputs(cfg, seed, B),
+        )
+
+    def window_tokens(self, B, K):
+        t = self.inputs.token_inputs(self.cfg, self.inputs.seed_for(2) + 0x51, B * K)
+        return {k: v.reshape(B, K, -1) for k, v in t.items()}
+
+    def proj_data(self, B, hidden, N):
+        g = self.inputs.Gen(self.inputs.seed_for(2) + 0x61)
+        h = g.normal_bf16(1, (B, hidden))
+        w = self.bf16.from_f32((g.normal(2, (N, hidden)) * 0.05).astype(np.float32))
+        return h, w
+
+    def prefill_data(self, T):
+        """Configuration 3's inputs (seed 0x6D4E0003), generated once."""
+        if self.record.get("prefill_data", (None,))[0] != T:
+            inp, cfg = self.inputs, self.cfg
+            seed = inp.seed_for(3)
+            self.record["prefill_data"] = (T, dict(params=inp.layer_params(cfg, seed),
+                                                   tokens=inp.token_inputs(cfg, seed, T)))
+        return self.record["prefill_data"][1]
+
+    def latency_data(self):
+        inp, cfg = self.inputs, self.cfg
+        seed = inp.seed_for(1)
+        st = inp.initial_states(cfg, seed, 1)
+        return dict(params=inp.layer_params(cfg, seed), state0=st["state"], cs0=st["conv_state"],
+                    tokens=[inp.token_inputs(cfg, seed, 1, step=i) for i in range(8)])
+
+    # ---- checks ----
+    def fail(self, what):
+        self.failures.append(what)
+        print(f"bench gate FAILED: {what}", file=sys.stderr)
+
+    def check_bf16_out(self, what, bits, ref, tol=TOL_O_ABS):
+        """bf16 outputs within tol of the double reference beyond bf16's own half-ulp rounding."""
+        ref = np.asarray(ref, np.float64)
+        got32 = bf16_f32(bits)
+        got = got32.astype(np.float64)
+
+        def binade(v):   # 2^e with 2^e <= |v| < 2^(e+1)
+            return (np.abs(v).view(np.uint32) & np.uint32(0x7F800000)).view(np.float32).astype(np.float64)
+
+        # half a bf16 ulp, of whichever of ref and the output lies in the higher binade (the
+        # rounding may cross a power of two)
+        half = np.maximum(np.maximum(binade(ref.astype(np.float32)), binade(got32)) * 2.0 ** -8, 2.0 ** -133)
+        err = float(np.max(np.abs(got - ref) - half)) if ref.size else 0.0
+        if not err <= tol:
+            self.fail(f"{what}: bf16 output error beyond rounding {err:.3g} > {tol}")
+        return err
+
+    def check_state(self, what, got, ref):
+        rel = self.oracle.rel_err(got, ref)
+        if not rel <= TOL_STATE_REL:
+            self.fail(f"{what}: state rel err {rel:.3g} > {TOL_STATE_REL}")
+        return rel
+
+    def check_equal(self, what, got, ref):
+        if not np.array_equal(got, ref):
+            self.fail(f"{what}: not bit-identical")
+
+    # ---- decode replay (the CPU baseline and the decode gate) ----
+    def replay_decode(self, D, order, L, P, B, nthreads):
+        """The timed GPU sequence launch by launch: launch i is one step of layer order[i] % L
+        with token set order[i] % P. Returns per-layer (conv state, state), the last output
+        and the seconds spent in the oracle."""
+        o_ = self.oracle
+        cs = [D["cs0"].copy() for _ in range(L)]
+        st = [D["state0"].astype(np.float64) for _ in range(L)]
+        o_last, sec = None, 0.0
+        for i in order:
+            l, t, p = i % L, D["tokens"][i % P], D["params"][i % L]
+            t0 = time.perf_counter()
+            cs[l], st[l], o_last = o_.decode(self.cfg, B, t["x"], cs[l], p["w"], t["a"], t["b"], p["A_log"],
+                                             p["dt_bias"], st[l], nthreads=nthreads)
+            sec += time.perf_counter() - t0
+        return cs, st, o_last, sec
+
+    def gate_decode(self, D, order, args, res, gated_res=None):
+        L, P, B = args.layers, args.inputs, args.batch
+        cs, st, o_last, sec = self.replay_decode(D, order, L, P, B, self.nt)
+        self.record["decode"] = dict(tokens_per_s=B * len(order) / sec, steps=len(order), sec=sec)
+        errs = []
+        for l in range(L):
+            self.check_equal(f"decode layer {l} conv state", res["cs"][l], cs[l])
+            errs.append(self.check_state(f"decode layer {l}", res["st"][l], st[l]))
+        e_o = self.check_bf16_out("decode last o", res["out"], o_last)
+        out = dict(state_rel_err=max(errs), o_err=e_o)
+        if gated_res is not None:
+            for l in range(L):
+                self.check_equal(f"gated decode layer {l} state vs ungated", gated_res["st"][l], res["st"][l])
+                self.check_equal(f"gated decode layer {l} conv state vs ungated", gated_res["cs"][l], res["cs"][l])
+            g = D["gate"]
+            y_ref = self.oracle.gated_out(o_last, g["z"], g["nrm"], 1e-6)
+            y = bf16_f32(gated_res["out"]).astype(np.float64)
+            half = np.abs(y_ref) * 2.0 ** -8
+            y_err = float(np.max(np.maximum(np.abs(y - y_ref) - half, 0.0)) / max(np.max(np.abs(y_ref)), 1e-30))
+            if not y_err <= TOL_Y_REL:
+                self.fail(f"gated decode last y: rel err beyond bf16 rounding {y_err:.3g} > {TOL_Y_REL}")
+            out["y_rel_err"] = y_err
+        return out
+
+    def cpu_decode_1core(self, D, args, budget_s=6.0, max_steps=16):
+        """Single-thread rate on a bounded sample: launches of layer 0 until the budget is used."""
+        cs, st = D["cs0"].copy(), D["state0"].astype(np.float64)
+        p, steps, t0 = D["params"][0], 0, time.perf_counter()
+        while steps < max_steps:
+            t = D["tokens"][steps % args.inputs]
+            cs, st, _ = self.oracle.decode(self.cfg, args.batch, t["x"], cs, p["w"], t["a"], t["b"], p["A_log"],
+                                           p["dt_bias"], st, nthreads=1)
+            steps += 1
+            if time.perf_counter() - t0 >= budget_s:
+                break
+        return args.batch * steps / (time.perf_counter() - t0), steps
+
+    # ---- window, projection and prefill gates ----
+    def gate_window(self, D, W, B, K, o_win, cs_after, st_after):
+        cs, st = D["cs0"].copy(), D["state0"].astype(np.float64)
+        p = D["params"][0]
+        errs = []
+        for t in range(K):
+            cs, st, ro = self.oracle.decode(self.cfg, B, W["x"][:, t], cs, p["w"], W["a"][:, t], W["b"][:, t],
+                                            p["A_log"], p["dt_bias"], st, nthreads=self.nt)
+            errs.append(self.check_bf16_out(f"window token {t} o", o_win[:, t], ro))
+        self.check_equal("window commit conv state", cs_after, cs)
+        rel = self.check_state("window commit", st_after, st)
+        return dict(o_err=max(errs), state_rel_err=rel)
+
+    def gate_proj(self, h, w, y):
+        ref, mag = self.proj.in_proj_ref(h, w)
+        err = float(np.max(np.abs(y.astype(np.float64) - ref) / np.maximum(mag, 1e-30)))
+        if not err <= TOL_PROJ:
+            self.fail(f"in_proj: error {err:.3g} x magnitude > {TOL_PROJ}")
+        return err
+
+    def gate_prefill(self, D, T, cs_gpu, st_gpu, o_gpu):
+        cfg, inp = self.cfg, self.inputs
+        st0 = inp.initial_states(cfg, inp.seed_for(3), 1, state_std=0.0, conv_std=0.0)
+        p, tok = D["params"], D["tokens"]
+        t0 = time.perf_counter()
+        cs, st, o = self.oracle.prefill(cfg, [0, T], tok["x"], st0["conv_state"], p["w"], tok["a"], tok["b"],
+                                        p["A_log"], p["dt_bias"], st0["state"], nthreads=self.nt)
+        sec = time.perf_counter() - t0
+        self.record["prefill"] = dict(tokens_per_s=T / sec, T=T, sec=sec)
+        self.check_equal("prefill conv state", cs_gpu, cs)
+        rel = self.check_state("prefill", st_gpu, st)
+        e_o = self.check_bf16_out("prefill o", o_gpu, o)
+        return dict(state_rel_err=rel, o_err=e_o)
+
+    def cpu_prefill_1core(self, D, Tp=256):
+        cfg, inp = self.cfg, self.inputs
+        st0 = inp.initial_states(cfg, inp.seed_for(3), 1, state_std=0.0, conv_std=0.0)
+        p, tok = D["params"], D["tokens"]
+        t0 = time.perf_counter()
+        self.oracle.prefill(cfg, [0, Tp], tok["x"][:Tp], st0["conv_state"], p["w"], tok["a"][:Tp], tok["b"][:Tp],
+                            p["A_log"], p["dt_bias"], st0["state"], nthreads=1)
+        return Tp / (time.perf_counter() - t0)
+
+
+# ---------------------------------------------------------------------------------------------
+# GPU legs
+# ---------------------------------------------------------------------------------------------
+
+def decode_leg(args, D, gated=False):
     """B-sequence decode over rotated layers; gated=True times ix_gdn_decode_gated (the same
-    step with the gated output norm fused in, y written as bf16)."""
+    step with the gated output norm fused in, y written as bf16). Launch i runs layer i % L
+    with token set i % P; the warmup launches i < W, then the timed launches i < K."""
     import torch
 
     import baloon_amd as bx
 
     cfg = bx.make_cfg()
     B, L, P = args.batch, args.layers, args.inputs
-    C, hv = cfg.channels, cfg.h_v
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x6D4E0002)
+    hv = cfg.h_v
+    st0 = np.ascontiguousarray(np.swapaxes(D["state0"], -1, -2))
     layers = []
-    for _ in range(L):
-        layers.append(dict(
-            w=(torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16),
-            A_log=torch.rand(hv, generator=g, device=dev) * float(torch.log(torch.tensor(16.0))),
-            dt=torch.randn(hv, generator=g, device=dev) * 0.1,
-            state=torch.randn(B, hv, 128, 128, generator=g, device=dev) * 0.02,
-            cs=torch.randn(B, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16),
-        ))
-    ins = [dict(x=torch.randn(B, C, generator=g, device=dev).to(torch.bfloat16),
-                a=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16),
-                b=torch.randn(B, hv, generator=g, device=dev).to(torch.bfloat16)) for _ in range(P)]
-    o = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
-    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device=dev)   # stream-ordered: shared
-    z = torch.randn(B, hv, 128, generator=g, device=dev).to(torch.bfloat16)
-    nrm = 1.0 + 0.1 * torch.randn(128, generator=g, device=dev)
-    y = torch.empty(B, hv, 128, dtype=torch.bfloat16, device=dev)
-    gate = bx.out_gate(z, nrm, 1e-6, None, y)
+    for l in range(L):
+        p = D["params"][l]
+        layers.append(dict(w=to_dev(p["w"]), A_log=to_dev(p["A_log"]), dt=to_dev(p["dt_bias"]), state=to_dev(st0),
+                           cs=to_dev(D["cs0"])))
+    ins = [dict(x=to_dev(t["x"]), a=to_dev(t["a"]), b=to_dev(t["b"])) for t in D["tokens"]]
+    out = torch.empty(B, hv, 128, dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, B), dtype=torch.uint8, device="cuda")
+    z, nrm = to_dev(D["gate"]["z"]), to_dev(D["gate"]["nrm"])
+    gate = bx.out_gate(z, nrm, 1e-6, None, out)
     stream = torch.cuda.current_stream()
-    lib = bx.lib()
-    import ctypes
-    cfg_ref = ctypes.byref(cfg)
-    s_ptr = stream.cuda_stream
-
-    gate_ref = ctypes.byref(gate)
+    lib, cfg_ref, gate_ref, s_ptr = bx.lib(), ctypes.byref(cfg), ctypes.byref(gate), stream.cuda_stream
 
     def launch(i):
         Ly, In = layers[i % L], ins[i % P]
@@ -92,69 +343,45 @@ def decode_bench(args, gated=False):
                                            ws.data_ptr(), s_ptr)
         return lib.ix_gdn_decode(cfg_ref, B, In["x"].data_ptr(), Ly["cs"].data_ptr(), Ly["w"].data_ptr(),
                                  In["a"].data_ptr(), In["b"].data_ptr(), Ly["A_log"].data_ptr(), Ly["dt"].data_ptr(),
-                                 Ly["state"].data_ptr(), None, o.data_ptr(), ws.data_ptr(), s_ptr)
+                                 Ly["state"].data_ptr(), None, out.data_ptr(), ws.data_ptr(), s_ptr)
 
     for i in range(args.warmup):
         bx.check("ix_gdn_decode", launch(i))
-    torch.cuda.synchronize()
+    sec = timed(stream, launch, args.steps)            # the timed region: K back-to-back launches
     K = args.steps
-    # Timed region: K back-to-back launches on `stream`, bracketed by HIP events recorded on
-    # that same stream. Every launch's status is checked after the region.
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    rcs = []
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for i in range(K):
-        rcs.append(launch(i))
-    t1.record(stream)
-    torch.cuda.synchronize()
-    for rc in rcs:
-        bx.check("ix_gdn_decode", rc)
-    total_ms = t0.elapsed_time(t1)
-    avg_launch_s = total_ms / K / 1e3          # average launch duration seen by the stream
+    avg_launch_s = sec / K
     state_bytes = 2 * B * hv * STATE_TILE
     achieved = state_bytes / avg_launch_s / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "decode_traffic.json")
-    if os.path.exists(tf) and B == 64 and L == 4:
-        traffic = json.load(open(tf))["bytes_per_launch"]      # PMC-measured HBM bytes per launch
-    return dict(
-        tokens_per_s=B * K / (total_ms / 1e3),
-        ms_per_step=total_ms / K,
-        avg_kernel_us=avg_launch_s * 1e6,
+    res = dict(
+        tokens_per_s=B * K / sec, ms_per_step=sec * 1e3 / K, avg_kernel_us=avg_launch_s * 1e6,
         state_bytes_per_launch=state_bytes,
         roofline=dict(bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                      frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic),
+                      frac=round(achieved / HBM_PEAK_GBS, 4)),
+        cs=[to_host(Ly["cs"]) for Ly in layers], st=[state_host(Ly["state"]) for Ly in layers], out=to_host(out),
     )
+    del layers, ins
+    torch.cuda.empty_cache()
+    return res
 
 
-def window_bench(args, K=4, iters=64):
+def window_leg(args, D, W, O, K=4, iters=64):
     """Speculative window at B = 64: ix_gdn_decode_window over K draft tokens, then
     ix_gdn_commit_window with all K accepted (the most state work), layers rotated as in the
-    decode leg. Reports microseconds per call and the state GB/s of each (verify reads the
-    state once, commit reads and writes it once)."""
+    decode leg. One verify + commit on layer 0 is checked against the CPU replay first."""
     import torch
 
     import baloon_amd as bx
 
     cfg = bx.make_cfg()
     B, L = args.batch, args.layers
-    C, hv = cfg.channels, cfg.h_v
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x6D4E0005)
-    layers = [dict(w=(torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16),
-                   A_log=torch.rand(hv, generator=g, device=dev) * 2.77,
-                   dt=torch.randn(hv, generator=g, device=dev) * 0.1,
-                   state=torch.randn(B, hv, 128, 128, generator=g, device=dev) * 0.02,
-                   cs=torch.randn(B, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16))
-              for _ in range(L)]
-    x = torch.randn(B, K, C, generator=g, device=dev).to(torch.bfloat16)
-    a = torch.randn(B, K, hv, generator=g, device=dev).to(torch.bfloat16)
-    b = torch.randn(B, K, hv, generator=g, device=dev).to(torch.bfloat16)
-    o = torch.empty(B, K, hv, 128, dtype=torch.bfloat16, device=dev)
-    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device=dev)
-    acc = torch.full((B,), K, dtype=torch.int32, device=dev)
+    hv = cfg.h_v
+    st0 = np.ascontiguousarray(np.swapaxes(D["state0"], -1, -2))
+    layers = [dict(w=to_dev(p["w"]), A_log=to_dev(p["A_log"]), dt=to_dev(p["dt_bias"]), state=to_dev(st0),
+                   cs=to_dev(D["cs0"])) for p in D["params"][:L]]
+    x, a, b = to_dev(W["x"]), to_dev(W["a"]), to_dev(W["b"])
+    o = torch.empty(B, K, hv, 128, dtype=torch.bfloat16, device="cuda")
+    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
+    acc = torch.full((B,), K, dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
 
     def verify(i):
@@ -166,30 +393,28 @@ def window_bench(args, K=4, iters=64):
         Ly = layers[i % L]
         return bx.ix_gdn_commit_window(cfg, B, K, acc, x, rec, Ly["cs"], Ly["state"], stream)
 
+    bx.check("ix_gdn_decode_window", verify(0))
+    bx.check("ix_gdn_commit_window", commit(0))
+    torch.cuda.synchronize()
+    gate = O.gate_window(D, W, B, K, to_host(o), to_host(layers[0]["cs"]), state_host(layers[0]["state"]))
     out = {}
     for name, fn in (("verify", verify), ("commit", commit)):
         for i in range(8):
             bx.check(name, fn(i))
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        rcs = [fn(i) for i in range(iters)]
-        e1.record(stream)
-        torch.cuda.synchronize()
-        for rc in rcs:
-            bx.check(name, rc)
-        out[name] = e0.elapsed_time(e1) * 1e3 / iters
+        out[name] = timed(stream, fn, iters) * 1e6 / iters
     sb = B * hv * STATE_TILE
+    del layers
+    torch.cuda.empty_cache()
     return dict(K=K, B=B, verify_us=round(out["verify"], 2), commit_us=round(out["commit"], 2),
                 verify_state_gbs=round(sb / out["verify"] / 1e3, 1),
                 commit_state_gbs=round(2 * sb / out["commit"] / 1e3, 1),
-                us_per_token_window=round((out["verify"] + out["commit"]) / K, 2))
+                us_per_token_window=round((out["verify"] + out["commit"]) / K, 2), check=gate)
 
 
-def in_proj_bench(args, hidden=2048, iters=100):
-    """The layer's input projection at the decode batch: y = h W^T for B = 64 rows, hidden
-    2048 (Qwen3-Next), N = 12352 outputs (x | z | a | b). Weight-streaming bound: reports
-    microseconds per call, the weight bytes' GB/s and TFLOP/s."""
+def in_proj_leg(args, O, hidden=2048, iters=100):
+    """The layer's input projection at the decode batch: [x | z | a | b] = h W^T for B = 64
+    rows, hidden 2048 (Qwen3-Next), N = 12352 outputs. Weight-streaming bound: 8 rotated copies
+    of W (405 MB, more than the 256 MB MALL). One call is checked against the double reference."""
     import torch
 
     import baloon_amd as bx
@@ -197,119 +422,117 @@ def in_proj_bench(args, hidden=2048, iters=100):
     cfg = bx.make_cfg()
     B = args.batch
     N = bx.ix_gdn_in_proj_width(cfg)
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x6D4E0006)
-    nw = 8                                                    # rotated weight copies: 8 x 50.6 MB exceeds the 256 MB MALL
-    ws = [(torch.randn(N, hidden, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(nw)]
-    h = torch.randn(B, hidden, generator=g, device=dev).to(torch.bfloat16)
-    x = torch.empty(B, cfg.channels, dtype=torch.bfloat16, device=dev)
-    z = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device=dev)
-    a = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device=dev)
-    b = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device=dev)
+    h_np, w_np = O.proj_data(B, hidden, N)
+    h, w0 = to_dev(h_np), to_dev(w_np)
+    nw = 8
+    ws = [w0] + [w0.clone() for _ in range(nw - 1)]
+    x = torch.empty(B, cfg.channels, dtype=torch.bfloat16, device="cuda")
+    z = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
+    a = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device="cuda")
+    b = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(B, N, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
+    bx.check("ix_gdn_in_proj", bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[0], x, z, a, b, y, stream))
+    torch.cuda.synchronize()
+    err = O.gate_proj(h_np, w_np, to_host(y))
     for i in range(8):
         bx.check("ix_gdn_in_proj", bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[i % nw], x, z, a, b, None, stream))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    rcs = [bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[i % nw], x, z, a, b, None, stream) for i in range(iters)]
-    e1.record(stream)
-    torch.cuda.synchronize()
-    for rc in rcs:
-        bx.check("ix_gdn_in_proj", rc)
-    us = e0.elapsed_time(e1) * 1e3 / iters
+    us = timed(stream, lambda i: bx.ix_gdn_in_proj(cfg, B, hidden, h, ws[i % nw], x, z, a, b, None, stream),
+               iters) * 1e6 / iters
     wbytes = N * hidden * 2
+    del ws
+    torch.cuda.empty_cache()
     return dict(B=B, hidden=hidden, N=N, us=round(us, 2), weight_gbs=round(wbytes / us / 1e3, 1),
-                tflops=round(2.0 * B * hidden * N / us / 1e6, 2))
+                tflops=round(2.0 * B * hidden * N / us / 1e6, 2), check=dict(err_x_magnitude=err))
 
 
-def decode_latency(iters=200):
-    """Configuration 1: one decode token at B = 1 (2 MiB state), microseconds per call."""
+def latency_leg(O, iters=200, graph_steps=32, graph_replays=20):
+    """Configuration 1: one decode token at B = 1 (2 MiB state), microseconds per call: eager
+    back-to-back launches, and the same launches captured once in a HIP graph and replayed
+    (launch-free; the calls record one kernel each and no memset)."""
     import torch
 
     import baloon_amd as bx
 
     cfg = bx.make_cfg()
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x6D4E0001)
-    C, hv = cfg.channels, cfg.h_v
-    w = (torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16)
-    A_log = torch.rand(hv, generator=g, device=dev) * 2.77
-    dt = torch.randn(hv, generator=g, device=dev) * 0.1
-    st = torch.randn(1, hv, 128, 128, generator=g, device=dev) * 0.02
-    cs = torch.randn(1, C, cfg.d_conv - 1, generator=g, device=dev).to(torch.bfloat16)
-    x = torch.randn(1, C, generator=g, device=dev).to(torch.bfloat16)
-    a = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
-    b = torch.randn(1, hv, generator=g, device=dev).to(torch.bfloat16)
-    o = torch.empty(1, hv, 128, dtype=torch.bfloat16, device=dev)
-    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, 1), dtype=torch.uint8, device=dev)
+    D = O.latency_data()
+    p = D["params"]
+    w, A_log, dt = to_dev(p["w"]), to_dev(p["A_log"]), to_dev(p["dt_bias"])
+    st, cs = state_dev(D["state0"]), to_dev(D["cs0"])
+    toks = [dict(x=to_dev(t["x"]), a=to_dev(t["a"]), b=to_dev(t["b"])) for t in D["tokens"]]
+    o = torch.empty(1, cfg.h_v, 128, dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(bx.ix_gdn_decode_workspace_size(cfg, 1), dtype=torch.uint8, device="cuda")
+
+    def call(i, stream):
+        t = toks[i % len(toks)]
+        return bx.ix_gdn_decode(cfg, 1, t["x"], cs, w, t["a"], t["b"], A_log, dt, st, None, o, ws, stream)
+
     stream = torch.cuda.current_stream()
-    for _ in range(20):
-        bx.check("ix_gdn_decode", bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, ws, stream))
+    for i in range(20):
+        bx.check("ix_gdn_decode", call(i, stream))
+    eager_us = timed(stream, lambda i: call(i, stream), iters) * 1e6 / iters
+
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        bx.check("ix_gdn_decode", call(0, side))
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream()
+        for i in range(graph_steps):
+            bx.check("ix_gdn_decode", call(i, cap))
+    torch.cuda.synchronize()
+    graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    rcs = [bx.ix_gdn_decode(cfg, 1, x, cs, w, a, b, A_log, dt, st, None, o, ws, stream) for _ in range(iters)]
-    e1.record(stream)
+    e0.record()
+    for _ in range(graph_replays):
+        graph.replay()
+    e1.record()
     torch.cuda.synchronize()
-    for rc in rcs:
-        bx.check("ix_gdn_decode", rc)
-    return round(e0.elapsed_time(e1) * 1e3 / iters, 2)
+    graph_us = e0.elapsed_time(e1) * 1e3 / (graph_replays * graph_steps)
+    return round(eager_us, 2), round(graph_us, 2)
 
 
-PREFILL_FLOP_PER_TOKEN = 5_767_168     # 2C^2(3d_k+2d_v) + 6 C d_k d_v per (v head, chunk of 64) / 64, x 32 heads
-MFMA_BF16_PEAK_TFLOPS = 2500.0
-
-
-def prefill_bench(T=4096, iters=10):
-    """Configuration 3: ix_gdn_prefill of one T-token sequence from a zero state."""
+def prefill_leg(O, T=4096, iters=10):
+    """Configuration 3: ix_gdn_prefill of one T-token sequence from a zero state. Every call
+    starts from zeroed states (the zero fills, 2.1 MB, are inside the timed region), so the
+    outputs and states left by the last timed call are checked against the CPU replay."""
     import torch
 
     import baloon_amd as bx
 
     cfg = bx.make_cfg()
-    dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x6D4E0003)
-    C, hv = cfg.channels, cfg.h_v
-    w = (torch.randn(C, cfg.d_conv, generator=g, device=dev) * 0.1).to(torch.bfloat16)
-    A_log = torch.rand(hv, generator=g, device=dev) * 2.77
-    dt = torch.randn(hv, generator=g, device=dev) * 0.1
-    x = torch.randn(T, C, generator=g, device=dev).to(torch.bfloat16)
-    a = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
-    b = torch.randn(T, hv, generator=g, device=dev).to(torch.bfloat16)
-    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
-    st = torch.zeros(1, hv, 128, 128, device=dev)
-    cs = torch.zeros(1, C, cfg.d_conv - 1, dtype=torch.bfloat16, device=dev)
-    o = torch.empty(T, hv, 128, dtype=torch.bfloat16, device=dev)
+    D = O.prefill_data(T)
+    p, tok = D["params"], D["tokens"]
+    w, A_log, dt = to_dev(p["w"]), to_dev(p["A_log"]), to_dev(p["dt_bias"])
+    x, a, b = to_dev(tok["x"]), to_dev(tok["a"]), to_dev(tok["b"])
+    cu = torch.tensor([0, T], dtype=torch.int32, device="cuda")
+    st = torch.zeros(1, cfg.h_v, 128, 128, device="cuda")
+    cs = torch.zeros(1, cfg.channels, cfg.d_conv - 1, dtype=torch.bfloat16, device="cuda")
+    o = torch.empty(T, cfg.h_v, 128, dtype=torch.bfloat16, device="cuda")
     need = bx.ix_gdn_prefill_workspace_size(cfg, 1, T)
-    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
     stream = torch.cuda.current_stream()
 
-    def run():
+    def run(i):
         st.zero_()
         cs.zero_()
         return bx.ix_gdn_prefill(cfg, 1, T, cu, x, cs, w, a, b, A_log, dt, st, None, o, ws, need, stream)
 
-    for _ in range(2):
-        bx.check("ix_gdn_prefill", run())
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # the zero fills of the state and conv state (2.1 MB) are inside the region
-    e0.record(stream)
-    rcs = [run() for _ in range(iters)]
-    e1.record(stream)
-    torch.cuda.synchronize()
-    for rc in rcs:
-        bx.check("ix_gdn_prefill", rc)
-    sec = e0.elapsed_time(e1) / 1e3 / iters
+    for i in range(2):
+        bx.check("ix_gdn_prefill", run(i))
+    sec = timed(stream, run, iters) / iters
     tflops = PREFILL_FLOP_PER_TOKEN * T / sec / 1e12
+    check = O.gate_prefill(D, T, to_host(cs), state_host(st), to_host(o))
+    del ws
+    torch.cuda.empty_cache()
     return dict(T=T, tokens_per_s=round(T / sec, 1), us_per_call=round(sec * 1e6, 1),
                 mfma=dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                           frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)),
-                workspace_mib=round(need / 2 ** 20, 1))
+                workspace_mib=round(need / 2 ** 20, 1), check=check)
 
 
 def hbm_ceiling(nbuf=4, mib=128, iters=20):
@@ -331,61 +554,13 @@ def hbm_ceiling(nbuf=4, mib=128, iters=20):
     return round(2 * (mib << 20) / sec / 1e9, 1)
 
 
-def cpu_baseline(args):
-    """Oracle (C port of the reference's double recurrence, tests/test_gdn.cu:22-26, extended
-    with the fused conv/gates/L2) timed on this host's cores over a bounded sample of the same
-    workload: B = 64 sequences, decode steps until the time budget is used."""
-    import numpy as np
-
-    import oracle
-    from oracle import inputs
-
-    cfg = oracle.make_cfg()
-    B = args.batch
-    seed = inputs.seed_for(2)
-    p = inputs.layer_params(cfg, seed)
-    s = inputs.initial_states(cfg, seed, B)
-    toks = [inputs.token_inputs(cfg, seed, B, step=i) for i in range(2)]
-    ncores = min(16, os.cpu_count() or 1)
-    out = {}
-    for cores in sorted({1, ncores}):
-        cs, st = s["conv_state"], s["state"].astype(np.float64)
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            t = toks[steps % 2]
-            cs, st, _ = oracle.decode(cfg, B, t["x"], cs, p["w"], t["a"], t["b"], p["A_log"], p["dt_bias"], st,
-                                      nthreads=cores)
-            steps += 1
-            el = time.perf_counter() - t0
-            if el >= args.cpu_seconds or steps >= 256:
-                break
-        out[cores] = (B * steps / el, steps, el)
-    best = max(out)
-    v, steps, el = out[best]
-    # prefill: token-by-token recurrence of one sequence (configuration 3's shape), bounded sample
-    Tp = 256
-    tok = inputs.token_inputs(cfg, inputs.seed_for(3), Tp)
-    st0 = inputs.initial_states(cfg, inputs.seed_for(3), 1, state_std=0.0, conv_std=0.0)
-    pre = {}
-    for cores in sorted({1, ncores}):
-        t0 = time.perf_counter()
-        oracle.prefill(cfg, [0, Tp], tok["x"], st0["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
-                       p["dt_bias"], st0["state"], nthreads=cores)
-        pre[cores] = Tp / (time.perf_counter() - t0)
-    cpu_model = ""
-    try:
-        for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                cpu_model = ln.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return dict(value=round(v, 1), unit="tokens/s", cores=best, kind="port", nproc=os.cpu_count(),
-                cpu_model=cpu_model,
-                sample=f"B={B} decode, {steps} steps in {el:.1f} s on {best} threads (oracle/gdn_oracle.c, double)",
-                value_1core=round(out[1][0], 1),
-                prefill_tokens_per_s=round(pre[best], 1), prefill_tokens_per_s_1core=round(pre[1], 1),
-                prefill_sample=f"one sequence of {Tp} tokens, token-by-token recurrence")
+def replayed_traffic(args):
+    """HBM bytes per launch of the headline decode kernel from the committed rocprofv3 --pmc
+    (FETCH_SIZE, WRITE_SIZE) runs of this workload; not measured in this run."""
+    if not os.path.exists(TRAFFIC_FILE) or args.batch != 64 or args.layers != 4:
+        return None, None
+    t = json.load(open(TRAFFIC_FILE))
+    return t["bytes_per_launch"], f"replayed from {os.path.relpath(TRAFFIC_FILE, ROOT)} ({t['source']})"
 
 
 def main():
@@ -400,14 +575,44 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     torch.cuda.synchronize()
-    d = decode_bench(args)
-    dg = decode_bench(args, gated=True)
-    win = window_bench(args)
-    ip = in_proj_bench(args)
-    lat = decode_latency()
-    pf = prefill_bench()
+    O = CpuBaselineLeg()
+    D = O.decode_data(args.batch, args.layers, args.inputs)
+
+    d = decode_leg(args, D)
+    dg = decode_leg(args, D, gated=True)
+    win = window_leg(args, D, O.window_tokens(args.batch, 4), O)
+    ip = in_proj_leg(args, O)
+    lat_eager, lat_graph = latency_leg(O)
+    pf = prefill_leg(O)
     ceiling = hbm_ceiling()
-    cpu = None if args.no_cpu else cpu_baseline(args)
+
+    # the CPU replay of the timed decode sequence: the CPU baseline, and the decode gate
+    order = list(range(args.warmup)) + list(range(args.steps))
+    dcheck = O.gate_decode(D, order, args, d, dg)
+    cpu = dict(value=round(O.record["decode"]["tokens_per_s"], 1), unit="tokens/s", cores=O.nt, kind="port",
+               nproc=os.cpu_count(),
+               sample=(f"the benchmark's own decode sequence: {len(order)} steps of B={args.batch} "
+                       f"({args.layers} layers) in {O.record['decode']['sec']:.1f} s on {O.nt} threads "
+                       "(oracle/gdn_oracle.c, double)"),
+               prefill_tokens_per_s=round(O.record["prefill"]["tokens_per_s"], 1),
+               prefill_sample=f"one sequence of {pf['T']} tokens, token-by-token recurrence on {O.nt} threads")
+    if not args.no_cpu:
+        v1, n1 = O.cpu_decode_1core(D, args)
+        cpu.update(value_1core=round(v1, 1), sample_1core=f"{n1} steps of B={args.batch} on 1 thread",
+                   prefill_tokens_per_s_1core=round(O.cpu_prefill_1core(O.prefill_data(pf["T"])), 1))
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu["cpu_model"] = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+
+    if O.failures:
+        print(f"bench.py: {len(O.failures)} correctness check(s) failed; no result line", file=sys.stderr)
+        sys.exit(3)
+    traffic, traffic_src = replayed_traffic(args)
+    roofline = dict(d["roofline"], traffic=traffic, traffic_source=traffic_src)
     line = {
         "metric": "GDN decode tokens/s + state HBM GB/s (%peak) at B=64; prefill tok/s T=4096",
         "value": round(d["tokens_per_s"], 1),
@@ -420,20 +625,24 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic",
+        "data": "synthetic (seeded generator of oracle/inputs.py)",
         "config": {"workload": "C2 batched GDN decode: B=64, h_k=16, h_v=32, d=128, fused conv k=4, "
                                f"{args.layers} layers rotated (state {args.layers}x128 MiB)",
                    "B": args.batch, "layers": args.layers, "parallelism": "single-gpu"},
         "avg_kernel_us": round(d["avg_kernel_us"], 2),
         "state_gbs": d["roofline"]["achieved"],
         "hbm_inplace_ceiling_gbs": ceiling,
-        "decode_b1_us_per_token": lat,
+        "decode_b1_us_per_token": lat_eager,
+        "decode_b1_us_per_token_graph": lat_graph,
         "decode_gated": {"avg_kernel_us": round(dg["avg_kernel_us"], 2), "state_gbs": dg["roofline"]["achieved"],
                          "note": "same step with the gated RMS output norm fused in (bf16 y instead of bf16 o)"},
         "spec_window": win,
         "in_proj": ip,
         "prefill": pf,
-        "roofline": d["roofline"],
+        "correctness": dict(gated="every leg checked against the CPU replay (oracle/); tolerances: fp32 o 1e-3 "
+                                  "abs beyond bf16 rounding, state max|d|/max|ref| 1e-4, conv state bit-exact",
+                            decode=dcheck),
+        "roofline": roofline,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

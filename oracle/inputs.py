@@ -36,37 +36,59 @@ def seed_for(config_id: int) -> int:
 
 
 class Gen:
+    _CHUNK = 1 << 22          # normals per pass: bounded temporaries, same values
+
     def __init__(self, seed: int):
         self.seed = np.uint64(seed)
 
-    def _bits(self, tid: int, n: int) -> np.ndarray:
-        key = _mix(np.array([self.seed ^ _mix(np.array([np.uint64(tid)]))[0]], dtype=np.uint64))[0]
+    def _key(self, tid: int) -> np.uint64:
+        return _mix(np.array([self.seed ^ _mix(np.array([np.uint64(tid)]))[0]], dtype=np.uint64))[0]
+
+    @staticmethod
+    def _bits_at(key: np.uint64, start: int, n: int) -> np.ndarray:
+        """mix(i + key) for counters i = start .. start + n - 1."""
         if n >= 1 << 16:                 # the same integers from the C oracle library, much faster
             from . import lib
             out = np.empty(n, dtype=np.uint64)
-            lib().ixo_mix_counter(int(key), n, out.ctypes.data_as(ctypes.c_void_p))
+            with np.errstate(over="ignore"):
+                k = int((key + np.uint64(start)) & _M)
+            lib().ixo_mix_counter(k, n, out.ctypes.data_as(ctypes.c_void_p))
             return out
         with np.errstate(over="ignore"):
-            return _mix((np.arange(n, dtype=np.uint64) + key) & _M)
+            return _mix((np.arange(start, start + n, dtype=np.uint64) + key) & _M)
+
+    def _bits(self, tid: int, n: int) -> np.ndarray:
+        return self._bits_at(self._key(tid), 0, n)
 
     def uniform(self, tid: int, shape, lo=0.0, hi=1.0) -> np.ndarray:
         n = int(np.prod(shape))
         u = (self._bits(tid, n) >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
         return (lo + (hi - lo) * u).reshape(shape)
 
+    def _normal_into(self, tid: int, n: int, std, mean, out: np.ndarray, convert) -> np.ndarray:
+        key = self._key(tid)
+        for lo in range(0, n, self._CHUNK):
+            m = min(self._CHUNK, n - lo)
+            b = self._bits_at(key, 2 * lo, 2 * m)      # normal i uses counters 2i and 2i + 1
+            u1 = (b[0::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+            u2 = (b[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
+            z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * math.pi * u2)
+            out[lo:lo + m] = convert(mean + std * z)
+        return out
+
     def normal(self, tid: int, shape, std=1.0, mean=0.0) -> np.ndarray:
         n = int(np.prod(shape))
-        b = self._bits(tid, 2 * n)
-        u1 = (b[0::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-        u2 = (b[1::2] >> np.uint64(11)).astype(np.float64) * (1.0 / 9007199254740992.0)
-        z = np.sqrt(-2.0 * np.log1p(-u1)) * np.cos(2.0 * math.pi * u2)
-        return (mean + std * z).reshape(shape)
+        return self._normal_into(tid, n, std, mean, np.empty(n, np.float64), lambda v: v).reshape(shape)
 
     def normal_bf16(self, tid: int, shape, std=1.0) -> np.ndarray:
-        return bf16.from_f32(self.normal(tid, shape, std).astype(np.float32))
+        n = int(np.prod(shape))
+        return self._normal_into(tid, n, std, 0.0, np.empty(n, np.uint16),
+                                 lambda v: bf16.from_f32(v.astype(np.float32))).reshape(shape)
 
     def normal_f32(self, tid: int, shape, std=1.0) -> np.ndarray:
-        return self.normal(tid, shape, std).astype(np.float32)
+        n = int(np.prod(shape))
+        return self._normal_into(tid, n, std, 0.0, np.empty(n, np.float32),
+                                 lambda v: v.astype(np.float32)).reshape(shape)
 
 
 # Tensor ids (stable; step-dependent tensors add step * 0x100).

@@ -74,12 +74,17 @@ def state_from_dev(t) -> np.ndarray:
 
 
 def bf16_excess_err(got_bits: np.ndarray, ref_f64: np.ndarray) -> float:
-    """max(|bf16 - ref| - half a bf16 ulp of ref): the error beyond bf16's own rounding."""
+    """max(|bf16 - ref| - half a bf16 ulp): the error beyond bf16's own rounding."""
     ref = np.asarray(ref_f64, dtype=np.float64)
-    got = bf16.to_f32(got_bits).astype(np.float64)
-    mag = np.abs(ref.astype(np.float32)).view(np.uint32) & np.uint32(0x7F800000)   # 2^e of |ref|
-    ulp = (mag.view(np.float32).astype(np.float64)) * 2.0 ** -7
-    half = np.maximum(ulp / 2, 2.0 ** -133)
+    got32 = bf16.to_f32(got_bits)
+    got = got32.astype(np.float64)
+
+    def binade(v):   # 2^e with 2^e <= |v| < 2^(e+1)
+        return (np.abs(v).view(np.uint32) & np.uint32(0x7F800000)).view(np.float32).astype(np.float64)
+
+    # half a bf16 ulp of whichever of ref and the output lies in the higher binade (the rounding
+    # may cross a power of two)
+    half = np.maximum(np.maximum(binade(ref.astype(np.float32)), binade(got32)) * 2.0 ** -8, 2.0 ** -133)
     return float(np.max(np.abs(got - ref) - half)) if ref.size else 0.0
 
 

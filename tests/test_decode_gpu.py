@@ -205,3 +205,44 @@ def test_workspace_and_group_kernels_agree():
         assert float(np.max(np.abs(oa - ob))) <= 1e-5
     np.testing.assert_array_equal(host(ra.d_cs), host(rb.d_cs))
     assert oracle.rel_err(host(ra.d_st), host(rb.d_st)) <= 1e-5
+
+
+@pytest.mark.parametrize("ws", WS)
+def test_graph_replays_match_eager(ws):
+    # K decode calls captured once in a HIP graph (each records one kernel and no memset) and
+    # replayed three times, the states restored by eager copies between replays: every replay
+    # gives the eager calls' outputs and states bit for bit.
+    torch = _torch()
+    cfg = bx.make_cfg()
+    B, K, seed = 3, 4, inputs.seed_for(1) + 41
+    r = Run(cfg, B, seed, ws=ws)
+    toks = [inputs.token_inputs(cfg, seed, B, step=k) for k in range(K)]
+    d_toks = [(dev(t["x"]), dev(t["a"]), dev(t["b"])) for t in toks]
+    outs = [torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda") for _ in range(K)]
+    cs0, st0 = r.d_cs.clone(), r.d_st.clone()
+
+    def calls(stream):
+        for k, (x, a, b) in enumerate(d_toks):
+            assert bx.ix_gdn_decode(cfg, B, x, r.d_cs, r.d_w, a, b, r.d_A, r.d_dt, r.d_st, outs[k], None, r.ws,
+                                    stream) == 0
+
+    calls(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    eager = ([host(o).copy() for o in outs], host(r.d_cs).copy(), host(r.d_st).copy())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls(torch.cuda.current_stream())
+    for rep in range(3):
+        r.d_cs.copy_(cs0)
+        r.d_st.copy_(st0)
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for k in range(K):
+            np.testing.assert_array_equal(host(outs[k]), eager[0][k], err_msg=f"replay {rep} output {k}")
+        np.testing.assert_array_equal(host(r.d_cs), eager[1], err_msg=f"replay {rep} conv state")
+        np.testing.assert_array_equal(host(r.d_st), eager[2], err_msg=f"replay {rep} state")
+        if ws:
+            assert int(r.ws.count_nonzero()) == 0, "counters not left zeroed"
