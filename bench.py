@@ -60,7 +60,15 @@ def parse():
     ap.add_argument("--inputs", type=int, default=8, help="distinct token input sets cycled through")
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the single-core CPU samples (the multi-core replays, which gate the run, always run)")
-    return ap.parse_args()
+    ap.add_argument("--legs", default="all",
+                    help="comma-separated subset of decode,gated,window,in_proj,latency,prefill,ceiling for "
+                         "profiling passes; the result line needs all of them (the default)")
+    a = ap.parse_args()
+    known = ("decode", "gated", "window", "in_proj", "latency", "prefill", "ceiling")
+    a.legs = set(known) if a.legs == "all" else set(a.legs.split(","))
+    if not a.legs <= set(known):
+        ap.error(f"--legs: unknown {sorted(a.legs - set(known))}")
+    return a
 
 
 def cpu_share() -> int:
@@ -563,6 +571,36 @@ def replayed_traffic(args):
     return t["bytes_per_launch"], f"replayed from {os.path.relpath(TRAFFIC_FILE, ROOT)} ({t['source']})"
 
 
+def partial_run(args, O):
+    """A subset of the legs (--legs), for profiling passes: each leg runs and is gated as in the
+    full run, and one JSON object with their results is printed (not the result line)."""
+    out = {}
+    D = O.decode_data(args.batch, args.layers, args.inputs) if args.legs & {"decode", "gated", "window"} else None
+    if "decode" in args.legs or "gated" in args.legs:
+        order = list(range(args.warmup)) + list(range(args.steps))
+        d = decode_leg(args, D) if "decode" in args.legs else None
+        dg = decode_leg(args, D, gated=True) if "gated" in args.legs else None
+        if d is not None:
+            out["decode"] = dict(avg_kernel_us=round(d["avg_kernel_us"], 2), roofline=d["roofline"],
+                                 check=O.gate_decode(D, order, args, d, dg))
+        if dg is not None:
+            out["decode_gated"] = dict(avg_kernel_us=round(dg["avg_kernel_us"], 2))
+    if "window" in args.legs:
+        out["spec_window"] = window_leg(args, D, O.window_tokens(args.batch, 4), O)
+    if "in_proj" in args.legs:
+        out["in_proj"] = in_proj_leg(args, O)
+    if "latency" in args.legs:
+        out["decode_b1_us_per_token"], out["decode_b1_us_per_token_graph"] = latency_leg(O)
+    if "prefill" in args.legs:
+        out["prefill"] = prefill_leg(O)
+    if "ceiling" in args.legs:
+        out["hbm_inplace_ceiling_gbs"] = hbm_ceiling()
+    if O.failures:
+        print(f"bench.py: {len(O.failures)} correctness check(s) failed", file=sys.stderr)
+        sys.exit(3)
+    print(json.dumps(dict(partial_legs=sorted(args.legs), **out)))
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -576,6 +614,10 @@ def main():
         sys.exit(1)
     torch.cuda.synchronize()
     O = CpuBaselineLeg()
+    legs = args.legs
+    if legs != {"decode", "gated", "window", "in_proj", "latency", "prefill", "ceiling"}:
+        partial_run(args, O)
+        return
     D = O.decode_data(args.batch, args.layers, args.inputs)
 
     d = decode_leg(args, D)

@@ -92,6 +92,14 @@ def test_config1_single_token(ws):
     run_steps(oracle.make_cfg(), 1, 1, inputs.seed_for(1), ws=ws)
 
 
+@pytest.mark.parametrize("B", [1, 2, 3, 5])
+def test_small_batches(B):
+    # Configuration 1's batch and its neighbours, over several carried steps: at small B the
+    # workspace kernel runs fewer workgroups than the chip has CUs, and each group counter
+    # and conv history still has to come out right every step.
+    run_steps(oracle.make_cfg(), B, 6, inputs.seed_for(1) + 200 + B, ws=True)
+
+
 @pytest.mark.parametrize("ws", WS)
 def test_config2_batch64_256_steps(ws):
     # Configuration 2 as stated: B=64 independent sequences, 256 consecutive decode steps with
