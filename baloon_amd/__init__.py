@@ -32,7 +32,7 @@ EXPORTS = (
     "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
     "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
-    "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_commit_window",
+    "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_decode_window_mfma", "ix_gdn_commit_window",
     "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
     "ix_gdn_version", "ix_gdn_decode_noalloc",
 )
@@ -102,6 +102,7 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_prefill_gated": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
         "ix_gdn_window_record_size": ([P, I, I], Z),
         "ix_gdn_decode_window": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_gdn_decode_window_mfma": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_commit_window": ([P, I, I, P, P, P, P, P, P], I),
         "ix_bf16_gemv": ([P, P, P, LL, LL, P], I),
         "ix_bf16_gemv_pair": ([P, P, P, LL, P, P, LL, LL, P], I),
@@ -244,6 +245,15 @@ def ix_gdn_decode_window(cfg: Cfg, B, K, x, conv_state, conv_w, a, b, A_log, dt_
     return lib().ix_gdn_decode_window(ctypes.byref(cfg), B, K, _ptr(x), _ptr(conv_state), _ptr(conv_w), _ptr(a),
                                       _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o), _ptr(o_bf16),
                                       _ptr(record), _stream(s))
+
+
+def ix_gdn_decode_window_mfma(cfg: Cfg, B, K, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None,
+                              o_bf16=None, record=None, s=None) -> int:
+    """ix_gdn_decode_window on the matrix cores: outputs to fp32 rounding of the exact verify,
+    the same record."""
+    return lib().ix_gdn_decode_window_mfma(ctypes.byref(cfg), B, K, _ptr(x), _ptr(conv_state), _ptr(conv_w),
+                                           _ptr(a), _ptr(b), _ptr(A_log), _ptr(dt_bias), _ptr(state), _ptr(o),
+                                           _ptr(o_bf16), _ptr(record), _stream(s))
 
 
 def ix_gdn_commit_window(cfg: Cfg, B, K, accepted, x, record, conv_state, state, s=None) -> int:

@@ -156,4 +156,46 @@ __device__ __forceinline__ void out_gate_head(const OutGate& g, size_t row, floa
     out_gate_apply(g, row, lo, hi, wave_sum_sq(lo), wave_sum_sq(hi), lane);
 }
 
+// ---------------------------------------------------------------------------------------
+// Split-bf16 products on v_mfma_f32_16x16x32_bf16: an fp32 operand x is split into
+// hi = RNE(x) and lo = RNE(x - hi), and a product is hi*hi + hi*lo + lo*hi in fp32
+// accumulators (relative error ~2^-16, against 2^-8 for one bf16 product).
+// ---------------------------------------------------------------------------------------
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u4x __attribute__((ext_vector_type(4)));
+typedef float v4 __attribute__((ext_vector_type(4)));
+
+// k index of slot e (0..7) of lane group g (lane / 16) in an A or B operand: the row order of
+// two stacked 16 x 16 accumulator tiles (lane group g holds rows 4g..4g+3 of each), so that
+// an accumulator pair is the next product's operand as it stands, and so that a lane's 8
+// values are two runs of 4 consecutive k (16-byte loads). A and B agree on it, so the k sum
+// covers the same terms.
+__device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
+
+// Split two fp32 values into packed bf16 pairs: hi = RNE(x), lo = RNE(x - hi). The hi values
+// return to fp32 by a shift and a mask, so a pair costs one convert per plane.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    hi = pack_bf16x2(x0, x1);
+    lo = pack_bf16x2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
+}
+
+// Split 8 fp32 values into hi and lo bf16 vectors.
+__device__ __forceinline__ void split8(const float (&x)[8], bf8& hi, bf8& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) split2(x[2 * i], x[2 * i + 1], h[i], l[i]);
+    hi = __builtin_bit_cast(bf8, u4x{h[0], h[1], h[2], h[3]});
+    lo = __builtin_bit_cast(bf8, u4x{l[0], l[1], l[2], l[3]});
+}
+
+__device__ __forceinline__ v4 mfma_bf16(const bf8& a, const bf8& b, const v4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// c += A B with both operands split: hi hi + hi lo + lo hi.
+__device__ __forceinline__ v4 mfma_split(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, v4 c) {
+    c = mfma_bf16(ah, bh, c);
+    c = mfma_bf16(ah, bl, c);
+    return mfma_bf16(al, bh, c);
+}
+
 }  // namespace ixg

@@ -45,8 +45,6 @@ namespace {
 constexpr int kChunk = 64;
 constexpr int kPlanThreads = 1024;
 
-typedef float v4 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ v4 mfma4(float a, float b, v4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -320,29 +318,8 @@ __device__ __forceinline__ void commit_history(const PrefillParams& p, int ch, i
 // 4g..4g+3 of each), so the chain feeds its accumulators (S, D) to the next product as B
 // operands without moving them between lanes; A and B agree on the order of the k sum.
 // ---------------------------------------------------------------------------------------
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u4x __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int kperm(int g, int e) { return e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4); }
-
 __device__ __forceinline__ size_t frag_at(int m, int ks, int nks, int plane, int lane) {
     return ((((size_t)m * nks + ks) * 2 + plane) * kWave + lane) * 8;       // in bf16 elements
-}
-
-// Split two fp32 values into packed bf16 pairs: hi = RNE(x), lo = RNE(x - hi). The hi values
-// return to fp32 by a shift and a mask, so a pair costs one convert per plane.
-__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
-    hi = pack_bf16x2(x0, x1);
-    lo = pack_bf16x2(x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u));
-}
-
-// Split 8 fp32 values into hi and lo bf16 vectors.
-__device__ __forceinline__ void split8(const float (&x)[8], bf8& hi, bf8& lo) {
-    uint32_t h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) split2(x[2 * i], x[2 * i + 1], h[i], l[i]);
-    hi = __builtin_bit_cast(bf8, u4x{h[0], h[1], h[2], h[3]});
-    lo = __builtin_bit_cast(bf8, u4x{l[0], l[1], l[2], l[3]});
 }
 
 __device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nks, int lane, const float (&x)[8]) {
@@ -827,15 +804,6 @@ __device__ __forceinline__ void split_tiles(const v4& a, const v4& b, bf8& hi, b
     lo = __builtin_bit_cast(bf8, u4x{l0, l1, l2, l3});
 }
 
-__device__ __forceinline__ v4 mfma_bf16(const bf8& a, const bf8& b, const v4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-// c += A B with both operands split: hi hi + hi lo + lo hi.
-__device__ __forceinline__ v4 mfma_split(const bf8& ah, const bf8& al, const bf8& bh, const bf8& bl, v4 c) {
-    c = mfma_bf16(ah, bh, c);
-    c = mfma_bf16(ah, bl, c);
-    return mfma_bf16(al, bh, c);
-}
 
 __device__ __forceinline__ int chain_w_slot(int q) { return q * kOpsBytes; }
 __device__ __forceinline__ int chain_k_slot(int q) { return (2 + q) * kOpsBytes; }

@@ -192,6 +192,221 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
 }
 
 // ---------------------------------------------------------------------------------------
+// verify on the matrix cores (ix_gdn_decode_window_mfma): grid (2 h_v, B), the workgroups of
+// window_verify_kernel. With S the committed state, G_t = g_0 g_1 ... g_t and
+// r(t, s) = g_{s+1} ... g_t (r(t, t) = 1), the K steps unroll to
+//   d_t = beta_t (v_t - G_t (S^T k_t) - sum_{s<t} r(t, s) (k_t . k_s) d_s)
+//   o_t = G_t (S^T q_t) + sum_{s<=t} r(t, s) (q_t . k_s) d_s
+// (k, q normalised; q with its scale). The state enters only through the 2K products
+// S^T k_t and S^T q_t: one split-bf16 MFMA product per wave, the state as the A operand
+// loaded from HBM straight into the fragments -- lane (li, lg) of wave w holds column
+// j = 64 hf + 16 w + li at key rows 32 ks + kperm(lg, e) -- and never stored. The K x K
+// products k_t . k_s and q_t . k_s come from the same token fragments. Each column then runs
+// the K-step recurrence above in fp32. Outputs agree with K ix_gdn_decode calls to fp32
+// rounding (not bit for bit); the record is computed exactly as window_verify_kernel computes
+// it, so ix_gdn_commit_window gives the same committed states after either verify.
+// ---------------------------------------------------------------------------------------
+template <int DC, int KMAX>
+__global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kernel(const WindowParams p) {
+    static_assert(KMAX == 4 || KMAX == 8 || KMAX == 16, "window size class");
+    constexpr int KP = KMAX + 1;                              // padded row of the token tables
+    // q and k rows padded to 132 floats: the token fragments read 16 rows at one column
+    // offset with 16-byte reads, which then meet in at most two ways per bank.
+    constexpr int QS = kD + 4;
+    __shared__ __align__(16) float q_s[KMAX][QS], k_s[KMAX][QS], v_s[KMAX][kHalf];
+    __shared__ float sq_s[KMAX], sk_s[KMAX], g_s[KMAX], b_s[KMAX];
+    __shared__ float kk_s[KMAX][KP], qk_s[KMAX][KP];         // k_t . k_s, q_t . k_s
+    __shared__ float sk_t[kHalf][KP], sq_t[kHalf][KP];       // S^T k_t, S^T q_t per column
+
+    const Layer& L = p.L;
+    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int li = lane & 15, lg = lane >> 4;
+    const int hf = blockIdx.x & 1, h = blockIdx.x >> 1, bseq = blockIdx.y;
+    const int src = src_of(L, h);
+    const int K = p.K;
+    const bool rec_k = hf == 0 && h == mapped_head(L, src, 0);
+
+    // Conv channel pair of this thread: 0..63 q, 64..127 k, 128..159 the half tile's v; the
+    // inputs of all K tokens at once (rows past K repeat row K-1).
+    int ch = 0, col = 0;
+    if (tid < 64) { ch = q_channel(L, src, 2 * tid); col = 2 * tid; }
+    else if (tid < 128) { ch = k_channel(L, src, 2 * (tid - 64)); col = 2 * (tid - 64); }
+    else if (tid < 128 + kHalf / 2) { ch = v_channel(L, h, hf * kHalf + 2 * (tid - 128)); col = 2 * (tid - 128); }
+    const bool conv_thread = tid < 128 + kHalf / 2;
+    ConvPair<DC> cp;
+    uint32_t xk[KMAX];
+    if (conv_thread) {
+        const uint32_t* hp = reinterpret_cast<const uint32_t*>(p.conv_state + ((size_t)bseq * L.C + ch) * (DC - 1));
+#pragma unroll
+        for (int i = 0; i < DC - 1; ++i) cp.h[i] = hp[i];
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(L.conv_w + (size_t)ch * DC);
+#pragma unroll
+        for (int i = 0; i < DC; ++i) cp.w[i] = wp[i];
+#pragma unroll
+        for (int t = 0; t < KMAX; ++t)
+            xk[t] = *reinterpret_cast<const uint32_t*>(p.x + ((size_t)bseq * K + min(t, K - 1)) * L.C + ch);
+    }
+    // Gate inputs, one thread per token (loaded ahead of the state, by threads past the conv).
+    const int gt = tid - (kThreads - KMAX);
+    uint16_t a_in = 0, b_in = 0;
+    if (gt >= 0 && gt < K) {
+        const size_t ab = ((size_t)bseq * K + gt) * L.h_v + h;
+        a_in = p.a[ab];
+        b_in = p.b[ab];
+    }
+
+    // State fragments (k-steps ks = 0..3, the two runs of 4 key rows of kperm).
+    const float* colp = p.state + (((size_t)bseq * L.h_v + h) * kD + hf * kHalf + 16 * w + li) * kD + 4 * lg;
+    v4f sf[4][2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        sf[ks][0] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(colp + 32 * ks));
+        sf[ks][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(colp + 32 * ks + 16));
+    }
+
+    // Phase 1: conv outputs, squared norms (waves 0 and 1) and gates of every token.
+    if (conv_thread) {
+        float* dst = tid < 64 ? q_s[0] : tid < 128 ? k_s[0] : v_s[0];
+        const int stride = tid < 128 ? QS : kHalf;
+#pragma unroll
+        for (int t = 0; t < KMAX; ++t) {
+            if (t >= K) break;
+            float y0, y1;
+            uint32_t nh[DC - 1];
+            cp.x = xk[t];
+            conv_pair_eval<DC>(L, cp, y0, y1, nh);
+            dst[t * stride + col] = y0;
+            dst[t * stride + col + 1] = y1;
+#pragma unroll
+            for (int i = 0; i < DC - 1; ++i) cp.h[i] = nh[i];
+            if (w < 2) {                                       // wave-uniform: q (wave 0), k (wave 1)
+                const float r = wave_sum(fmaf(y0, y0, y1 * y1));
+                if (lane == 0) (w == 0 ? sq_s : sk_s)[t] = r;
+            }
+        }
+    }
+    if (gt >= 0 && gt < K) {
+        g_s[gt] = expf(log_gate(L, h, bf16_to_f32(a_in)));
+        b_s[gt] = sigmoid_f(bf16_to_f32(b_in));
+    }
+    lds_barrier();
+
+    // The record, exactly as window_verify_kernel writes it: it depends on phase 1 only, so
+    // it is written here, where its stores overlap the products and the recurrence below.
+    for (int t = 0; t < K; ++t) {
+        const size_t row = (size_t)bseq * K + t;
+        if (rec_k && tid < kD) p.rec.k[(row * L.h_k + src) * kD + tid] = k_s[t][tid] * (1.0f / sqrtf(sk_s[t] + L.l2_eps));
+        if (tid < kHalf) p.rec.v[(row * L.h_v + h) * kD + hf * kHalf + tid] = v_s[t][tid];
+        if (hf == 0 && tid == 0) { p.rec.g[row * L.h_v + h] = g_s[t]; p.rec.bt[row * L.h_v + h] = b_s[t]; }
+    }
+
+    // Token fragments: the normalised k_t and q_t (the decode kernel's inverse norms) at this
+    // lane's key rows. Up to 8 tokens share one 16-wide operand tile: column n < K is k_n,
+    // K <= n < 2K is q_{n-K}; beyond that two tiles hold k (column n = token n) and q. With
+    // the state fragments as A: S^T k and S^T q for this wave's 16 columns. The token
+    // fragments also serve as A operands (row li of an A operand holds the same values):
+    // wave 1 forms the token products k_t . k_s and q_t . k_s.
+    v4 ak = {0.f, 0.f, 0.f, 0.f}, aq = ak, kk = ak, qk = ak;
+    constexpr bool kShared = KMAX <= 8;
+    // fragment 0: k_li (or, shared, k_li | q_{li-K}); fragment 1: q_li (unshared) or k_li (the B of k . k, q . k)
+    const bool is_k0 = li < K, is_q0 = kShared && li >= K && li < 2 * K;
+    const int row0 = is_k0 ? li : is_q0 ? li - K : 0;
+    const float s0 = is_k0 ? 1.0f / sqrtf(sk_s[row0] + L.l2_eps)
+                           : is_q0 ? L.q_scale / sqrtf(sq_s[row0] + L.l2_eps) : 0.0f;
+    const float* base0 = is_q0 ? q_s[row0] : k_s[row0];
+    const bool tok1 = li < K;
+    const int row1 = tok1 ? li : 0;
+    const float s1 = tok1 ? (kShared ? 1.0f / sqrtf(sk_s[row1] + L.l2_eps) : L.q_scale / sqrtf(sq_s[row1] + L.l2_eps))
+                          : 0.0f;
+    const float* base1 = kShared ? k_s[row1] : q_s[row1];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        float x0[8], x1[8], sx[8];
+        const int i0 = 32 * ks + 4 * lg;                        // kperm: rows i0..i0+3, i0+16..i0+19
+        const v4f a0 = *reinterpret_cast<const v4f*>(base0 + i0), a1 = *reinterpret_cast<const v4f*>(base0 + i0 + 16);
+        const v4f c0 = *reinterpret_cast<const v4f*>(base1 + i0), c1 = *reinterpret_cast<const v4f*>(base1 + i0 + 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x0[e] = a0[e] * s0;
+            x0[e + 4] = a1[e] * s0;
+            x1[e] = c0[e] * s1;
+            x1[e + 4] = c1[e] * s1;
+            sx[e] = sf[ks][0][e];
+            sx[e + 4] = sf[ks][1][e];
+        }
+        bf8 h0, l0, h1, l1, sh, sl;
+        split8(x0, h0, l0);
+        split8(x1, h1, l1);
+        split8(sx, sh, sl);
+        ak = mfma_split(sh, sl, h0, l0, ak);
+        if constexpr (kShared) {
+            if (w == 1) kk = mfma_split(h0, l0, h1, l1, kk);       // rows k_t then q_t, columns k_s
+        } else {
+            aq = mfma_split(sh, sl, h1, l1, aq);
+            if (w == 1) kk = mfma_split(h0, l0, h0, l0, kk);
+            if (w == 2) qk = mfma_split(h1, l1, h0, l0, qk);
+        }
+    }
+    // Accumulator element r of lane (li, lg) is row 4 lg + r, column li.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int jr = 16 * w + 4 * lg + r, n = 4 * lg + r;
+        if constexpr (kShared) {
+            if (li < K) sk_t[jr][li] = ak[r];
+            else if (li < 2 * K) sq_t[jr][li - K] = ak[r];
+            if (w == 1 && li < K) {
+                if (n < K) kk_s[n][li] = kk[r];
+                else if (n < 2 * K) qk_s[n - K][li] = kk[r];
+            }
+        } else {
+            if (li < KMAX) { sk_t[jr][li] = ak[r]; sq_t[jr][li] = aq[r]; }
+            if (li < KMAX && n < KMAX) {
+                if (w == 1) kk_s[n][li] = kk[r];
+                if (w == 2) qk_s[n][li] = qk[r];
+            }
+        }
+    }
+    lds_barrier();
+
+    // Phase 2: the K-step recurrence of each column (threads 0..63), outputs as they come.
+    // G_t and r(t, s) are running products of the decays (no division: G_t may underflow).
+    if (tid < kHalf) {
+        const int j = hf * kHalf + tid;
+        float d[KMAX], r[KMAX];
+        float G = 1.0f;
+#pragma unroll
+        for (int t = 0; t < KMAX; ++t) {
+            if (t >= K) break;
+            const float g = g_s[t];
+            G *= g;
+#pragma unroll
+            for (int s2 = 0; s2 < t; ++s2) r[s2] = s2 == t - 1 ? g : r[s2] * g;   // r(t, s) = r(t-1, s) g_t
+            float u = G * sk_t[tid][t];
+#pragma unroll
+            for (int s2 = 0; s2 < t; ++s2) u = fmaf(r[s2] * kk_s[t][s2], d[s2], u);
+            d[t] = (v_s[t][tid] - u) * b_s[t];
+            float ov = fmaf(qk_s[t][t], d[t], G * sq_t[tid][t]);
+#pragma unroll
+            for (int s2 = 0; s2 < t; ++s2) ov = fmaf(r[s2] * qk_s[t][s2], d[s2], ov);
+            const size_t ob = (((size_t)bseq * K + t) * L.h_v + h) * kD + j;
+            if (p.o) p.o[ob] = ov;
+            if (p.o_bf16) p.o_bf16[ob] = f32_to_bf16(ov);
+        }
+    }
+}
+
+// The window size class KMAX (4, 8 or 16 tokens) sizes the LDS tables and the registers.
+template <int KMAX>
+void launch_window_mfma(const ix_gdn_cfg* cfg, int B, const WindowParams& p, hipStream_t s) {
+    const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B), block(kThreads);
+    switch (cfg->d_conv) {
+        case 2: hipLaunchKernelGGL((window_mfma_kernel<2, KMAX>), grid, block, 0, s, p); break;
+        case 3: hipLaunchKernelGGL((window_mfma_kernel<3, KMAX>), grid, block, 0, s, p); break;
+        default: hipLaunchKernelGGL((window_mfma_kernel<4, KMAX>), grid, block, 0, s, p); break;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
 // commit: grid (2 h_v, B)
 // ---------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowParams p) {
@@ -279,12 +494,11 @@ static hipError_t window_params(const ix_gdn_cfg* cfg, int B, int K, const uint1
     return hipSuccess;
 }
 
-extern "C" hipError_t ix_gdn_decode_window(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x,
-                                           const uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
-                                           const uint16_t* b, const float* A_log, const float* dt_bias,
-                                           const float* state, float* o, uint16_t* o_bf16, void* record,
-                                           hipStream_t s) {
-    ixg::WindowParams p;
+// Validation and parameters shared by the two verify entry points.
+static hipError_t verify_params(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x, const uint16_t* conv_state,
+                                const uint16_t* conv_w, const uint16_t* a, const uint16_t* b, const float* A_log,
+                                const float* dt_bias, const float* state, float* o, uint16_t* o_bf16, void* record,
+                                ixg::WindowParams& p) {
     const hipError_t e = window_params(cfg, B, K, x, const_cast<uint16_t*>(conv_state), conv_w,
                                        const_cast<float*>(state), record, p);
     if (e != hipSuccess) return e;
@@ -296,12 +510,39 @@ extern "C" hipError_t ix_gdn_decode_window(const ix_gdn_cfg* cfg, int B, int K, 
         return hipErrorInvalidValue;
     p.L.A_log = A_log; p.L.dt_bias = dt_bias;
     p.a = a; p.b = b; p.o = o; p.o_bf16 = o_bf16;
+    return hipSuccess;
+}
+
+extern "C" hipError_t ix_gdn_decode_window(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x,
+                                           const uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                                           const uint16_t* b, const float* A_log, const float* dt_bias,
+                                           const float* state, float* o, uint16_t* o_bf16, void* record,
+                                           hipStream_t s) {
+    ixg::WindowParams p;
+    const hipError_t e = verify_params(cfg, B, K, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16,
+                                       record, p);
+    if (e != hipSuccess) return e;
     const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B), block(ixg::kThreads);
     switch (cfg->d_conv) {
         case 2: hipLaunchKernelGGL(ixg::window_verify_kernel<2>, grid, block, 0, s, p); break;
         case 3: hipLaunchKernelGGL(ixg::window_verify_kernel<3>, grid, block, 0, s, p); break;
         default: hipLaunchKernelGGL(ixg::window_verify_kernel<4>, grid, block, 0, s, p); break;
     }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ix_gdn_decode_window_mfma(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x,
+                                                const uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                                                const uint16_t* b, const float* A_log, const float* dt_bias,
+                                                const float* state, float* o, uint16_t* o_bf16, void* record,
+                                                hipStream_t s) {
+    ixg::WindowParams p;
+    const hipError_t e = verify_params(cfg, B, K, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o, o_bf16,
+                                       record, p);
+    if (e != hipSuccess) return e;
+    if (K <= 4) ixg::launch_window_mfma<4>(cfg, B, p, s);
+    else if (K <= 8) ixg::launch_window_mfma<8>(cfg, B, p, s);
+    else ixg::launch_window_mfma<16>(cfg, B, p, s);
     return hipGetLastError();
 }
 

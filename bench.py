@@ -270,7 +270,7 @@ class CpuBaselineLeg:
         return args.batch * steps / (time.perf_counter() - t0), steps
 
     # ---- window, projection and prefill gates ----
-    def gate_window(self, D, W, B, K, o_win, cs_after, st_after):
+    def gate_window(self, D, W, B, K, o_win, cs_after, st_after, o_exact=None):
         cs, st = D["cs0"].copy(), D["state0"].astype(np.float64)
         p = D["params"][0]
         errs = []
@@ -278,6 +278,8 @@ class CpuBaselineLeg:
             cs, st, ro = self.oracle.decode(self.cfg, B, W["x"][:, t], cs, p["w"], W["a"][:, t], W["b"][:, t],
                                             p["A_log"], p["dt_bias"], st, nthreads=self.nt)
             errs.append(self.check_bf16_out(f"window token {t} o", o_win[:, t], ro))
+            if o_exact is not None:
+                errs.append(self.check_bf16_out(f"window (exact verify) token {t} o", o_exact[:, t], ro))
         self.check_equal("window commit conv state", cs_after, cs)
         rel = self.check_state("window commit", st_after, st)
         return dict(o_err=max(errs), state_rel_err=rel)
@@ -373,9 +375,11 @@ def decode_leg(args, D, gated=False):
 
 
 def window_leg(args, D, W, O, K=4, iters=64):
-    """Speculative window at B = 64: ix_gdn_decode_window over K draft tokens, then
+    """Speculative window at B = 64: verify K draft tokens on the matrix cores
+    (ix_gdn_decode_window_mfma; the bit-exact ix_gdn_decode_window is timed beside it), then
     ix_gdn_commit_window with all K accepted (the most state work), layers rotated as in the
-    decode leg. One verify + commit on layer 0 is checked against the CPU replay first."""
+    decode leg. One verify of each kind and a commit on layer 0 are checked against the CPU
+    replay first."""
     import torch
 
     import baloon_amd as bx
@@ -394,6 +398,11 @@ def window_leg(args, D, W, O, K=4, iters=64):
 
     def verify(i):
         Ly = layers[i % L]
+        return bx.ix_gdn_decode_window_mfma(cfg, B, K, x, Ly["cs"], Ly["w"], a, b, Ly["A_log"], Ly["dt"],
+                                            Ly["state"], None, o, rec, stream)
+
+    def verify_exact(i):
+        Ly = layers[i % L]
         return bx.ix_gdn_decode_window(cfg, B, K, x, Ly["cs"], Ly["w"], a, b, Ly["A_log"], Ly["dt"], Ly["state"],
                                        None, o, rec, stream)
 
@@ -401,20 +410,24 @@ def window_leg(args, D, W, O, K=4, iters=64):
         Ly = layers[i % L]
         return bx.ix_gdn_commit_window(cfg, B, K, acc, x, rec, Ly["cs"], Ly["state"], stream)
 
-    bx.check("ix_gdn_decode_window", verify(0))
+    bx.check("ix_gdn_decode_window", verify_exact(0))
+    torch.cuda.synchronize()
+    o_exact = to_host(o)
+    bx.check("ix_gdn_decode_window_mfma", verify(0))
     bx.check("ix_gdn_commit_window", commit(0))
     torch.cuda.synchronize()
-    gate = O.gate_window(D, W, B, K, to_host(o), to_host(layers[0]["cs"]), state_host(layers[0]["state"]))
+    gate = O.gate_window(D, W, B, K, to_host(o), to_host(layers[0]["cs"]), state_host(layers[0]["state"]),
+                         o_exact=o_exact)
     out = {}
-    for name, fn in (("verify", verify), ("commit", commit)):
+    for name, fn in (("verify", verify), ("verify_exact", verify_exact), ("commit", commit)):
         for i in range(8):
             bx.check(name, fn(i))
         out[name] = timed(stream, fn, iters) * 1e6 / iters
     sb = B * hv * STATE_TILE
     del layers
     torch.cuda.empty_cache()
-    return dict(K=K, B=B, verify_us=round(out["verify"], 2), commit_us=round(out["commit"], 2),
-                verify_state_gbs=round(sb / out["verify"] / 1e3, 1),
+    return dict(K=K, B=B, verify_us=round(out["verify"], 2), verify_exact_us=round(out["verify_exact"], 2),
+                commit_us=round(out["commit"], 2), verify_state_gbs=round(sb / out["verify"] / 1e3, 1),
                 commit_state_gbs=round(2 * sb / out["commit"] / 1e3, 1),
                 us_per_token_window=round((out["verify"] + out["commit"]) / K, 2), check=gate)
 

@@ -216,6 +216,18 @@ hipError_t ix_gdn_decode_window(const ix_gdn_cfg* cfg, int B, int K, const uint1
                                 const uint16_t* b, const float* A_log, const float* dt_bias, const float* state,
                                 float* o, uint16_t* o_bf16, void* record, hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* The same verify on the matrix cores: the committed state enters only through the products
+ * S^T k_t and S^T q_t of the K tokens (split-bf16 MFMA, ~2^-16 relative), and the K steps are
+ * unrolled in the K-token space. Outputs agree with K ix_gdn_decode calls to fp32 rounding
+ * (within the decode tolerances of the reference's double recurrence), not bit for bit; the
+ * record is bit-identical to ix_gdn_decode_window's, so ix_gdn_commit_window then gives the
+ * same committed states. Arguments and requirements as ix_gdn_decode_window. */
+hipError_t ix_gdn_decode_window_mfma(const ix_gdn_cfg* cfg, int B, int K, const uint16_t* x,
+                                     const uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
+                                     const uint16_t* b, const float* A_log, const float* dt_bias,
+                                     const float* state, float* o, uint16_t* o_bf16, void* record,
+                                     hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* Commit a window: accepted [B] int32 device array, each clamped to [0, K]; x and record as
  * given to ix_gdn_decode_window. Sequence b's conv_state and state advance by accepted[b]
  * tokens; a sequence with accepted[b] = 0 is not touched. */

@@ -202,18 +202,22 @@ def test_window_validation_without_launch():
     for B, K in [(0, 4), (2, 0), (2, 17), (-1, 1)]:
         assert bx.ix_gdn_window_record_size(cfg, B, K) == 0
 
-    def verify(K, c=cfg, rec=p, state=p):
-        return L.ix_gdn_decode_window(ctypes.byref(c), 2, K, p, p, p, p, p, p, p, state, NULL, NULL, rec, NULL)
+    def verify(K, c=cfg, rec=p, state=p, fn=L.ix_gdn_decode_window):
+        return fn(ctypes.byref(c), 2, K, p, p, p, p, p, p, p, state, NULL, NULL, rec, NULL)
+
+    def verify_mfma(K, c=cfg, rec=p, state=p):
+        return verify(K, c, rec, state, L.ix_gdn_decode_window_mfma)
 
     def commit(K, c=cfg, acc=p, rec=p):
         return L.ix_gdn_commit_window(ctypes.byref(c), 2, K, acc, p, rec, p, p, NULL)
 
-    for f in (verify, commit):
+    for f in (verify, verify_mfma, commit):
         assert f(0) == INVALID and f(17) == INVALID
         assert f(4, c=bx.make_cfg(h_k=4, h_v=2)) == INVALID            # a q/k head feeds no v head
         assert f(4, rec=ctypes.c_void_p((1 << 20) + 16)) == INVALID     # record not 256-byte aligned
         assert f(4, rec=NULL) == INVALID
     assert verify(4, state=ctypes.c_void_p((1 << 20) + 8)) == INVALID  # state not 16-byte aligned
+    assert verify_mfma(4, state=ctypes.c_void_p((1 << 20) + 8)) == INVALID
     assert commit(4, acc=NULL) == INVALID
 
 

@@ -1,17 +1,21 @@
 """GPU parity of the speculative-window calls (ix_gdn_decode_window, ix_gdn_commit_window).
 
-The window's outputs must be bit-identical to K ix_gdn_decode calls on the same states (the
-kernels share the column math), the verify call must leave both states untouched, and commit
-with n accepted tokens must leave the states bit-identical to n decode calls; against the
-double oracle the decode tolerances hold (fp32 outputs 1e-3 absolute, state max|d|/max|ref|
-<= 1e-4, conv state bit-exact). Accepted counts are clamped to [0, K].
+Two verify paths. The exact one (ix_gdn_decode_window) must give outputs bit-identical to K
+ix_gdn_decode calls on the same states (the kernels share the column math). The matrix-core
+one (ix_gdn_decode_window_mfma) computes the same outputs in the K-token space from S^T k and
+S^T q: within 1e-4 absolute of the decode calls' outputs (fp32 and split-bf16 rounding), and
+its window record must be bit-identical to the exact path's. Either verify must leave both
+states untouched, and commit with n accepted tokens must leave the states bit-identical to n
+decode calls; against the double oracle the decode tolerances hold (fp32 outputs 1e-3
+absolute, state max|d|/max|ref| <= 1e-4, conv state bit-exact). Accepted counts are clamped
+to [0, K].
 """
 import numpy as np
 import pytest
 
 import baloon_amd as bx
 import oracle
-from oracle import inputs
+from oracle import bf16, inputs
 from tests.common import (NT, TOL_O_ABS, TOL_STATE_REL, dev, extreme_gates, extreme_params, host, state_from_dev,
                           state_to_dev)
 
@@ -23,7 +27,11 @@ def _torch():
     return torch
 
 
-def window_case(cfg, B, K, accepted, seed, extreme=False):
+TOL_MFMA_VS_DECODE = 1e-4
+MODES = [pytest.param("exact", id="exact"), pytest.param("mfma", id="mfma")]
+
+
+def window_case(cfg, B, K, accepted, seed, extreme=False, mode="exact"):
     torch = _torch()
     p = inputs.layer_params(cfg, seed)
     st = inputs.initial_states(cfg, seed, B)
@@ -39,13 +47,24 @@ def window_case(cfg, B, K, accepted, seed, extreme=False):
     # verify
     d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
     cs0, st0 = host(d_cs).copy(), host(d_st).copy()
-    rec = torch.empty(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
+    # zeroed: the record's sections are padded to 256 bytes, and the comparison below of the
+    # two verifies' records covers the padding too
+    rec = torch.zeros(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
     o_win = torch.full((B, K, cfg.h_v, cfg.d_v), float("nan"), dtype=torch.float32, device="cuda")
-    assert bx.ix_gdn_decode_window(cfg, B, K, d_x, d_cs, d_w, d_a, d_b, d_A, d_dt, d_st, o_win, None, rec) == 0
+    ob_win = torch.zeros(B, K, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
+    verify = bx.ix_gdn_decode_window if mode == "exact" else bx.ix_gdn_decode_window_mfma
+    assert verify(cfg, B, K, d_x, d_cs, d_w, d_a, d_b, d_A, d_dt, d_st, o_win, ob_win, rec) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(d_st), st0)                    # verify changes no state
     np.testing.assert_array_equal(host(d_cs), cs0)
     o_win = host(o_win)
+    np.testing.assert_array_equal(host(ob_win), bf16.from_f32(o_win))
+    if mode == "mfma":                                                # the same record as the exact verify
+        rec_exact = torch.zeros_like(rec)
+        assert bx.ix_gdn_decode_window(cfg, B, K, d_x, d_cs, d_w, d_a, d_b, d_A, d_dt, d_st, None, None,
+                                       rec_exact) == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(rec), host(rec_exact), err_msg="window record")
 
     # the same tokens through K decode calls, keeping the states after each
     l_cs, l_st = dev(st["conv_state"]), state_to_dev(st["state"])
@@ -56,7 +75,11 @@ def window_case(cfg, B, K, accepted, seed, extreme=False):
         assert bx.ix_gdn_decode(cfg, B, dev(x[:, t]), l_cs, d_w, dev(a[:, t]), dev(b[:, t]), d_A, d_dt, l_st, od,
                                 None, ws) == 0
         torch.cuda.synchronize()
-        np.testing.assert_array_equal(o_win[:, t], host(od), err_msg=f"window output t={t}")
+        if mode == "exact":
+            np.testing.assert_array_equal(o_win[:, t], host(od), err_msg=f"window output t={t}")
+        else:
+            err = float(np.max(np.abs(o_win[:, t] - host(od))))
+            assert err <= TOL_MFMA_VS_DECODE, f"window output t={t}: {err} from the decode call's"
         after.append((host(l_cs).copy(), host(l_st).copy()))
 
     # commit
@@ -90,20 +113,28 @@ def window_case(cfg, B, K, accepted, seed, extreme=False):
     (8, [8, 5, 0, 13, 3, -1]),
     (16, [16, 3, 0, 16, 15, 7]),                      # the largest window
 ])
-def test_window_verify_and_commit(K, accepted):
-    window_case(bx.make_cfg(), 6, K, accepted, inputs.seed_for(2) + 50 + K)
+@pytest.mark.parametrize("mode", MODES)
+def test_window_verify_and_commit(K, accepted, mode):
+    window_case(bx.make_cfg(), 6, K, accepted, inputs.seed_for(2) + 50 + K, mode=mode)
 
 
 @pytest.mark.parametrize("kw", [dict(head_map=1, h_k=4, h_v=12), dict(d_conv=2), dict(d_conv=3, conv_act=1),
                                 dict(h_k=3, h_v=8, q_scale=0.125), dict(h_k=1, h_v=16), dict(h_k=2, h_v=18),
                                 dict(h_k=2, h_v=32, head_map=1)])
-def test_window_variants(kw):
-    window_case(bx.make_cfg(**kw), 3, 3, [3, 1, 2], inputs.seed_for(2) + 60 + len(kw) + kw.get("h_v", 0))
+@pytest.mark.parametrize("mode", MODES)
+def test_window_variants(kw, mode):
+    window_case(bx.make_cfg(**kw), 3, 3, [3, 1, 2], inputs.seed_for(2) + 60 + len(kw) + kw.get("h_v", 0), mode=mode)
 
 
-def test_window_extreme_gates():
+@pytest.mark.parametrize("mode", MODES)
+def test_window_extreme_gates(mode):
     # gate logits past softplus's threshold on both sides, beta logits at +-30, A_log = ln 16
-    window_case(bx.make_cfg(), 6, 8, [8, 5, 0, 3, 7, 1], inputs.seed_for(2) + 90, extreme=True)
+    window_case(bx.make_cfg(), 6, 8, [8, 5, 0, 3, 7, 1], inputs.seed_for(2) + 90, extreme=True, mode=mode)
+
+
+def test_window_mfma_at_bench_shape():
+    # configuration 2's batch, K = 4, all accepted: the shape the benchmark times
+    window_case(bx.make_cfg(), 64, 4, [4] * 64, inputs.seed_for(2) + 95, mode="mfma")
 
 
 def test_window_then_decode_continues():
