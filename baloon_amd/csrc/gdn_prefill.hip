@@ -21,13 +21,15 @@
 // Kernels, in stream order:
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
 //                  the chunk table (sequence and first token of each chunk)
-//   chunk_kernel   per (chunk, q/k head): conv (history from conv_state at sequence starts),
-//                  L2 norms of q and k; K K^T and Q K^T (lower block triangle) once for all
-//                  the v heads mapped to the q/k head; then per v head its decay factors and
-//                  beta, its v rows, A and M, T = (I + A)^-1 by a blocked inverse (fp32
-//                  MFMA block products), W = T diag(beta Gam) K and U = T diag(beta) V; the
-//                  chain's operands W (negated, so the chain's D accumulates from U), M,
-//                  K^T and Q written as split-bf16 MFMA fragments, U^T in fp32
+//   qk_kernel      per (chunk, q/k head): conv (history from conv_state at sequence starts)
+//                  and L2 norms of q and k; K K^T and Q K^T (lower block triangle) once for
+//                  all the v heads mapped to the q/k head, stored raw; K^T and Q written as
+//                  split-bf16 MFMA fragments
+//   v_kernel       per (chunk, v head): decay factors and beta, v rows, A and M from the raw
+//                  products, T = (I + A)^-1 by a blocked inverse (fp32 MFMA block products),
+//                  U = T diag(beta) V and W = T diag(beta Gam) K; the chain's operands W
+//                  (negated, so the chain's D accumulates from U) and M as split-bf16
+//                  fragments, U^T in fp32
 //   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
 //                  One wave carries the strip in MFMA accumulators with no barrier on its
 //                  data path; four waves compute the outputs from the S and D it hands over;
@@ -63,8 +65,9 @@ struct Ws {
                          // inclusive cumulative log decay G (padded rows repeat the last)
     uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
+    v4* raw;             // [NC][h_k][4][3][2][64] raw K K^T, Q K^T triangle blocks (accumulator layout)
 };
-constexpr int kWsSections = 9;
+constexpr int kWsSections = 10;
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -76,6 +79,7 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
         sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * 2 * kChunk,
         sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
+        sizeof(v4) * NC * c->h_k * 4 * 3 * 2 * kWave,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -93,6 +97,7 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.G = reinterpret_cast<float*>(base + off[6]);
     w.Ktf = reinterpret_cast<uint16_t*>(base + off[7]);
     w.Qf = reinterpret_cast<uint16_t*>(base + off[8]);
+    w.raw = reinterpret_cast<v4*>(base + off[9]);
     return w;
 }
 
@@ -354,7 +359,6 @@ constexpr size_t kFragKt = 8 * 2 * 2 * 512;    // 128 x 64 (K^T)
 constexpr int kKS = kD + 4;          // padded LDS row stride of the K / Q / V tiles
 constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
 constexpr int kChunkThreads = 512;
-constexpr int kMaxMap = 16;          // v heads per q/k head (the configuration limit)
 
 // Normalised k and q rows in LDS as split-bf16 planes (hi, then lo; hi + lo is the fp32 value
 // to ~2^-17): [64 tokens][128 channels] bf16, 256-byte rows whose 16-byte chunks are
@@ -416,94 +420,53 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
     }
 }
 
-// Phases (one workgroup, 8 waves; every barrier orders LDS only, so no wave ever waits for
-// its own global stores):
-//   gate inputs of the v heads | q and k rows of the chunk: conv, L2 norm, q scale, into LDS
-//   (zero past the chunk end) | decay scan and beta of each v head | raw K K^T and Q K^T of
-//   the lower block triangle on split-bf16 MFMA, kept in registers, while the other waves
-//   write K^T and Q as split fragments | then, per mapped v head: M as fragments |
-//   T = (I + A)^-1: the four 16 x 16 diagonal blocks by substitution (one wave, while four
-//   others compute the next head's v rows), then the off-diagonal blocks
-//   T_ij = -T_ii sum_k A_ik T_kj in three dependency levels of fp32 MFMA block products |
-//   U = T diag(beta) V and W = T diag(beta Gam) K as split-bf16 MFMA GEMMs (the zero blocks
-//   of T skipped) | U^T stored from the MFMA layout, W through LDS into fragments | A and M
-//   of the next head.
-// The v rows of even and odd heads alternate between two tiles (the odd one is the q tile,
-// free once the triangle and the Q fragments are done).
+// The chunk-local work runs as two kernels, so that each holds a fraction of the registers and
+// LDS of a single one and two workgroups share a CU (one hides the other's load latency and
+// barriers):
+//   qk_kernel (chunk, q/k head): q and k rows (conv, L2 norm, q scale) as split-bf16 planes in
+//     LDS; the lower block triangle of K K^T and Q K^T on split-bf16 MFMA, stored raw in the
+//     accumulator layout for the v kernel; K^T and Q as the chain's fragments.
+//   v_kernel (chunk, v head): decay scan and beta; v rows (conv); A and M from the raw
+//     products; M fragments; T = (I + A)^-1 by a blocked inverse; U = T diag(beta) V and
+//     W = T diag(beta Gam) K on split-bf16 MFMA (K from the K^T fragments); U^T and -W
+//     fragments for the chain.
+// Every barrier orders LDS only, so no wave waits for its own global stores.
+
+// Raw triangle products: per (chunk, q/k head), wave w (0..3) of the triangle and its block
+// slot j (0..2, block i = w + 4 j), the K K^T then the Q K^T accumulator, one 16-byte v4 per
+// lane: [NC][h_k][4][3][2][64] v4.
+__device__ __forceinline__ size_t raw_at(size_t cs, int w, int j, int kind, int lane) {
+    return ((((cs * 4 + w) * 3 + j) * 2 + kind) * kWave + lane);
+}
+
 template <int DC>
-__global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[3 * kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
-    float (*K_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);         // k rows
-    float (*Q_s)[kKS] = K_s + kChunk;                                  // q rows, then v rows of odd heads
-    float (*V_s)[kKS] = Q_s + kChunk;                                  // v rows of even heads
-    float* A_s = lds + 3 * kChunk * kKS;                               // [64][kTS]
-    float* M_s = A_s + kChunk * kTS;                                   // M, then T
-    float* T_s = M_s;
-    float (*W_s)[kKS] = reinterpret_cast<float (*)[kKS]>(A_s);        // W, over A and T
-    float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
-    static_assert(kChunk * kKS <= 2 * kChunk * kTS, "W fits over A and T");
-    static_assert(2 * kQKPlane <= kChunk * kKS * 4, "k and q planes fit their tiles");
-    uint8_t* Kp = reinterpret_cast<uint8_t*>(K_s);                     // k rows as split planes
-    uint8_t* Qp = reinterpret_cast<uint8_t*>(Q_s);                     // q rows as split planes
-    __shared__ float G_s[kMaxMap][kChunk], B_s[kMaxMap][kChunk], BG_s[kMaxMap][kChunk];
+__global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p) {
+    __shared__ __align__(16) uint8_t planes[4 * kQKPlane];     // k hi, k lo, q hi, q lo
+    uint8_t* Kp = planes;
+    uint8_t* Qp = planes + 2 * kQKPlane;
 
     ChunkGeo g;
     const int c = blockIdx.x;
     if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
-    const int src = blockIdx.y, nmap = mapped_count(L, src);
-    if (nmap == 0) return;
-    const int lo = g.lo;
+    const int src = blockIdx.y;
+    if (mapped_count(L, src) == 0) return;                     // no v head reads this q/k head
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);        // wave-uniform: scalar branches
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
     const size_t cs = (size_t)c * L.h_k + src;
-    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);   // this wave's conv rows
+    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);   // this wave's rows
 
-    // Gate inputs of v heads w and w + 8 (lane = token), issued first.
-    uint16_t ra[2] = {0, 0}, rb[2] = {0, 0};
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int hh = w + 8 * j;
-        if (hh < nmap && lane < g.len) {
-            const size_t ab = (size_t)(g.t0 + lane) * L.h_v + mapped_head(L, src, hh);
-            ra[j] = p.a[ab];
-            rb[j] = p.b[ab];
-        }
-    }
-
-    // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave: the loads are issued
-    // first, the decay scan (which needs only the gate inputs) runs while they are in flight.
+    // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave: lane l carries channels
+    // 2l, 2l+1, so every x access of a wave is a 256-byte row segment and each row's norm is
+    // one wave sum. Rows past the chunk end are zero.
     const bool isk = w >= 4;
-    ConvIn<DC> in;
-    conv_load<DC>(p, g, lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
-    // Decay scan and beta of v heads w and w + 8.
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int hh = w + 8 * j;
-        if (hh >= nmap) continue;
-        const int h = mapped_head(L, src, hh);
-        const bool ok = lane < g.len;
-        float lgt = ok ? log_gate(L, h, bf16_to_f32(ra[j])) : 0.0f;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {          // inclusive scan over the 64 lanes
-            const float o = __shfl_up(lgt, off, kWave);
-            if (lane >= off) lgt += o;
-        }
-        const float bt = ok ? sigmoid_f(bf16_to_f32(rb[j])) : 0.0f;
-        G_s[hh][lane] = lgt;
-        B_s[hh][lane] = bt;
-        BG_s[hh][lane] = bt * expf(lgt);
-        const float glast = __shfl(lgt, kChunk - 1, kWave);
-        float* E = p.ws.G + ((size_t)c * L.h_v + h) * 2 * kChunk;
-        E[lane] = expf(glast - lgt);
-        E[kChunk + lane] = expf(lgt);
-    }
     {
+        ConvIn<DC> in;
+        conv_load<DC>(p, g, g.lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
         float y0[kConvTok], y1[kConvTok];
         conv_run<DC>(L, in, y0, y1);
-        // All 16 row sums first (independent, so their shuffle latencies overlap), then the
-        // scaled rows; rows past the chunk end are zero.
+        // All 16 row sums first (independent, so their shuffle latencies overlap).
         float ss[kConvTok];
 #pragma unroll
         for (int t = 0; t < kConvTok; ++t) ss[t] = wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t]));
@@ -521,44 +484,40 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
     }
     lds_barrier();
 
-    // Raw K K^T and Q K^T (waves 0-3) on split-bf16 MFMA (16x16x32, three bf16 products per
-    // fp32 product), operands straight from the planes: lane (li, lg4) supplies channels
-    // 32 ks + 8 lg4 .. +7 of token row li for both operands. Waves 4-7 first issue the
-    // loads of the first v head's rows, then copy K^T (rows i, k = token t: 8 x 2 fragments)
-    // and Q (rows t, k = i: 4 x 4 fragments) from the planes into split fragments.
-    v4 kk[3], qk[3];
-    ConvIn<DC> vin;
     if (w < 4) {
+        // Raw K K^T and Q K^T of this wave's triangle blocks (16x16x32 split-bf16 MFMA,
+        // operands straight from the planes: lane (li, lg4) supplies channels
+        // 32 ks + 8 lg4 .. +7 of token row li for both operands), then stored.
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int i = w + 4 * j;
-            kk[j] = v4{0.f, 0.f, 0.f, 0.f};
-            qk[j] = kk[j];
-            if (i < 10) {
-                int br, bc;
-                tri_block(i, br, bc);
-                const int arow = 16 * br + li, brow = 16 * bc + li;
+            if (i >= 10) continue;
+            v4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
+            int br, bc;
+            tri_block(i, br, bc);
+            const int arow = 16 * br + li, brow = 16 * bc + li;
 #pragma unroll
-                for (int ks = 0; ks < kD / 32; ++ks) {
-                    const int ch = 32 * ks + 8 * lg4, oa = qk_off(arow, ch), ob = qk_off(brow, ch);
-                    const bf8 akh = *reinterpret_cast<const bf8*>(Kp + oa);
-                    const bf8 akl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + oa);
-                    const bf8 aqh = *reinterpret_cast<const bf8*>(Qp + oa);
-                    const bf8 aql = *reinterpret_cast<const bf8*>(Qp + kQKPlane + oa);
-                    const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
-                    const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
-                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akh, bkh, kk[j], 0, 0, 0);
-                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aqh, bkh, qk[j], 0, 0, 0);
-                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akh, bkl, kk[j], 0, 0, 0);
-                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aqh, bkl, qk[j], 0, 0, 0);
-                    kk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(akl, bkh, kk[j], 0, 0, 0);
-                    qk[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aql, bkh, qk[j], 0, 0, 0);
-                }
+            for (int ks = 0; ks < kD / 32; ++ks) {
+                const int ch = 32 * ks + 8 * lg4, oa = qk_off(arow, ch), ob = qk_off(brow, ch);
+                const bf8 akh = *reinterpret_cast<const bf8*>(Kp + oa);
+                const bf8 akl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + oa);
+                const bf8 aqh = *reinterpret_cast<const bf8*>(Qp + oa);
+                const bf8 aql = *reinterpret_cast<const bf8*>(Qp + kQKPlane + oa);
+                const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
+                const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
+                kk = mfma_bf16(akh, bkh, kk);
+                qk = mfma_bf16(aqh, bkh, qk);
+                kk = mfma_bf16(akh, bkl, kk);
+                qk = mfma_bf16(aqh, bkl, qk);
+                kk = mfma_bf16(akl, bkh, kk);
+                qk = mfma_bf16(aql, bkh, qk);
             }
-            __builtin_amdgcn_sched_barrier(0);       // one block's operands live at a time
+            p.ws.raw[raw_at(cs, w, j, 0, lane)] = kk;
+            p.ws.raw[raw_at(cs, w, j, 1, lane)] = qk;
         }
     } else {
-        if (nt > 0) conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, 0), c2), tb, nt, vin);
+        // K^T (rows i, k = token t: 8 x 2 fragments) and Q (rows t, k = i: 4 x 4 fragments)
+        // from the planes into split fragments, k in accumulator row order (kperm).
         const int t4 = tid - 4 * kWave;
         uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
         for (int u = t4; u < 8 * 2 * kWave; u += 4 * kWave) {
@@ -585,167 +544,230 @@ __global__ void __launch_bounds__(kChunkThreads) chunk_kernel(const PrefillParam
             *reinterpret_cast<u4x*>(Qf + frag_at(m, ks, 4, 1, ln)) = u4x{al.x, al.y, bl.x, bl.y};
         }
     }
-    lds_barrier();
+}
 
-    // v rows of the first head (waves 4-7); A and M of the first head (waves 0-3).
-    if (w >= 4) {
+// v_kernel: grid (NC, h_v), 512 threads; workgroup = (chunk, v head). Phases: decay scan and
+// beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
+// compute the v rows | A and M (waves 0-3) | M fragments | the four 16 x 16 diagonal blocks
+// of T by substitution (wave 0), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj
+// in three dependency levels of fp32 MFMA block products | U = (T diag beta) V and
+// W = (T diag beta Gam) K, wave w taking columns 16 w .. +15 | U^T stored from the MFMA
+// layout, -W through LDS into fragments.
+template <int DC>
+__global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p) {
+    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
+    float (*V_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);        // v rows
+    float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
+    float* M_s = A_s + kChunk * kTS;                                   // M, then T
+    float* T_s = M_s;
+    float (*W_s)[kKS] = reinterpret_cast<float (*)[kKS]>(A_s);        // W, over A and T
+    float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
+    static_assert(kChunk * kKS <= 2 * kChunk * kTS, "W fits over A and T");
+    __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
+
+    ChunkGeo g;
+    const int c = blockIdx.x;
+    if (!chunk_geo(p, c, g)) return;
+    const Layer& L = p.L;
+    const int h = blockIdx.y, src = src_of(L, h);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
+    const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
+    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);
+
+    // K^T fragments of this wave's 16 columns (the B operand of W), issued first.
+    bf8 kt[2][2];
+    {
+        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) kt[ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(w, ks, 2, pl, lane));
+    }
+    v4 kk[3], qk[3];
+    if (w < 4) {
+        uint16_t ra = 0, rb = 0;
+        if (w == 0 && lane < g.len) {
+            const size_t ab = (size_t)(g.t0 + lane) * L.h_v + h;
+            ra = p.a[ab];
+            rb = p.b[ab];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            kk[j] = v4{0.f, 0.f, 0.f, 0.f};
+            qk[j] = kk[j];
+            if (w + 4 * j < 10) {
+                kk[j] = p.ws.raw[raw_at(cs, w, j, 0, lane)];
+                qk[j] = p.ws.raw[raw_at(cs, w, j, 1, lane)];
+            }
+        }
+        if (w == 0) {
+            // Inclusive scan of the log decay over the chunk's tokens, beta, and the decay
+            // factors the chain reads: exp(G_last - G_t), then exp(G_t).
+            const bool ok = lane < g.len;
+            float lgt = ok ? log_gate(L, h, bf16_to_f32(ra)) : 0.0f;
+#pragma unroll
+            for (int off = 1; off < kWave; off <<= 1) {
+                const float o = __shfl_up(lgt, off, kWave);
+                if (lane >= off) lgt += o;
+            }
+            const float bt = ok ? sigmoid_f(bf16_to_f32(rb)) : 0.0f;
+            G_s[lane] = lgt;
+            B_s[lane] = bt;
+            BG_s[lane] = bt * expf(lgt);
+            const float glast = __shfl(lgt, kChunk - 1, kWave);
+            float* E = p.ws.G + ch * 2 * kChunk;
+            E[lane] = expf(glast - lgt);
+            E[kChunk + lane] = expf(lgt);
+        }
+    } else {
+        // v rows of the head, 16 tokens per wave, zero past the chunk end.
+        ConvIn<DC> vin;
+        conv_load<DC>(p, g, g.lo, v_channel(L, h, c2), tb, nt, vin);
         float y0[kConvTok], y1[kConvTok];
-        if (nt > 0) conv_run<DC>(L, vin, y0, y1);
+        conv_run<DC>(L, vin, y0, y1);
 #pragma unroll
         for (int t = 0; t < kConvTok; ++t)
             *reinterpret_cast<float2*>(&V_s[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
-    } else {
-        am_head(kk, qk, G_s[0], B_s[0], A_s, M_s, w, li, lg4);
     }
     lds_barrier();
+    if (w < 4) am_head(kk, qk, G_s, B_s, A_s, M_s, w, li, lg4);
+    lds_barrier();
 
-    for (int mi = 0; mi < nmap; ++mi) {
-        const int h = mapped_head(L, src, mi);
-        const size_t ch = (size_t)c * L.h_v + h;
-        float (*Vb)[kKS] = (mi & 1) ? Q_s : V_s;                        // this head's v rows
-        float (*Vn)[kKS] = (mi & 1) ? V_s : Q_s;                        // the next head's
-        const bool next = mi + 1 < nmap, conv_next = w >= 4 && next && nt > 0;
-
-        // M as fragments (4 x 2 fragments x 64 lanes: one unit per thread); the blocks
-        // above the diagonal are zero.
-        {
-            uint16_t* Mf = p.ws.Mf + ch * kFragM;
-            const int m = w >> 1, ks = w & 1;
-            const int row = 16 * m + li, k0 = 32 * ks + 4 * lg4;            // kperm halves
-            float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // M as fragments (4 x 2 fragments x 64 lanes: one unit per thread); the blocks above
+    // the diagonal are zero.
+    {
+        uint16_t* Mf = p.ws.Mf + ch * kFragM;
+        const int m = w >> 1, ks = w & 1;
+        const int row = 16 * m + li, k0 = 32 * ks + 4 * lg4;            // kperm halves
+        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int hb = 0; hb < 2; ++hb) {                              // 16-column block 2 ks + hb
-                if (2 * ks + hb > m) continue;
+        for (int hb = 0; hb < 2; ++hb) {                              // 16-column block 2 ks + hb
+            if (2 * ks + hb > m) continue;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) x[4 * hb + e] = M_s[row * kTS + k0 + 16 * hb + e];
-            }
-            store_frag(Mf, m, ks, 2, lane, x);
+            for (int e = 0; e < 4; ++e) x[4 * hb + e] = M_s[row * kTS + k0 + 16 * hb + e];
         }
-        lds_barrier();                     // M_s is read: T takes its place
+        store_frag(Mf, m, ks, 2, lane, x);
+    }
+    lds_barrier();                         // M_s is read: T takes its place
 
-        // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane =
-        // 16 b + column c); waves 4-7 load and compute the next head's v rows.
-        if (w == 0) {
-            const int b = lane >> 4, cc = lane & 15;
-            const float* Ab = A_s + (16 * b) * kTS + 16 * b;
-            float x[16];
+    // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane = 16 b +
+    // column c).
+    if (w == 0) {
+        const int b = lane >> 4, cc = lane & 15;
+        const float* Ab = A_s + (16 * b) * kTS + 16 * b;
+        float x[16];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float acc = r == cc ? 1.0f : 0.0f;
+        for (int r = 0; r < 16; ++r) {
+            float acc = r == cc ? 1.0f : 0.0f;
 #pragma unroll
-                for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
-                x[r] = acc;
-                if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // loads hoisted 4 rows ahead at most
-            }
+            for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
+            x[r] = acc;
+            if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // loads hoisted 4 rows ahead at most
+        }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
-        } else if (w >= 4 && next) {
-            // The next head's conv inputs are loaded here, where wave 0's substitution
-            // covers their latency (loading them earlier holds ~26 registers longer).
-            float y0[kConvTok], y1[kConvTok];
-            if (conv_next) {
-                ConvIn<DC> nin;
-                conv_load<DC>(p, g, lo, v_channel(L, mapped_head(L, src, mi + 1), c2), tb, nt, nin);
-                conv_run<DC>(L, nin, y0, y1);
-            }
+        for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
+    }
+    lds_barrier();
+    // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
+    // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
 #pragma unroll
-            for (int t = 0; t < kConvTok; ++t)
-                *reinterpret_cast<float2*>(&Vn[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
+    for (int lev = 1; lev <= 3; ++lev) {
+        if (w < 4 - lev) {
+            const int j = w, i = w + lev;
+            v4 pc = {0.f, 0.f, 0.f, 0.f};
+            for (int k = j; k < i; ++k)
+                pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
+            float* Pw = P_s + w * 16 * 17;
+            put16(Pw, 17, pc, lane, 1.0f);
+            __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's P stores done
+            const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
+            put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
         }
         lds_barrier();
-        // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
-        // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
-#pragma unroll
-        for (int lev = 1; lev <= 3; ++lev) {
-            if (w < 4 - lev) {
-                const int j = w, i = w + lev;
-                v4 pc = {0.f, 0.f, 0.f, 0.f};
-                for (int k = j; k < i; ++k)
-                    pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
-                float* Pw = P_s + w * 16 * 17;
-                put16(Pw, 17, pc, lane, 1.0f);
-                __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's P stores done
-                const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
-                put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
-            }
-            lds_barrier();
-        }
+    }
 
-        // U = T (beta V), then W = T (beta Gam K), on split-bf16 MFMA (16x16x32, three bf16
-        // products per fp32 product; one accumulator set live at a time): wave w takes
-        // columns 16 w .. 16 w + 15, all four 16-row tiles. T[t][s] = 0 for s > t, so tile
-        // mt needs the 32-token k-steps up to mt / 2, and the blocks of T above the block
-        // diagonal (never written) are read as zeros. Lane (li, lg4) supplies k = 32 ks +
-        // 8 lg4 .. +7 of row / column li.
-        const int col = 16 * w + li;
-        auto t_gemm = [&](bool is_w, v4 (&acc)[4]) {
+    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32, one
+    // accumulator set live at a time): wave w takes columns 16 w .. +15, all four 16-row
+    // tiles. The k index (token s) runs in kperm order, the order of the K^T fragments that
+    // are W's B operand: lane (li, lg4) of k-step ks holds tokens 32 ks + 4 lg4 .. +3 (the
+    // 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block 2 ks + 1). T[t][s] = 0 for
+    // s > t: tile mt needs the k-steps up to mt / 2, and the blocks of T above the block
+    // diagonal (never written) are read as zeros.
+    const int col = 16 * w + li;
+    auto t_gemm = [&](bool is_w, v4 (&acc)[4]) {
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) acc[mt] = v4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < 4; ++mt) acc[mt] = v4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+        for (int ks = 0; ks < 2; ++ks) {
+            const int s0 = 32 * ks + 4 * lg4;
+            const v4 sc0 = *reinterpret_cast<const v4*>((is_w ? BG_s : B_s) + s0);
+            const v4 sc1 = *reinterpret_cast<const v4*>((is_w ? BG_s : B_s) + s0 + 16);
+            bf8 bh, bl;
+            if (is_w) {
+                bh = kt[ks][0];
+                bl = kt[ks][1];
+            } else {
                 float bv[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const int sr = 32 * ks + 8 * lg4 + e;
-                    bv[e] = is_w ? qk_f32(Kp, sr, col) * BG_s[mi][sr] : B_s[mi][sr] * Vb[sr][col];
+                for (int e = 0; e < 4; ++e) {
+                    bv[e] = V_s[s0 + e][col];
+                    bv[e + 4] = V_s[s0 + 16 + e][col];
                 }
-                bf8 bh, bl;
                 split8(bv, bh, bl);
-#pragma unroll
-                for (int mt = 2 * ks; mt < 4; ++mt) {
-                    const bool live = 2 * ks + (lg4 >> 1) <= mt;    // this lane's 16-token block of T
-                    const float* tr = T_s + (16 * mt + li) * kTS + 32 * ks + 8 * lg4;
-                    const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 4);
-                    float av[8];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) { av[e] = live ? t0[e] : 0.0f; av[e + 4] = live ? t1[e] : 0.0f; }
-                    bf8 ah, al;
-                    split8(av, ah, al);
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc[mt], 0, 0, 0);
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc[mt], 0, 0, 0);
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc[mt], 0, 0, 0);
-                }
             }
-        };
-        {
-            v4 uacc[4];
-            t_gemm(false, uacc);
-            // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
-            float* Ut = p.ws.Ut + ch * kD * kChunk;
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+            for (int mt = 2 * ks; mt < 4; ++mt) {
+                const float* tr = T_s + (16 * mt + li) * kTS + s0;
+                const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16);
+                const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
+                float av[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    av[e] = live0 ? t0[e] * sc0[e] : 0.0f;
+                    av[e + 4] = live1 ? t1[e] * sc1[e] : 0.0f;
+                }
+                bf8 ah, al;
+                split8(av, ah, al);
+                acc[mt] = mfma_bf16(ah, bh, acc[mt]);
+                acc[mt] = mfma_bf16(ah, bl, acc[mt]);
+                acc[mt] = mfma_bf16(al, bh, acc[mt]);
+            }
         }
-        v4 wacc[4];
-        t_gemm(true, wacc);
-        lds_barrier();                     // A and T are read: W takes their place
+    };
+    {
+        v4 uacc[4];
+        t_gemm(false, uacc);
+        // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
+        float* Ut = p.ws.Ut + ch * kD * kChunk;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
+            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+    }
+    v4 wacc[4];
+    t_gemm(true, wacc);
+    lds_barrier();                         // A and T are read: W takes their place
 #pragma unroll
-            for (int r = 0; r < 4; ++r) W_s[16 * mt + 4 * lg4 + r][col] = wacc[mt][r];
-        lds_barrier();
-        // -W as fragments (4 x 4 x 64 = 1024 units, two per thread): negated, so the chain's
-        // D = U - W S accumulates from U.
-        uint16_t* Wf = p.ws.Wf + ch * kFragW;
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int rep = 0; rep < 2; ++rep) {
-            const int u = tid + rep * kChunkThreads;
-            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
-            float x[8];
-            const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 16]);
+        for (int r = 0; r < 4; ++r) W_s[16 * mt + 4 * lg4 + r][col] = wacc[mt][r];
+    lds_barrier();
+    // -W as fragments (4 x 4 x 64 = 1024 units, two per thread): negated, so the chain's
+    // D = U - W S accumulates from U.
+    uint16_t* Wf = p.ws.Wf + ch * kFragW;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { x[e] = -a[e]; x[e + 4] = -b[e]; }
-            store_frag(Wf, m, ks, 4, ln, x);
-        }
-        if (next) {
-            lds_barrier();                 // W is read: the next head's A and M take its place
-            if (w < 4) am_head(kk, qk, G_s[mi + 1], B_s[mi + 1], A_s, M_s, w, li, lg4);
-            lds_barrier();
-        }
+    for (int rep = 0; rep < 2; ++rep) {
+        const int u = tid + rep * kChunkThreads;
+        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
+        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
+        float x[8];
+        const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 16]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { x[e] = -a[e]; x[e + 4] = -b[e]; }
+        store_frag(Wf, m, ks, 4, ln, x);
     }
 }
-
 // ---------------------------------------------------------------------------------------
 // chain: one workgroup per (sequence, v head, 16-column state strip), 7 waves
 // ---------------------------------------------------------------------------------------
@@ -1266,11 +1288,20 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const dim3 kgrid((unsigned)NC, (unsigned)cfg->h_k);
+    const dim3 qgrid((unsigned)NC, (unsigned)cfg->h_k), vgrid((unsigned)NC, (unsigned)cfg->h_v);
     switch (cfg->d_conv) {
-        case 2: hipLaunchKernelGGL(chunk_kernel<2>, kgrid, dim3(kChunkThreads), 0, s, p); break;
-        case 3: hipLaunchKernelGGL(chunk_kernel<3>, kgrid, dim3(kChunkThreads), 0, s, p); break;
-        default: hipLaunchKernelGGL(chunk_kernel<4>, kgrid, dim3(kChunkThreads), 0, s, p); break;
+        case 2:
+            hipLaunchKernelGGL(qk_kernel<2>, qgrid, dim3(kChunkThreads), 0, s, p);
+            hipLaunchKernelGGL(v_kernel<2>, vgrid, dim3(kChunkThreads), 0, s, p);
+            break;
+        case 3:
+            hipLaunchKernelGGL(qk_kernel<3>, qgrid, dim3(kChunkThreads), 0, s, p);
+            hipLaunchKernelGGL(v_kernel<3>, vgrid, dim3(kChunkThreads), 0, s, p);
+            break;
+        default:
+            hipLaunchKernelGGL(qk_kernel<4>, qgrid, dim3(kChunkThreads), 0, s, p);
+            hipLaunchKernelGGL(v_kernel<4>, vgrid, dim3(kChunkThreads), 0, s, p);
+            break;
     }
     const long long groups = (pairs + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
