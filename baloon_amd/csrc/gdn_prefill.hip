@@ -432,6 +432,35 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
 //     fragments for the chain.
 // Every barrier orders LDS only, so no wave waits for its own global stores.
 
+// The v kernel's unit (chunk, v head) of 1-D workgroup id. Workgroups are dispatched to the
+// 8 XCDs round robin (id % 8), so ids are first made XCD-major (XCD x runs units
+// x * N/8 .. (x+1) * N/8 - 1, in order), and the units walk the v heads of one q/k head one
+// after the other within a chunk: the heads that share a q/k head read the same K^T fragments
+// and raw triangle blocks, and run back to back on one XCD, where the second reads hit L2.
+__device__ __forceinline__ void v_unit(const Layer& L, int NC, int id, int& c, int& h) {
+    const long long N = (long long)NC * L.h_v, per = N / 8;
+    const long long u = id < per * 8 ? (long long)(id % 8) * per + id / 8 : id;
+    c = (int)(u / L.h_v);
+    const int k = (int)(u % L.h_v);
+    if (L.head_map != IX_GDN_HEAD_MOD) {
+        h = k;                                   // h / per_src: a q/k head's v heads are adjacent
+        return;
+    }
+    // h mod h_k: q/k head s has v heads s, s + h_k, ...; the first h_v mod h_k heads have
+    // one more than the others.
+    const int lo = L.h_v / L.h_k, r = L.h_v % L.h_k, hi = lo + (r ? 1 : 0);
+    int s, m;
+    if (k < r * hi) {
+        s = k / hi;
+        m = k % hi;
+    } else {
+        const int k2 = k - r * hi;
+        s = r + k2 / lo;
+        m = k2 % lo;
+    }
+    h = s + m * L.h_k;
+}
+
 // Raw triangle products: per (chunk, q/k head), wave w (0..3) of the triangle and its block
 // slot j (0..2, block i = w + 4 j), the K K^T then the Q K^T accumulator, one 16-byte v4 per
 // lane: [NC][h_k][4][3][2][64] v4.
@@ -566,10 +595,11 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
 
     ChunkGeo g;
-    const int c = blockIdx.x;
-    if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
-    const int h = blockIdx.y, src = src_of(L, h);
+    int c, h;
+    v_unit(L, p.NC, blockIdx.x, c, h);
+    if (!chunk_geo(p, c, g)) return;
+    const int src = src_of(L, h);
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
@@ -1275,7 +1305,7 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
         return hipErrorInvalidValue;
     const long long NC = (total_T + kChunk - 1) / kChunk + (long long)n_seq;
     const long long pairs = (long long)n_seq * cfg->h_v;
-    if (NC > 0x7fffffffLL || ((pairs + 7) / 8) * 8 * kStrips > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (NC * cfg->h_v > 0x7fffffffLL || ((pairs + 7) / 8) * 8 * kStrips > 0x7fffffffLL) return hipErrorInvalidValue;
     const long long rows = (long long)total_T * cfg->h_v;
     if (gate && (rows + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidValue;
 
@@ -1288,7 +1318,7 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const dim3 qgrid((unsigned)NC, (unsigned)cfg->h_k), vgrid((unsigned)NC, (unsigned)cfg->h_v);
+    const dim3 qgrid((unsigned)NC, (unsigned)cfg->h_k), vgrid((unsigned)(NC * cfg->h_v));
     switch (cfg->d_conv) {
         case 2:
             hipLaunchKernelGGL(qk_kernel<2>, qgrid, dim3(kChunkThreads), 0, s, p);
