@@ -16,7 +16,7 @@
 // load/store instruction moves 1 KiB of contiguous state, and the column sums are
 // in-wave reductions over 32 lanes (DPP within rows, v_permlane16_swap across them).
 //
-// Two kernels, chosen by the launcher:
+// Kernels, chosen by the launcher:
 //  * slab_kernel (a workspace of per-group counters is given): one workgroup per
 //    (sequence, v head, 64-column half tile), 4096 workgroups at B=64 for a short,
 //    well-balanced stream. Every workgroup evaluates the q/k conv of its q/k head
@@ -24,13 +24,14 @@
 //    of the (sequence, q/k head) group to finish reading it, found with one atomic counter
 //    per group. The counter is reset by that workgroup, so the workspace is all zeros
 //    again when the kernel ends. No workgroup ever waits for another.
+//  * head_kernel (the gated decode, ix_gdn_decode_gated, with the counters): the same with
+//    one 512-thread workgroup per (sequence, v head), so the head's 128 outputs meet in LDS
+//    and the gated RMS output norm (the semantics of ix_gdn_out_norm, src/ix_gdn.cu:87-100)
+//    is applied by one wave after one barrier.
 //  * group_kernel (no workspace): one workgroup per (sequence, q/k head) that owns every
-//    channel and tile of the group; race free by ownership.
-// Both have a gated variant (ix_gdn_decode_gated) that ends with the gated RMS output norm
-// of each head (the semantics of ix_gdn_out_norm, src/ix_gdn.cu:87-100). The group kernel
-// holds whole heads; in the slab kernel the two half-tile workgroups of a head publish their
-// 64 outputs and partial sum of squares to the workspace before their state stores, and
-// the second to count in on the head's counter finishes the head (again without waiting).
+//    channel and tile of the group; race free by ownership. It has the gated variant too.
+// The gated norm's sum of squares is the same two wave sums (columns 0..63, 64..127) in the
+// head and group kernels, so they give the same bits.
 // State loads use nontemporal hints and are issued right after the conv inputs so that
 // HBM latency overlaps the conv; the state is streamed once per token.
 #include "gdn_common.h"
@@ -57,23 +58,13 @@ struct DecodeParams {
     OutGate og;                 // gated variant only
 };
 
-// Workspace sections (each 256-byte aligned): group counters [B][h_k], head counters
-// [B][h_v], exchanged half-head outputs [B][h_v][2][64] and their sums of squares
-// [B][h_v][2]. The counters are zero between calls; the rest is scratch.
+// Workspace: the group counters [B][h_k] (one per sequence and q/k head), zero between
+// calls: each call's last group member resets its counter.
 struct DecodeWs {
     int* group;
-    int* head;
-    float* xo;
-    float* xs;
 };
 
-inline size_t decode_ws_layout(int B, int h_k, int h_v, size_t (&off)[4]) {
-    const size_t sz[4] = {(size_t)B * h_k * 4, (size_t)B * h_v * 4, (size_t)B * h_v * 2 * kHalfCols * 4,
-                          (size_t)B * h_v * 2 * 4};
-    size_t at = 0;
-    for (int i = 0; i < 4; ++i) { off[i] = at; at += (sz[i] + 255) & ~(size_t)255; }
-    return at;
-}
+inline size_t decode_ws_bytes(int B, int h_k) { return ((size_t)B * h_k * 4 + 255) & ~(size_t)255; }
 
 template <int DC>
 __device__ __forceinline__ void conv_pair_load(const DecodeParams& p, int bseq, int ch, ConvPair<DC>& c) {
@@ -124,78 +115,14 @@ __device__ __forceinline__ float column_update(const DecodeParams& p, v4f s, v4f
     return ov;
 }
 
-// The same column math split in two: the sums and the output first, the state store later.
-__device__ __forceinline__ float column_reduce(const DecodeParams& p, const v4f& s, const v4f& kr, const v4f& qr,
-                                               float vj, float g, float bt, float kq, size_t o_index, bool writer,
-                                               float& d) {
-    float ak = s[0] * kr[0], aq = s[0] * qr[0];
-#pragma unroll
-    for (int e = 1; e < 4; ++e) { ak = fmaf(s[e], kr[e], ak); aq = fmaf(s[e], qr[e], aq); }
-    ak = half_sum(ak);
-    aq = half_sum(aq);
-    d = (vj - g * ak) * bt;
-    const float ov = fmaf(d, kq, g * aq);
-    if (writer) {
-        if (p.o) p.o[o_index] = ov;
-        if (p.o_bf16) p.o_bf16[o_index] = f32_to_bf16(ov);
-    }
-    return ov;
-}
-__device__ __forceinline__ void column_store(const v4f& s, v4f* dst, const v4f& kr, float d, float g) {
-    v4f r;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = fmaf(kr[e], d, s[e] * g);
-    __builtin_nontemporal_store(r, dst);
-}
-
-// Gated norm of head (bseq, h) split over two workgroups, run by one whole wave of each:
-// lane l holds the output of column hf*64 + l. Each publishes its half and partial sum of
-// squares, then counts in; the second to count in reads the other half and writes y for the
-// head, then resets the counter.
-// The published values go through agent-scope atomic stores and loads, which are coherent
-// across the XCDs' L2 caches without cache maintenance (an agent-scope fence would write
-// back and invalidate the whole L2, full of this kernel's state lines, per workgroup). The
-// stores are complete (vmcnt 0) before the counting atomic is issued, and the reads are
-// issued only after it has returned the partner's count.
-// This ordering is a gfx950 contract, not a HIP memory-model guarantee: the accesses are
-// relaxed, and what orders them is gfx950's code generation (agent-scope atomic stores and
-// loads bypass the non-coherent caches, and s_waitcnt vmcnt(0) retires the stores before the
-// counting atomic issues). A port to another target must replace it with release/acquire.
-#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
-#error "head_gate_exchange relies on gfx950 ordering of relaxed agent-scope atomics"
-#endif
-__device__ __forceinline__ void head_gate_exchange(const DecodeParams& p, const DecodeWs& ws, int bseq, int h,
-                                                   int hf, float v, int lane) {
-    const size_t hd = (size_t)bseq * p.L.h_v + h;
-    const float part = wave_sum_sq(v);
-    __hip_atomic_store(ws.xo + (hd * 2 + hf) * kHalfCols + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (lane == 0) __hip_atomic_store(ws.xs + hd * 2 + hf, part, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    int last = 0;
-    if (lane == 0) {
-        last = __hip_atomic_fetch_add(ws.head + hd, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 1;
-        if (last) __hip_atomic_store(ws.head + hd, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    last = __builtin_amdgcn_readfirstlane(last);
-    if (!last) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const int oh = hf ^ 1;
-    const float vo =
-        __hip_atomic_load(ws.xo + (hd * 2 + oh) * kHalfCols + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float po = __hip_atomic_load(ws.xs + hd * 2 + oh, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    out_gate_apply(p.og, hd * kD, hf ? vo : v, hf ? v : vo, hf ? po : part, hf ? part : po, lane);
-}
 
 // ---------------------------------------------------------------------------------------
 // slab_kernel: grid (2 h_v, B); workgroup = (sequence bseq, v head h, half tile hf)
 // ---------------------------------------------------------------------------------------
-template <int DC, bool GATED>
+template <int DC>
 __global__ void __launch_bounds__(kThreads)
 slab_kernel(const DecodeParams p, const DecodeWs ws) {
     __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kHalfCols];
-    __shared__ float o_s[GATED ? kHalfCols : 1];
     int* __restrict__ counters = ws.group;
     __shared__ float scal_s[2], gb_s[2];
     __shared__ int last_s;
@@ -263,29 +190,101 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
     }
     const float g = gb_s[0], bt = gb_s[1];
     const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
-    if constexpr (!GATED) {
 #pragma unroll
-        for (int u = 0; u < kPairsPerWave; ++u) {
-            const int j = j0 + 2 * u;
-            column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j,
-                          i4 == 0);
-        }
-    } else {
-        float dv[kPairsPerWave];
-#pragma unroll
-        for (int u = 0; u < kPairsPerWave; ++u) {
-            const int j = j0 + 2 * u;
-            const float ov = column_reduce(p, s[u], kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0, dv[u]);
-            if (i4 == 0) o_s[j - hf * kHalfCols] = ov;
-        }
-        __syncthreads();
-        if (w == 0) head_gate_exchange(p, ws, bseq, h, hf, o_s[lane], lane);
-#pragma unroll
-        for (int u = 0; u < kPairsPerWave; ++u) column_store(s[u], tile + (size_t)(j0 + 2 * u) * (kD / 4), kr, dv[u], g);
+    for (int u = 0; u < kPairsPerWave; ++u) {
+        const int j = j0 + 2 * u;
+        column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0);
     }
 
     if (tid == 0) last_s = old == mapped_count(L, src) * 2 - 1;
     lds_barrier();
+    if (last_s) {
+        if (tid < 128) hist_store<DC>(p, bseq, ch, nh);
+        if (tid == 0) counters[(size_t)bseq * L.h_k + src] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// head_kernel: grid (h_v, B); workgroup = (sequence bseq, v head h), 512 threads, gated
+// ---------------------------------------------------------------------------------------
+// The gated decode with one workgroup per head: the slab kernel's column math over all 128
+// columns (wave w owns columns 16 w + 2 u + half, u = 0..7), o collected in LDS, and the
+// gated RMS norm of the head applied by wave 0 after one barrier, so no two workgroups
+// exchange anything. The q/k conv history is written by the group's last member, found
+// with the same counters as the slab kernel (one arrival per head instead of two).
+constexpr int kHeadThreads = 512;
+template <int DC>
+__global__ void __launch_bounds__(kHeadThreads)
+head_kernel(const DecodeParams p, const DecodeWs ws) {
+    __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kD], o_s[kD];
+    __shared__ float scal_s[2], gb_s[2];
+    __shared__ int last_s;
+    int* __restrict__ counters = ws.group;
+
+    const Layer& L = p.L;
+    const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
+    const int half = lane >> 5, i4 = lane & 31;
+    const int h = blockIdx.x, bseq = blockIdx.y;
+    const int src = src_of(L, h);
+
+    // Conv inputs: threads 0..63 q pairs, 64..127 k pairs, 128..191 the head's v pairs.
+    int ch = 0;
+    float* dst = nullptr;
+    if (tid < 64) { ch = q_channel(L, src, 2 * tid); dst = q_s + 2 * tid; }
+    else if (tid < 128) { ch = k_channel(L, src, 2 * (tid - 64)); dst = k_s + 2 * (tid - 64); }
+    else if (tid < 192) { ch = v_channel(L, h, 2 * (tid - 128)); dst = v_s + 2 * (tid - 128); }
+    const bool conv_thread = tid < 192;
+    ConvPair<DC> cp;
+    if (conv_thread) conv_pair_load<DC>(p, bseq, ch, cp);
+    const size_t ab = (size_t)bseq * L.h_v + h;
+    const uint16_t a_in = p.a[ab], b_in = p.b[ab];
+
+    v4f* tile = reinterpret_cast<v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
+    const int j0 = 2 * kPairsPerWave * w + half;
+    v4f s[kPairsPerWave];
+#pragma unroll
+    for (int u = 0; u < kPairsPerWave; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
+
+    uint32_t nh[DC - 1];
+    float y0 = 0.0f, y1 = 0.0f;
+    if (conv_thread) {
+        conv_pair_eval<DC>(L, cp, y0, y1, nh);
+        dst[0] = y0;
+        dst[1] = y1;
+        if (tid >= 128) hist_store<DC>(p, bseq, ch, nh);
+    }
+    if (w < 2) {
+        const float r = wave_sum(fmaf(y0, y0, y1 * y1));
+        if (lane == 0) scal_s[w] = r;
+    }
+    if (tid == kHeadThreads - 1) {
+        gb_s[0] = expf(log_gate(L, h, bf16_to_f32(a_in)));
+        gb_s[1] = sigmoid_f(bf16_to_f32(b_in));
+    }
+    lds_barrier();
+
+    int old = 0;
+    if (tid == 0) old = atomicAdd(counters + (size_t)bseq * L.h_k + src, 1);
+    const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
+    const float inv_k = 1.0f / sqrtf(scal_s[1] + L.l2_eps);
+    const float kq = wave_sum(fmaf(q_s[lane], k_s[lane], q_s[lane + kWave] * k_s[lane + kWave])) * inv_q * inv_k;
+    v4f kr, qr;
+    {
+        const v4f kk = *reinterpret_cast<const v4f*>(k_s + 4 * i4), qq = *reinterpret_cast<const v4f*>(q_s + 4 * i4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { kr[e] = kk[e] * inv_k; qr[e] = qq[e] * inv_q; }
+    }
+    const float g = gb_s[0], bt = gb_s[1];
+    const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
+#pragma unroll
+    for (int u = 0; u < kPairsPerWave; ++u) {
+        const int j = j0 + 2 * u;
+        const float ov = column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j], g, bt, kq, ob + j, i4 == 0);
+        if (i4 == 0) o_s[j] = ov;
+    }
+    if (tid == 0) last_s = old == mapped_count(L, src) - 1;
+    lds_barrier();
+    if (w == 0) out_gate_head(p.og, ob, o_s[lane], o_s[lane + kWave], lane);
     if (last_s) {
         if (tid < 128) hist_store<DC>(p, bseq, ch, nh);
         if (tid == 0) counters[(size_t)bseq * L.h_k + src] = 0;
@@ -408,25 +407,25 @@ inline bool every_src_used(const ix_gdn_cfg* cfg) {
     return cfg->head_map == IX_GDN_HEAD_DIV || cfg->h_v >= cfg->h_k;
 }
 
-inline DecodeWs bind_decode_ws(void* workspace, int B, const ix_gdn_cfg* cfg) {
-    size_t off[4];
-    decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
-    char* base = static_cast<char*>(workspace);
-    return DecodeWs{reinterpret_cast<int*>(base + off[0]), reinterpret_cast<int*>(base + off[1]),
-                    reinterpret_cast<float*>(base + off[2]), reinterpret_cast<float*>(base + off[3])};
-}
+inline DecodeWs bind_decode_ws(void* workspace) { return DecodeWs{static_cast<int*>(workspace)}; }
 
-// ws: the workspace sections (group counters at least; the gated kernel also uses the head
-// counters and exchange slots), or null for the group kernel.
+// ws: the group counters, or null for the group kernel.
 template <bool GATED>
 void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, const DecodeWs* ws, hipStream_t s) {
     const dim3 block(kThreads);
-    if (ws && every_src_used(cfg)) {
+    if (ws && every_src_used(cfg) && GATED) {
+        const dim3 grid((unsigned)cfg->h_v, (unsigned)B), hblock(kHeadThreads);
+        switch (cfg->d_conv) {
+            case 2: hipLaunchKernelGGL(head_kernel<2>, grid, hblock, 0, s, p, *ws); break;
+            case 3: hipLaunchKernelGGL(head_kernel<3>, grid, hblock, 0, s, p, *ws); break;
+            default: hipLaunchKernelGGL(head_kernel<4>, grid, hblock, 0, s, p, *ws); break;
+        }
+    } else if (ws && every_src_used(cfg)) {
         const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
         switch (cfg->d_conv) {
-            case 2: hipLaunchKernelGGL((slab_kernel<2, GATED>), grid, block, 0, s, p, *ws); break;
-            case 3: hipLaunchKernelGGL((slab_kernel<3, GATED>), grid, block, 0, s, p, *ws); break;
-            default: hipLaunchKernelGGL((slab_kernel<4, GATED>), grid, block, 0, s, p, *ws); break;
+            case 2: hipLaunchKernelGGL(slab_kernel<2>, grid, block, 0, s, p, *ws); break;
+            case 3: hipLaunchKernelGGL(slab_kernel<3>, grid, block, 0, s, p, *ws); break;
+            default: hipLaunchKernelGGL(slab_kernel<4>, grid, block, 0, s, p, *ws); break;
         }
     } else {
         const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
@@ -464,8 +463,7 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
 
 extern "C" size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || B <= 0 || B > 65535) return 0;
-    size_t off[4];
-    return ixg::decode_ws_layout(B, cfg->h_k, cfg->h_v, off);
+    return ixg::decode_ws_bytes(B, cfg->h_k);
 }
 
 // Validation and parameter set-up shared by the plain and gated decode.
@@ -508,7 +506,7 @@ extern "C" hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t
                                        workspace, p);
     if (e != hipSuccess) return e;
     if (workspace) {
-        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace, B, cfg);
+        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace);
         ixg::launch_decode<false>(cfg, B, p, &ws, s);
     } else {
         ixg::launch_decode<false>(cfg, B, p, nullptr, s);
@@ -528,7 +526,7 @@ extern "C" hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const ui
     if ((e = ix_gdn_check_gate_(gate)) != hipSuccess) return e;
     p.og = ixg::make_out_gate(gate);
     if (workspace) {
-        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace, B, cfg);
+        const ixg::DecodeWs ws = ixg::bind_decode_ws(workspace);
         ixg::launch_decode<true>(cfg, B, p, &ws, s);
     } else {
         ixg::launch_decode<true>(cfg, B, p, nullptr, s);
@@ -589,7 +587,7 @@ extern "C" hipError_t ix_gdn_decode_noalloc(const ix_gdn_cfg* cfg, int B, const 
     }
     int* counters = nullptr;
     if ((e = noalloc_counters(s, &counters)) != hipSuccess) return e;
-    const ixg::DecodeWs ws{counters, nullptr, nullptr, nullptr};   // the ungated kernel uses the counters only
+    const ixg::DecodeWs ws{counters};
     ixg::launch_decode<false>(cfg, B, p, &ws, s);
     return hipGetLastError();
 }

@@ -89,8 +89,8 @@ int ix_gdn_channels(const ix_gdn_cfg* cfg);
  * element (b, h, i, j) is at ((b*h_v + h)*d_v + j)*d_k + i and every column is contiguous. */
 
 /* Bytes of the workspace ix_gdn_decode and ix_gdn_decode_gated can use for B sequences, or 0
- * for an invalid description. It holds per-group counters (which the calls keep at zero) and
- * per-head exchange slots for the gated output norm (scratch, never needs clearing). */
+ * for an invalid description. It holds one counter per (sequence, q/k head), which the
+ * calls keep at zero. */
 size_t ix_gdn_decode_workspace_size(const ix_gdn_cfg* cfg, int B);
 
 /* Gated RMS output norm fused into a layer call's epilogue: for every token row and v head,
@@ -149,8 +149,7 @@ hipError_t ix_gdn_decode_noalloc(const ix_gdn_cfg* cfg, int B, const uint16_t* x
 /* ix_gdn_decode followed by the gated output norm of each (sequence, v head), in the same
  * launch: gate->z, gate->y, gate->y_bf16 are [B][h_v][d_v]. o and o_bf16 may both be NULL.
  * gate must be non-NULL with z, ssm_norm and at least one of y, y_bf16 set. With a workspace
- * the two workgroups of a head pass their outputs through its exchange slots, and the second
- * to finish writes y for the whole head. */
+ * one workgroup per (sequence, v head) computes the head's outputs and applies the norm. */
 hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16_t* conv_state,
                                const uint16_t* conv_w, const uint16_t* a, const uint16_t* b,
                                const float* A_log, const float* dt_bias, float* state, float* o,

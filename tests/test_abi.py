@@ -182,13 +182,12 @@ def test_gated_validation_without_launch():
 
 
 def test_decode_workspace_sections():
-    # group counters [B][h_k], head counters [B][h_v], exchange [B][h_v][2][64] fp32 and
-    # [B][h_v][2] fp32, each section 256-byte aligned
-    cfg = bx.make_cfg()
+    # one int32 counter per (sequence, q/k head), rounded up to 256 bytes
     r = lambda n: (n + 255) // 256 * 256
-    for B in (1, 3, 64):
-        assert bx.ix_gdn_decode_workspace_size(cfg, B) == (r(B * 16 * 4) + r(B * 32 * 4) + r(B * 32 * 2 * 64 * 4)
-                                                          + r(B * 32 * 2 * 4))
+    for kw in ({}, dict(h_k=2, h_v=18), dict(h_k=3, h_v=8)):
+        cfg = bx.make_cfg(**kw)
+        for B in (1, 3, 64):
+            assert bx.ix_gdn_decode_workspace_size(cfg, B) == r(B * cfg.h_k * 4)
 
 
 def test_window_validation_without_launch():

@@ -28,11 +28,9 @@ def _torch():
 
 
 def counters_zero(ws, cfg, B):
-    r = lambda n: (n + 255) // 256 * 256
-    n = r(B * cfg.h_k * 4) + B * cfg.h_v * 4          # group counters, then head counters
-    head_off = r(B * cfg.h_k * 4)
     w = host(ws)
-    return not w[:B * cfg.h_k * 4].any() and not w[head_off:n].any()
+    assert w.size >= B * cfg.h_k * 4                  # one int32 counter per (sequence, q/k head)
+    return not w.any()
 
 
 class Layer:
@@ -101,7 +99,7 @@ def test_decode_gated_matches_out_norm(kw, B, ws):
 
 def test_decode_gated_kernels_agree_and_o_optional():
     # Both kernels give the same y within fp32 rounding of their (differently ordered) o; the
-    # workspace kernel's y does not depend on which half-head workgroup finishes last, so
+    # workspace kernel's y does not depend on which workgroup of a group finishes last, so
     # repeated runs are bit-identical; o may be omitted.
     cfg = bx.make_cfg()
     B, seed = 8, inputs.seed_for(2) + 77
