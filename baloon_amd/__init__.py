@@ -34,7 +34,7 @@ EXPORTS = (
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
     "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_decode_window_mfma", "ix_gdn_commit_window",
     "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
-    "ix_gdn_version", "ix_gdn_decode_noalloc",
+    "ix_gdn_version", "ix_gdn_decode_noalloc", "ix_q8_1_quantize",
 )
 
 
@@ -64,7 +64,7 @@ class OutGate(ctypes.Structure):
 
     _fields_ = [
         ("z", ctypes.c_void_p), ("ssm_norm", ctypes.c_void_p), ("eps", ctypes.c_float),
-        ("y", ctypes.c_void_p), ("y_bf16", ctypes.c_void_p),
+        ("y", ctypes.c_void_p), ("y_bf16", ctypes.c_void_p), ("y_q8_1", ctypes.c_void_p),
     ]
 
 
@@ -112,6 +112,7 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_in_proj": ([P, I, I, P, P, P, P, P, P, P, P], I),
         "ix_gdn_version": ([], ctypes.c_char_p),
         "ix_gdn_decode_noalloc": ([P, I, P, P, P, P, P, P, P, P, P, P, P], I),
+        "ix_q8_1_quantize": ([P, P, LL, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -206,9 +207,10 @@ def ix_gdn_prefill(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, 
                                 _ptr(o_bf16), _ptr(workspace), workspace_bytes, _stream(s))
 
 
-def out_gate(z, ssm_norm, eps, y=None, y_bf16=None) -> OutGate:
-    """The gate description of the gated calls, from device tensors (z bf16, ssm_norm fp32)."""
-    return OutGate(_ptr(z), _ptr(ssm_norm), eps, _ptr(y), _ptr(y_bf16))
+def out_gate(z, ssm_norm, eps, y=None, y_bf16=None, y_q8_1=None) -> OutGate:
+    """The gate description of the gated calls, from device tensors (z bf16, ssm_norm fp32;
+    y_q8_1 a byte buffer of 36 bytes per 32 outputs)."""
+    return OutGate(_ptr(z), _ptr(ssm_norm), eps, _ptr(y), _ptr(y_bf16), _ptr(y_q8_1))
 
 
 def ix_gdn_decode_gated(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias, state, o=None, o_bf16=None,
@@ -278,6 +280,11 @@ def ix_bf16_gemv_split(x, w, y, n_in, n_out, threads_per_row, s=None) -> int:
 
 def ix_mmvq_q8_0(weights, x_q8_1, y, n_in, n_out, ncols, s=None) -> int:
     return lib().ix_mmvq_q8_0(_ptr(weights), _ptr(x_q8_1), _ptr(y), n_in, n_out, ncols, _stream(s))
+
+
+def ix_q8_1_quantize(x, y_q8_1, n, s=None) -> int:
+    """q8_1 blocks (36 bytes per 32 values) of n fp32 values: the activation format of ix_mmvq_q8_0."""
+    return lib().ix_q8_1_quantize(_ptr(x), _ptr(y_q8_1), n, _stream(s))
 
 
 def ix_gdn_in_proj_width(cfg: Cfg) -> int:

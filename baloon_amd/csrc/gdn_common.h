@@ -118,12 +118,42 @@ struct OutGate {
     float eps;
     float* y;
     uint16_t* y_bf16;
+    uint8_t* y_q8_1;
 };
 
 inline OutGate make_out_gate(const ix_gdn_out_gate* g) {
     OutGate o{};
-    if (g) { o.z = g->z; o.nrm = g->ssm_norm; o.eps = g->eps; o.y = g->y; o.y_bf16 = g->y_bf16; }
+    if (g) {
+        o.z = g->z; o.nrm = g->ssm_norm; o.eps = g->eps; o.y = g->y; o.y_bf16 = g->y_bf16;
+        o.y_q8_1 = static_cast<uint8_t*>(g->y_q8_1);
+    }
     return o;
+}
+
+// q8_1 block (36 bytes: half d, half s, int8 qs[32]; the activation format of the Q8_0 product,
+// src/ix_mmvq_wave.cu:20-24) of the 32 values v held by the 32 lanes of this lane's half wave,
+// lane & 31 being the value's position: d = max|v| / 127, qs = roundf(v / d) (0 when max|v|
+// is 0), s = the sum of v in the xor-butterfly order 16, 8, 4, 2, 1; d and s rounded to half.
+// Every q8_1 producer here (ix_q8_1_quantize and the gated epilogues) goes through this one
+// function, so the same fp32 values give the same bytes, division included
+// (src/ix_q81_div.h:1-9). The inputs are finite. All 64 lanes of the wave must call it (its
+// reductions stay within each half wave); a half wave that passes blk == nullptr stores nothing.
+constexpr int kQ81Bytes = 36;
+__device__ __forceinline__ void q81_store(float v, int lane, uint8_t* blk) {
+    float amax = fabsf(v), sum = v;
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+        sum = sum + __shfl_xor(sum, off, kWave);
+    }
+    const float d = amax / 127.0f;
+    const int q = amax == 0.0f ? 0 : (int)roundf(v / d);
+    if (!blk) return;
+    blk[4 + (lane & 31)] = (uint8_t)(int8_t)q;
+    if ((lane & 31) == 0) {
+        const uint32_t hd = __builtin_bit_cast(uint16_t, (_Float16)d), hs = __builtin_bit_cast(uint16_t, (_Float16)sum);
+        *reinterpret_cast<uint32_t*>(blk) = hd | (hs << 16);
+    }
 }
 
 // Sum of v^2 over the wave, the same bits in every lane and in every kernel that calls it:
@@ -150,6 +180,7 @@ __device__ __forceinline__ void out_gate_apply(const OutGate& g, size_t row, flo
         const float y = (q ? hi : lo) * inv * g.nrm[j] * sigmoid_f(bf16_to_f32(g.z[row + j]));
         if (g.y) g.y[row + j] = y;
         if (g.y_bf16) g.y_bf16[row + j] = f32_to_bf16(y);
+        if (g.y_q8_1) q81_store(y, lane, g.y_q8_1 + ((row + j) / 32) * kQ81Bytes);
     }
 }
 __device__ __forceinline__ void out_gate_head(const OutGate& g, size_t row, float lo, float hi, int lane) {

@@ -490,9 +490,10 @@ static hipError_t decode_params(const ix_gdn_cfg* cfg, int B, const uint16_t* x,
 
 // The gate description of the gated calls: z and ssm_norm, at least one output, aligned.
 extern "C" hipError_t ix_gdn_check_gate_(const ix_gdn_out_gate* g) {
-    if (!g || !g->z || !g->ssm_norm || (!g->y && !g->y_bf16)) return hipErrorInvalidValue;
+    if (!g || !g->z || !g->ssm_norm || (!g->y && !g->y_bf16 && !g->y_q8_1)) return hipErrorInvalidValue;
     if ((reinterpret_cast<uintptr_t>(g->z) & 1) || (reinterpret_cast<uintptr_t>(g->ssm_norm) & 3) ||
-        (reinterpret_cast<uintptr_t>(g->y) & 3) || (reinterpret_cast<uintptr_t>(g->y_bf16) & 1))
+        (reinterpret_cast<uintptr_t>(g->y) & 3) || (reinterpret_cast<uintptr_t>(g->y_bf16) & 1) ||
+        (reinterpret_cast<uintptr_t>(g->y_q8_1) & 3))
         return hipErrorInvalidValue;
     return hipSuccess;
 }

@@ -9,6 +9,8 @@
 // is this build's own), and the pair product gives bit-identical results to the single one.
 #include "gdn_common.h"
 
+#include <algorithm>
+
 namespace ixg {
 namespace {
 
@@ -114,7 +116,7 @@ gemv_block_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w
 // the two integer halves are added exactly, then scaled once per block. Each column's sum is
 // computed by the same code whatever the number of columns launched.
 // ---------------------------------------------------------------------------------------
-constexpr int kQ80Bytes = 34, kQ81Bytes = 36;
+constexpr int kQ80Bytes = 34;                       // kQ81Bytes (36) is in gdn_common.h
 
 __device__ __forceinline__ float half_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -162,6 +164,19 @@ inline bool vec_rows(const uint16_t* x, const uint16_t* w, long long n_in) {
 }
 inline unsigned row_blocks(long long n_out) { return (unsigned)((n_out + kRowsPerBlock - 1) / kRowsPerBlock); }
 
+// q8_1 quantiser: x [n] fp32 -> [n/32] q8_1 blocks; each wave takes 64 consecutive values
+// (two blocks, one per half wave) per step, through the same q81_store as the gated epilogues.
+__global__ void __launch_bounds__(256) q81_kernel(const float* __restrict__ x, uint8_t* __restrict__ y, long long nb) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const long long waves = (long long)gridDim.x * (256 / kWave);
+    for (long long wv = ((long long)blockIdx.x * 256 + threadIdx.x) / kWave; 2 * wv < nb; wv += waves) {
+        const long long b = 2 * wv + (lane >> 5);            // this lane's block
+        const bool live = b < nb;                             // false only in the upper half of the last wave
+        const float v = live ? x[b * 32 + (lane & 31)] : 0.0f;
+        q81_store(v, lane, live ? y + b * kQ81Bytes : nullptr);
+    }
+}
+
 }  // namespace
 }  // namespace ixg
 
@@ -205,6 +220,15 @@ extern "C" hipError_t ix_bf16_gemv_split(const uint16_t* x, const uint16_t* w, f
         hipLaunchKernelGGL(gemv_block_kernel, dim3((unsigned)n_out), dim3(threads_per_row), 0, s, x, w, y, n_in,
                            threads_per_row, vec);
     }
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ix_q8_1_quantize(const float* x, void* y_q8_1, long long n, hipStream_t s) {
+    if (n <= 0 || n % 32 != 0 || !x || !y_q8_1) return hipErrorInvalidValue;
+    if ((reinterpret_cast<uintptr_t>(x) & 3) || (reinterpret_cast<uintptr_t>(y_q8_1) & 3)) return hipErrorInvalidValue;
+    const long long nb = n / 32, waves = (nb + 1) / 2;
+    const long long blocks = std::min<long long>((waves + 3) / 4, 65536);
+    hipLaunchKernelGGL(ixg::q81_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, static_cast<uint8_t*>(y_q8_1), nb);
     return hipGetLastError();
 }
 

@@ -105,6 +105,9 @@ typedef struct ix_gdn_out_gate {
     float eps;
     float* y;                 /* [rows][h_v][d_v] fp32, or NULL */
     uint16_t* y_bf16;         /* [rows][h_v][d_v] bf16 (RNE of the fp32 value), or NULL */
+    void* y_q8_1;             /* [rows][h_v*d_v/32] q8_1 blocks of the fp32 value (the activation
+                               * format of ix_mmvq_q8_0; see ix_q8_1_quantize), 4-byte aligned, or
+                               * NULL */
 } ix_gdn_out_gate;
 
 /* One decode token for B independent sequences of one GDN layer, in one launch:
@@ -266,6 +269,16 @@ hipError_t ix_bf16_gemv_split(const uint16_t* x, const uint16_t* w, float* y, lo
  * column's result does not depend on ncols. */
 hipError_t ix_mmvq_q8_0(const void* weights, const void* x_q8_1, float* y, int n_in, int n_out, int ncols,
                         hipStream_t s IX_GDN_DEFAULT_STREAM);
+
+/* q8_1 quantiser of fp32 activations for ix_mmvq_q8_0 (addition; the reference has the format,
+ * src/ix_mmvq_wave.cu:20-24, and the division rule every q8_1 producer shares,
+ * src/ix_q81_div.h:1-9, but no quantiser). x [n] fp32 -> y_q8_1 [n/32] blocks of 36 bytes:
+ * for each 32 consecutive values, d = max|x| / 127 (IEEE division), qs = roundf(x / d) (0 for
+ * an all-zero block), s = the sum of the 32 values in xor-butterfly order (16, 8, 4, 2, 1),
+ * d and s stored as fp16 (RNE). The gated calls' y_q8_1 output goes through the same device
+ * function, so it equals this quantiser applied to their fp32 y, byte for byte. Requires
+ * n > 0, n % 32 == 0, 4-byte aligned x and y_q8_1, finite x. */
+hipError_t ix_q8_1_quantize(const float* x, void* y_q8_1, long long n, hipStream_t s IX_GDN_DEFAULT_STREAM);
 
 /* Output width N of the layer's input projection: C + h_v*d_v + 2*h_v (x | z | a | b), or 0
  * for an invalid description. */

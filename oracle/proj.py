@@ -7,7 +7,12 @@ Restates the reference's double-precision host checks:
     d_w * d_x * (integer dot of the block's 32 int8 pairs) in double, with the scale
     sum |d_w d_x| * 32 * 127 * 127 of tests/test_mmvq_wave.cu:57-58 (tolerance 1e-5 x scale);
   * the block formats of src/ix_mmvq_wave.cu:22-25: Q8_0 = fp16 d + 32 int8 (34 bytes),
-    q8_1 = fp16 d, fp16 s + 32 int8 (36 bytes), little endian, packed back to back.
+    q8_1 = fp16 d, fp16 s + 32 int8 (36 bytes), little endian, packed back to back;
+  * the q8_1 quantiser (q8_1_quantize below): the reference fixes the division every q8_1
+    producer uses (src/ix_q81_div.h:1-9: d = amax / 127, q = roundf(x / d), IEEE division,
+    no fast-math) but ships no quantiser, so the rest follows the published q8_1 quantiser of
+    ggml (llama.cpp, ggml-cuda/quantize.cu, MIT): d = max|x| / 127, q = 0 for an all-zero
+    block, s = the sum of the block's values, d and s stored as fp16.
 The layer's input projection is the same GEMV for B rows, split into the pieces
 x | z | a | b (include/ix_gdn.h).
 """
@@ -87,3 +92,35 @@ def q8_0_ref(wd, wq, xd, xq):
     y = np.einsum("crb,rb,cb->cr", dots.astype(np.float64), dw, dx)
     sc = np.einsum("rb,cb->cr", np.abs(dw), np.abs(dx)) * 32 * 127 * 127
     return y, sc
+
+
+def q8_1_quantize(x) -> np.ndarray:
+    """fp32 values [n] (n % 32 == 0) -> q8_1 bytes [n / 32 * 36], per 32 consecutive values:
+    d = max|x| / 127 in fp32 (IEEE division, src/ix_q81_div.h:8-9), qs = roundf(x / d) with the
+    quotient in fp32 and ties away from zero (0 when max|x| = 0), s = the fp32 sum taken in
+    xor-butterfly order (offsets 16, 8, 4, 2, 1: the order of a 32-lane butterfly, in which
+    every lane ends with the same bits), d and s rounded to fp16.
+    Pinning: the division and rounding rule is the reference's (ix_q81_div.h); the block
+    layout its Q8_0 product's (src/ix_mmvq_wave.cu:20-24); the q = 0 rule and the s term are
+    ggml's. The Q8_0 product reads only d and qs, so s is "parity unpinned" against the
+    reference (checked here against a float64 sum and the butterfly order only)."""
+    x = np.asarray(x, np.float32).reshape(-1, 32)
+    amax = np.abs(x).max(axis=1)
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        t = (x / d[:, None]).astype(np.float32)
+        r = np.sign(t).astype(np.float64) * np.floor(np.abs(t).astype(np.float64) + 0.5)
+    q = np.where(amax[:, None] == 0, 0.0, r).astype(np.int8)
+    s = x.copy()
+    idx = np.arange(32)
+    for off in (16, 8, 4, 2, 1):
+        s = (s + s[:, idx ^ off]).astype(np.float32)
+    dh = d.astype(np.float16).view(np.uint16)[:, None]
+    sh = s[:, 0].astype(np.float16).view(np.uint16)[:, None]
+    return pack_q8_1(dh, q[:, None, :], sh)
+
+
+def q8_1_unpack(b):
+    """q8_1 bytes -> (d bits uint16 [nb], s bits uint16 [nb], qs int8 [nb][32])."""
+    b = np.asarray(b, np.uint8).reshape(-1, 36)
+    return b[:, 0:2].copy().view("<u2")[:, 0], b[:, 2:4].copy().view("<u2")[:, 0], b[:, 4:36].copy().view(np.int8)

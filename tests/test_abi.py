@@ -164,6 +164,7 @@ def test_gated_validation_without_launch():
     assert dec(bx.OutGate(1 << 20, 1 << 20, 1e-6, None, None)) == INVALID      # no output
     assert dec(bx.OutGate(1 << 20, (1 << 20) + 2, 1e-6, 1 << 20, None)) == INVALID   # ssm_norm alignment
     assert dec(bx.OutGate((1 << 20) + 1, 1 << 20, 1e-6, None, 1 << 20)) == INVALID   # z alignment
+    assert dec(bx.OutGate(1 << 20, 1 << 20, 1e-6, None, None, (1 << 20) + 2)) == INVALID   # y_q8_1 alignment
     assert dec(ok, bx.make_cfg(d_conv=7)) == INVALID
 
     need = bx.ix_gdn_prefill_workspace_size(cfg, 2, 100)
@@ -241,3 +242,13 @@ def test_projection_validation_without_launch():
         assert L.ix_gdn_in_proj(ctypes.byref(cfg), B, K, *ok) == INVALID
     assert L.ix_gdn_in_proj(ctypes.byref(cfg), 4, 2048, ctypes.c_void_p((1 << 20) + 8), p, p, p, p, p, NULL,
                             NULL) == INVALID                                    # h must be 16-byte aligned
+
+
+def test_q8_1_validation_without_launch():
+    L = bx.lib()
+    a = 1 << 20
+    assert L.ix_q8_1_quantize(a, a, 0, None) == INVALID
+    assert L.ix_q8_1_quantize(a, a, 48, None) == INVALID          # not whole blocks
+    assert L.ix_q8_1_quantize(None, a, 64, None) == INVALID
+    assert L.ix_q8_1_quantize(a + 2, a, 64, None) == INVALID      # fp32 alignment
+    assert L.ix_q8_1_quantize(a, a + 2, 64, None) == INVALID      # block alignment

@@ -68,3 +68,39 @@ def test_q8_blocks_distribution():
     assert dv.min() >= 1 / 1024 and dv.max() <= 2047 / 1024
     assert np.all(np.abs(dv * 1024 - np.round(dv * 1024)) == 0)      # exact multiples of 1/1024
     assert q.min() >= -127 and q.max() <= 127 and q.dtype == np.int8
+
+
+def test_q8_1_quantize_known_answers():
+    # One block with max|x| = 127 (d = 1): ties go away from zero (2.5 -> 3, -2.5 -> -3, a
+    # round-half-even mistake gives 2 and -2), 126.5 -> 127; a second, all-zero block is all
+    # zero bytes (d = 0, q = 0, not a division by zero); a third with max|x| = 63.5 (d = 0.5).
+    x = np.zeros(96, np.float32)
+    x[:5] = [2.5, -2.5, 127.0, -126.5, 0.49999997]
+    x[64:67] = [63.5, -1.25, 0.25]
+    d, s, q = proj.q8_1_unpack(proj.q8_1_quantize(x))
+    np.testing.assert_array_equal(d.view(np.float16), np.array([1.0, 0.0, 0.5], np.float16))
+    np.testing.assert_array_equal(q[0][:5], [3, -3, 127, -127, 0])
+    assert not q[0][5:].any() and not q[1].any() and d[1] == 0 and s[1] == 0
+    np.testing.assert_array_equal(q[2][:3], [127, -3, 1])                   # 63.5/0.5, -2.5 -> -3, 0.5 -> 1
+    assert s.view(np.float16)[0] == np.float16(2.5 - 2.5 + 127.0 - 126.5 + 0.49999997)
+    # block layout: d at bytes 0-1, s at 2-3, qs at 4-35 of each 36-byte block
+    b = proj.q8_1_quantize(x)
+    assert b.size == 3 * 36 and b[36 + 4:72].sum() == 0 and b[72:74].view("<u2")[0] == np.float16(0.5).view(np.uint16)
+
+
+def test_q8_1_quantize_bounds_and_sum():
+    g = Gen(41)
+    nb = 4000
+    scale = np.exp(g.normal(1, (nb, 1)) * 2).astype(np.float32)           # magnitudes over ~7 decades, sums in fp16 range
+    x = (g.normal(2, (nb, 32)) * scale).astype(np.float32)
+    d, s, q = proj.q8_1_unpack(proj.q8_1_quantize(x.reshape(-1)))
+    d32 = np.abs(x).max(axis=1) / np.float32(127.0)
+    assert np.abs(q).max() <= 127 and (np.abs(q).max(axis=1) == 127).all()  # the largest value maps to +-127
+    err = np.abs(x.astype(np.float64) - q.astype(np.float64) * d32[:, None].astype(np.float64))
+    assert (err <= 0.5 * d32[:, None] * (1 + 2.0 ** -20)).all()             # round to nearest in units of d
+    np.testing.assert_array_equal(d, d32.astype(np.float16).view(np.uint16))
+    ref = x.astype(np.float64).sum(axis=1)
+    assert np.abs(ref).max() < 60000
+    # fp32 summation error, then one fp16 rounding (relative 2^-11, or half the subnormal step)
+    tol = 32 * 2.0 ** -23 * np.abs(x).astype(np.float64).sum(axis=1) + np.abs(ref) * 2.0 ** -11 + 2.0 ** -25
+    assert (np.abs(s.view(np.float16).astype(np.float64) - ref) <= tol).all()
