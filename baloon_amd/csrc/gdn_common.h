@@ -132,8 +132,9 @@ inline OutGate make_out_gate(const ix_gdn_out_gate* g) {
 
 // q8_1 block (36 bytes: half d, half s, int8 qs[32]; the activation format of the Q8_0 product,
 // src/ix_mmvq_wave.cu:20-24) of the 32 values v held by the 32 lanes of this lane's half wave,
-// lane & 31 being the value's position: d = max|v| / 127, qs = roundf(v / d) (0 when max|v|
-// is 0), s = the sum of v in the xor-butterfly order 16, 8, 4, 2, 1; d and s rounded to half.
+// lane & 31 being the value's position: d = max|v| / 127, qs = roundf(v / d) (0 when d is 0:
+// an all-zero block, or one so small that d underflows), s = the sum of v in the
+// xor-butterfly order 16, 8, 4, 2, 1; d and s rounded to half.
 // Every q8_1 producer here (ix_q8_1_quantize and the gated epilogues) goes through this one
 // function, so the same fp32 values give the same bytes, division included
 // (src/ix_q81_div.h:1-9). The inputs are finite. All 64 lanes of the wave must call it (its
@@ -147,7 +148,7 @@ __device__ __forceinline__ void q81_store(float v, int lane, uint8_t* blk) {
         sum = sum + __shfl_xor(sum, off, kWave);
     }
     const float d = amax / 127.0f;
-    const int q = amax == 0.0f ? 0 : (int)roundf(v / d);
+    const int q = d == 0.0f ? 0 : (int)roundf(v / d);
     if (!blk) return;
     blk[4 + (lane & 31)] = (uint8_t)(int8_t)q;
     if ((lane & 31) == 0) {

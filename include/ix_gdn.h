@@ -273,8 +273,8 @@ hipError_t ix_mmvq_q8_0(const void* weights, const void* x_q8_1, float* y, int n
 /* q8_1 quantiser of fp32 activations for ix_mmvq_q8_0 (addition; the reference has the format,
  * src/ix_mmvq_wave.cu:20-24, and the division rule every q8_1 producer shares,
  * src/ix_q81_div.h:1-9, but no quantiser). x [n] fp32 -> y_q8_1 [n/32] blocks of 36 bytes:
- * for each 32 consecutive values, d = max|x| / 127 (IEEE division), qs = roundf(x / d) (0 for
- * an all-zero block), s = the sum of the 32 values in xor-butterfly order (16, 8, 4, 2, 1),
+ * for each 32 consecutive values, d = max|x| / 127 (IEEE division), qs = roundf(x / d) (0 when
+ * d is 0), s = the sum of the 32 values in xor-butterfly order (16, 8, 4, 2, 1),
  * d and s stored as fp16 (RNE). The gated calls' y_q8_1 output goes through the same device
  * function, so it equals this quantiser applied to their fp32 y, byte for byte. Requires
  * n > 0, n % 32 == 0, 4-byte aligned x and y_q8_1, finite x. */

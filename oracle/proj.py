@@ -97,7 +97,8 @@ def q8_0_ref(wd, wq, xd, xq):
 def q8_1_quantize(x) -> np.ndarray:
     """fp32 values [n] (n % 32 == 0) -> q8_1 bytes [n / 32 * 36], per 32 consecutive values:
     d = max|x| / 127 in fp32 (IEEE division, src/ix_q81_div.h:8-9), qs = roundf(x / d) with the
-    quotient in fp32 and ties away from zero (0 when max|x| = 0), s = the fp32 sum taken in
+    quotient in fp32 and ties away from zero (0 when d = 0: an all-zero block, or one whose d
+    underflows), s = the fp32 sum taken in
     xor-butterfly order (offsets 16, 8, 4, 2, 1: the order of a 32-lane butterfly, in which
     every lane ends with the same bits), d and s rounded to fp16.
     Pinning: the division and rounding rule is the reference's (ix_q81_div.h); the block
@@ -110,7 +111,7 @@ def q8_1_quantize(x) -> np.ndarray:
     with np.errstate(divide="ignore", invalid="ignore"):
         t = (x / d[:, None]).astype(np.float32)
         r = np.sign(t).astype(np.float64) * np.floor(np.abs(t).astype(np.float64) + 0.5)
-    q = np.where(amax[:, None] == 0, 0.0, r).astype(np.int8)
+    q = np.where(d[:, None] == 0, 0.0, r).astype(np.int8)
     s = x.copy()
     idx = np.arange(32)
     for off in (16, 8, 4, 2, 1):

@@ -39,6 +39,8 @@ def test_quantize_matches_oracle(nb):
         x[1] = 0.0                                                     # an all-zero block
         x[2] = 0.0
         x[2, :4] = [127.0, 2.5, -2.5, -0.5]                            # exact ties: d = 1
+        x[3] = 0.0
+        x[3, :2] = [1e-44, -1e-45]                                     # d = max/127 underflows to 0
     got = quantize(dev(x.reshape(-1)))
     want = proj.q8_1_quantize(x.reshape(-1))
     np.testing.assert_array_equal(got, want)
