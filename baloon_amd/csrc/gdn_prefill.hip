@@ -20,7 +20,8 @@
 //
 // Kernels, in stream order:
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
-//                  the chunk table (sequence and first token of each chunk)
+//                  the chunk table (sequence and first token of each chunk); not launched
+//                  for a single sequence, whose geometry the kernels derive from cu[0], cu[1]
 //   qk_kernel      per (chunk, q/k head): conv (history from conv_state at sequence starts)
 //                  and L2 norms of q and k; K K^T and Q K^T (lower block triangle) once for
 //                  all the v heads mapped to the q/k head, stored raw; K^T and Q written as
@@ -113,7 +114,20 @@ struct PrefillParams {
     float* o;                   // [T][h_v][128] or null
     uint16_t* o_bf16;           // [T][h_v][128] or null
     int n_seq, T, NC;
+    int single;                 // n_seq == 1: no plan pass; the geometry comes from cu[0], cu[1]
 };
+
+// Clamped bounds [lo, hi) of sequence s: the plan's seq_lo (running maximum of the offsets,
+// clamped to [0, T]), or for a single sequence the same two values from cu directly.
+__device__ __forceinline__ void seq_bounds(const PrefillParams& p, int s, int& lo, int& hi) {
+    if (p.single) {
+        lo = min(max(p.cu[0], 0), p.T);
+        hi = max(min(max(p.cu[1], 0), p.T), lo);
+    } else {
+        lo = p.ws.seq_lo[s];
+        hi = p.ws.seq_lo[s + 1];
+    }
+}
 
 // ---------------------------------------------------------------------------------------
 // plan: one workgroup of 1024 threads, block scans in tiles of 1024 sequences
@@ -190,6 +204,18 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const PrefillParams 
 // One load for the whole geometry (the chunk count is read alongside, independently).
 struct ChunkGeo { int s, t0, len, pos0, lo; };
 __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGeo& g) {
+    if (p.single) {                                   // chunk c of the only sequence
+        int lo, hi;
+        seq_bounds(p, 0, lo, hi);
+        const int t0 = lo + c * kChunk;
+        if (t0 >= hi) return false;
+        g.s = 0;
+        g.t0 = t0;
+        g.lo = lo;
+        g.len = min(kChunk, hi - t0);
+        g.pos0 = t0 - lo;
+        return true;
+    }
     const int nc = p.ws.chunk_off[p.n_seq];
     const int4 r = p.ws.chunk_rec[min(c, p.NC - 1)];
     if (c >= nc) return false;
@@ -1181,8 +1207,10 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     const int pair = (k / kStrips) * 8 + xcd;
     if (pair >= p.n_seq * L.h_v) return;
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
-    const int c_begin = p.ws.chunk_off[s], c_end = p.ws.chunk_off[s + 1];
-    const int seq_lo = p.ws.seq_lo[s], seq_hi = p.ws.seq_lo[s + 1];
+    int seq_lo, seq_hi;
+    seq_bounds(p, s, seq_lo, seq_hi);
+    const int c_begin = p.single ? 0 : p.ws.chunk_off[s];
+    const int c_end = p.single ? (seq_hi - seq_lo + kChunk - 1) / kChunk : p.ws.chunk_off[s + 1];
     if (c_begin >= c_end) return;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
@@ -1315,9 +1343,10 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     p.cu = cu_seqlens; p.x = x; p.conv_state = conv_state; p.a = a; p.b = b;
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
     p.n_seq = n_seq; p.T = total_T; p.NC = (int)NC;
+    p.single = n_seq == 1;
     if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
-    hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
+    if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
     const dim3 qgrid((unsigned)NC, (unsigned)cfg->h_k), vgrid((unsigned)(NC * cfg->h_v));
     switch (cfg->d_conv) {
         case 2:

@@ -221,3 +221,28 @@ def test_non_monotone_cu_seqlens_is_clamped_in_bounds():
     np.testing.assert_array_equal(cs, rcs)
     assert oracle.rel_err(s, rs) <= TOL_STATE_REL
     assert float(np.max(np.abs(o - ro))) <= TOL_O_ABS
+
+
+@pytest.mark.parametrize("cu,T", [([10, 70], 100), ([-5, 200], 100), ([50, 20], 100), ([30, 30], 40)])
+def test_single_sequence_bounds_are_clamped(cu, T):
+    # One sequence takes its bounds straight from cu (there is no plan pass for n_seq = 1),
+    # with the plan's clamping: lo = clamp(cu[0], 0, T), hi = max(clamp(cu[1], 0, T), lo).
+    # Tokens outside [lo, hi) are neither read into the state nor written to o.
+    cfg = bx.make_cfg(h_k=2, h_v=4)
+    seed = inputs.seed_for(4) + 11 + cu[0] + 7 * cu[1]
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, T)
+    st = inputs.initial_states(cfg, seed, 1)
+    cs, s, o, _ = gpu_prefill(cfg, cu, tok, p, st)
+    lo = min(max(cu[0], 0), T)
+    hi = max(min(max(cu[1], 0), T), lo)
+    assert np.isnan(o[:lo]).all() and np.isnan(o[hi:]).all()
+    if hi == lo:
+        np.testing.assert_array_equal(cs, st["conv_state"])
+        np.testing.assert_array_equal(s, st["state"].astype(s.dtype))
+        return
+    sub = {k: v[lo:hi] for k, v in tok.items()}
+    rcs, rs, ro = oracle_prefill(cfg, [0, hi - lo], sub, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    assert oracle.rel_err(s, rs) <= TOL_STATE_REL
+    assert float(np.max(np.abs(o[lo:hi] - ro))) <= TOL_O_ABS
