@@ -34,20 +34,22 @@ class GdnLayer:
         self.decode_ws = torch.zeros(ix_gdn_decode_workspace_size(c, n_slots), dtype=torch.uint8, device=self.device)
         self._ws = None
 
-    def decode(self, x, a, b, o=None, o_bf16=None, z=None, y=None, y_bf16=None, stream=None):
+    def decode(self, x, a, b, o=None, o_bf16=None, z=None, y=None, y_bf16=None, y_q8_1=None, stream=None):
         """One token for all n_slots sequences: x [n][C] bf16, a, b [n][h_v] bf16. With z
-        [n][h_v][d_v] bf16 the gated output norm is fused in and written to y and/or y_bf16."""
+        [n][h_v][d_v] bf16 the gated output norm is fused in and written to y, y_bf16 and/or
+        y_q8_1 (uint8, 36 bytes per 32 outputs: the activation format of ix_mmvq_q8_0)."""
         args = (self.cfg, self.n_slots, x, self.conv_state, self.conv_w, a, b, self.A_log, self.dt_bias, self.state,
                 o, o_bf16)
         if z is None:
             check("ix_gdn_decode", ix_gdn_decode(*args, self.decode_ws, stream))
         else:
-            g = out_gate(z, self.ssm_norm, self.norm_eps, y, y_bf16)
+            g = out_gate(z, self.ssm_norm, self.norm_eps, y, y_bf16, y_q8_1)
             check("ix_gdn_decode_gated", ix_gdn_decode_gated(*args, g, self.decode_ws, stream))
 
-    def prefill(self, cu_seqlens, x, a, b, o=None, o_bf16=None, z=None, y=None, y_bf16=None, stream=None):
+    def prefill(self, cu_seqlens, x, a, b, o=None, o_bf16=None, z=None, y=None, y_bf16=None, y_q8_1=None,
+                stream=None):
         """Packed prefill of n_slots sequences (cu_seqlens int32 [n+1] on the device); z, y,
-        y_bf16 as in decode, with [total_T] rows."""
+        y_bf16, y_q8_1 as in decode, with [total_T] rows."""
         total_T = x.shape[0]
         size = ix_gdn_prefill_workspace_size if z is None else ix_gdn_prefill_gated_workspace_size
         need = size(self.cfg, self.n_slots, total_T)
@@ -58,5 +60,5 @@ class GdnLayer:
         if z is None:
             check("ix_gdn_prefill", ix_gdn_prefill(*args, self._ws, self._ws.numel(), stream))
         else:
-            g = out_gate(z, self.ssm_norm, self.norm_eps, y, y_bf16)
+            g = out_gate(z, self.ssm_norm, self.norm_eps, y, y_bf16, y_q8_1)
             check("ix_gdn_prefill_gated", ix_gdn_prefill_gated(*args, g, self._ws, self._ws.numel(), stream))

@@ -121,7 +121,7 @@ def test_in_proj(kw, B, hidden):
 
 
 def test_in_proj_feeds_decode():
-    # The projection's pieces drive the gated decode directly.
+    # The projection's pieces drive the gated decode directly (through GdnLayer) ...
     torch = _torch()
     cfg = bx.make_cfg()
     B, hidden = 4, 256
@@ -136,6 +136,20 @@ def test_in_proj_feeds_decode():
     assert bx.ix_gdn_in_proj(cfg, B, hidden, dev(h), dev(w), x, z, a, b) == 0
     layer = bx.GdnLayer(B, cfg)
     yb = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
-    layer.decode(x, a, b, z=z, y_bf16=yb)
+    y = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
+    n_in = cfg.h_v * cfg.d_v
+    yq = torch.empty(B * n_in // 32 * 36, dtype=torch.uint8, device="cuda")
+    layer.decode(x, a, b, z=z, y=y, y_bf16=yb, y_q8_1=yq)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(yb.float()).all())
+    np.testing.assert_array_equal(host(yb), bf16.from_f32(host(y)))
+    # ... and its q8_1 output drives a Q8_0 out-projection (the quantiser's own bytes).
+    np.testing.assert_array_equal(host(yq), proj.q8_1_quantize(host(y).reshape(-1)))
+    n_out = 64
+    wd, wq = proj.q8_blocks(0x6D4E039A, 1, n_out, n_in // 32)
+    out = torch.empty(B, n_out, dtype=torch.float32, device="cuda")
+    assert bx.ix_mmvq_q8_0(dev(proj.pack_q8_0(wd, wq)), yq, out, n_in, n_out, B) == 0
+    torch.cuda.synchronize()
+    xd, _, xq = proj.q8_1_unpack(host(yq))
+    ref, sc = proj.q8_0_ref(wd, wq, xd.reshape(B, -1), xq.reshape(B, n_in // 32, 32))
+    assert float(np.max(np.abs(host(out).astype(np.float64) - ref) / sc)) <= 1e-5
