@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import baloon_amd as bx
-from oracle import bf16, proj
+from oracle import bf16, inputs, proj
 from oracle.inputs import Gen
 from tests.common import dev, host
 
@@ -135,6 +135,10 @@ def test_in_proj_feeds_decode():
     b = torch.empty(B, cfg.h_v, dtype=torch.bfloat16, device="cuda")
     assert bx.ix_gdn_in_proj(cfg, B, hidden, dev(h), dev(w), x, z, a, b) == 0
     layer = bx.GdnLayer(B, cfg)
+    lp = inputs.layer_params(cfg, 0x6D4E0398)                 # non-zero conv weights and gates
+    layer.conv_w.copy_(dev(lp["w"]).view(torch.bfloat16))
+    layer.A_log.copy_(dev(lp["A_log"]))
+    layer.dt_bias.copy_(dev(lp["dt_bias"]))
     yb = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
     y = torch.empty(B, cfg.h_v, cfg.d_v, dtype=torch.float32, device="cuda")
     n_in = cfg.h_v * cfg.d_v
@@ -151,5 +155,6 @@ def test_in_proj_feeds_decode():
     assert bx.ix_mmvq_q8_0(dev(proj.pack_q8_0(wd, wq)), yq, out, n_in, n_out, B) == 0
     torch.cuda.synchronize()
     xd, _, xq = proj.q8_1_unpack(host(yq))
+    assert (xd != 0).all()                                   # every block is a real one
     ref, sc = proj.q8_0_ref(wd, wq, xd.reshape(B, -1), xq.reshape(B, n_in // 32, 32))
     assert float(np.max(np.abs(host(out).astype(np.float64) - ref) / sc)) <= 1e-5
