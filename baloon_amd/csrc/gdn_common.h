@@ -171,21 +171,40 @@ __device__ __forceinline__ float wave_sum_sq(float v) {
 // The sum of squares is (sum over columns 0..63) + (sum over 64..127), each a wave_sum_sq,
 // so every kernel that holds the head in this form gets the same bits.
 // out_gate_apply takes the two partial sums already reduced.
+// The gate inputs of lane l's two columns (l and 64 + l), loaded ahead by a caller that
+// has them early.
+struct GateIn {
+    float nrm[2];
+    uint16_t z[2];
+};
+__device__ __forceinline__ GateIn gate_in(const OutGate& g, size_t row, int lane) {
+    GateIn in;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        in.nrm[q] = g.nrm[lane + q * (kD / 2)];
+        in.z[q] = g.z[row + lane + q * (kD / 2)];
+    }
+    return in;
+}
 __device__ __forceinline__ void out_gate_apply(const OutGate& g, size_t row, float lo, float hi, float ss_lo,
-                                               float ss_hi, int lane) {
+                                               float ss_hi, int lane, const GateIn& in) {
     const float ss = ss_lo + ss_hi;
     const float inv = 1.0f / sqrtf(ss * (1.0f / kD) + g.eps);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const int j = lane + q * (kD / 2);
-        const float y = (q ? hi : lo) * inv * g.nrm[j] * sigmoid_f(bf16_to_f32(g.z[row + j]));
+        const float y = (q ? hi : lo) * inv * in.nrm[q] * sigmoid_f(bf16_to_f32(in.z[q]));
         if (g.y) g.y[row + j] = y;
         if (g.y_bf16) g.y_bf16[row + j] = f32_to_bf16(y);
         if (g.y_q8_1) q81_store(y, lane, g.y_q8_1 + ((row + j) / 32) * kQ81Bytes);
     }
 }
+__device__ __forceinline__ void out_gate_head(const OutGate& g, size_t row, float lo, float hi, int lane,
+                                              const GateIn& in) {
+    out_gate_apply(g, row, lo, hi, wave_sum_sq(lo), wave_sum_sq(hi), lane, in);
+}
 __device__ __forceinline__ void out_gate_head(const OutGate& g, size_t row, float lo, float hi, int lane) {
-    out_gate_apply(g, row, lo, hi, wave_sum_sq(lo), wave_sum_sq(hi), lane);
+    out_gate_head(g, row, lo, hi, lane, gate_in(g, row, lane));
 }
 
 // ---------------------------------------------------------------------------------------

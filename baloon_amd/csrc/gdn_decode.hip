@@ -238,6 +238,9 @@ head_kernel(const DecodeParams p, const DecodeWs ws) {
     if (conv_thread) conv_pair_load<DC>(p, bseq, ch, cp);
     const size_t ab = (size_t)bseq * L.h_v + h;
     const uint16_t a_in = p.a[ab], b_in = p.b[ab];
+    const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
+    GateIn gin{};
+    if (w == 0) gin = gate_in(p.og, ob, lane);                     // the norm's inputs, loaded ahead
 
     v4f* tile = reinterpret_cast<v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
     const int j0 = 2 * kPairsPerWave * w + half;
@@ -275,7 +278,6 @@ head_kernel(const DecodeParams p, const DecodeWs ws) {
         for (int e = 0; e < 4; ++e) { kr[e] = kk[e] * inv_k; qr[e] = qq[e] * inv_q; }
     }
     const float g = gb_s[0], bt = gb_s[1];
-    const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
 #pragma unroll
     for (int u = 0; u < kPairsPerWave; ++u) {
         const int j = j0 + 2 * u;
@@ -284,7 +286,7 @@ head_kernel(const DecodeParams p, const DecodeWs ws) {
     }
     if (tid == 0) last_s = old == mapped_count(L, src) - 1;
     lds_barrier();
-    if (w == 0) out_gate_head(p.og, ob, o_s[lane], o_s[lane + kWave], lane);
+    if (w == 0) out_gate_head(p.og, ob, o_s[lane], o_s[lane + kWave], lane, gin);
     if (last_s) {
         if (tid < 128) hist_store<DC>(p, bseq, ch, nh);
         if (tid == 0) counters[(size_t)bseq * L.h_k + src] = 0;
