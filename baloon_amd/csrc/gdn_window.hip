@@ -410,6 +410,8 @@ void launch_window_mfma(const ix_gdn_cfg* cfg, int B, const WindowParams& p, hip
 // commit: grid (2 h_v, B)
 // ---------------------------------------------------------------------------------------
 __global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowParams p) {
+    __shared__ __align__(16) float k_s[kMaxWindow][kD], v_s[kMaxWindow][kHalf];
+    __shared__ float g_s[kMaxWindow], b_s[kMaxWindow];
     const Layer& L = p.L;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int half = lane >> 5, i4 = lane & 31;
@@ -418,24 +420,47 @@ __global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowPar
     const int n = min(max(p.accepted[bseq], 0), p.K);
     if (n == 0) return;                                      // nothing accepted: both states stay
     const int dm = L.dc - 1;
+    const size_t row0 = (size_t)bseq * p.K;
+
+    // Every load is issued before anything waits: this workgroup's share of the record of
+    // the n accepted tokens (key, the half tile's 64 values, gate, beta), the conv history
+    // inputs, then the state. Indices are clamped, so the loads are unconditional; only the
+    // stores are predicated.
+    v4f kq[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int e = min(tid + r * kThreads, n * (kD / 4) - 1), t = e / (kD / 4), c4 = e % (kD / 4);
+        kq[r] = *reinterpret_cast<const v4f*>(p.rec.k + ((row0 + t) * L.h_k + src) * kD + 4 * c4);
+    }
+    v4f vq;
+    {
+        const int e = min(tid, n * (kHalf / 4) - 1), t = e / (kHalf / 4), c4 = e % (kHalf / 4);
+        vq = *reinterpret_cast<const v4f*>(p.rec.v + ((row0 + t) * L.h_v + h) * kD + hf * kHalf + 4 * c4);
+    }
+    const int tg = min(tid, n - 1);
+    const float gq = p.rec.g[(row0 + tg) * L.h_v + h], bq = p.rec.bt[(row0 + tg) * L.h_v + h];
 
     // Conv history: the half tile's 64 v channels, and (one workgroup per q/k head) the 256
     // q and k channels. New history = the last dc-1 entries of (old history, x_0..x_{n-1}).
     const bool own_qk = hf == 0 && h == mapped_head(L, src, 0);
     const int nch = kHalf + (own_qk ? 2 * kD : 0);
-    for (int e = tid; e < nch; e += kThreads) {
+    uint16_t hnew[2][3];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int e = min(tid + r * kThreads, nch - 1);
         const int c = e < kHalf ? v_channel(L, h, hf * kHalf + e)
                                 : (e < kHalf + kD ? q_channel(L, src, e - kHalf) : k_channel(L, src, e - kHalf - kD));
-        uint16_t* hp = p.conv_state + ((size_t)bseq * L.C + c) * dm;
-        uint16_t old[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) old[i] = i < dm ? hp[i] : 0;
+        const uint16_t* hp = p.conv_state + ((size_t)bseq * L.C + c) * dm;
+        uint16_t old[3], xin[3];
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            if (i >= dm) break;
+            old[i] = hp[min(i, dm - 1)];
+            xin[i] = p.x[(row0 + min(max(n + i - dm, 0), p.K - 1)) * L.C + c];
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
             const int idx = n + i;                           // index into (old history, x_0, x_1, ...)
-            hp[i] = idx < dm ? (idx == 0 ? old[0] : idx == 1 ? old[1] : old[2])
-                             : p.x[((size_t)bseq * p.K + (idx - dm)) * L.C + c];
+            hnew[r][i] = idx < dm ? (idx == 0 ? old[0] : idx == 1 ? old[1] : old[2]) : xin[i];
         }
     }
 
@@ -444,18 +469,40 @@ __global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowPar
     v4f s[kPairs];
 #pragma unroll
     for (int u = 0; u < kPairs; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
+
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int e = tid + r * kThreads;
+        if (e < n * (kD / 4)) *reinterpret_cast<v4f*>(&k_s[e / (kD / 4)][4 * (e % (kD / 4))]) = kq[r];
+    }
+    if (tid < n * (kHalf / 4)) *reinterpret_cast<v4f*>(&v_s[tid / (kHalf / 4)][4 * (tid % (kHalf / 4))]) = vq;
+    if (tid < n) {
+        g_s[tid] = gq;
+        b_s[tid] = bq;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int e = tid + r * kThreads;
+        if (e >= nch) continue;
+        const int c = e < kHalf ? v_channel(L, h, hf * kHalf + e)
+                                : (e < kHalf + kD ? q_channel(L, src, e - kHalf) : k_channel(L, src, e - kHalf - kD));
+        uint16_t* hp = p.conv_state + ((size_t)bseq * L.C + c) * dm;
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+            if (i < dm) hp[i] = hnew[r][i];
+    }
+    lds_barrier();
+
     for (int t = 0; t < n; ++t) {
-        const size_t row = (size_t)bseq * p.K + t;
-        const v4f kr = *reinterpret_cast<const v4f*>(p.rec.k + (row * L.h_k + src) * kD + 4 * i4);
-        const float g = p.rec.g[row * L.h_v + h], bt = p.rec.bt[row * L.h_v + h];
-        const float* vr = p.rec.v + (row * L.h_v + h) * kD;
+        const v4f kr = *reinterpret_cast<const v4f*>(&k_s[t][4 * i4]);
+        const float g = g_s[t], bt = b_s[t];
 #pragma unroll
         for (int u = 0; u < kPairs; ++u) {
             float ak = s[u][0] * kr[0];
 #pragma unroll
             for (int e = 1; e < 4; ++e) ak = fmaf(s[u][e], kr[e], ak);
             ak = half_sum(ak);
-            const float d = (vr[j0 + 2 * u] - g * ak) * bt;
+            const float d = (v_s[t][j0 + 2 * u - hf * kHalf] - g * ak) * bt;
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[u][e] = fmaf(kr[e], d, s[u][e] * g);
         }
