@@ -605,9 +605,9 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
 // beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
 // compute the v rows | A and M (waves 0-3) | M fragments | the four 16 x 16 diagonal blocks
 // of T by substitution (wave 0), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj
-// in three dependency levels of fp32 MFMA block products | U = (T diag beta) V and
-// W = (T diag beta Gam) K, wave w taking columns 16 w .. +15 | U^T stored from the MFMA
-// layout, -W through LDS into fragments.
+// in three dependency levels of fp32 MFMA block products | U = (T diag beta) V, wave w
+// taking columns 16 w .. +15, U^T stored from the MFMA layout | W^T = K^T diag(beta Gam) T^T,
+// whose accumulators are the chain's -W fragments as they stand, stored from registers.
 template <int DC>
 __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p) {
     __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
@@ -615,9 +615,7 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
     float* M_s = A_s + kChunk * kTS;                                   // M, then T
     float* T_s = M_s;
-    float (*W_s)[kKS] = reinterpret_cast<float (*)[kKS]>(A_s);        // W, over A and T
     float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
-    static_assert(kChunk * kKS <= 2 * kChunk * kTS, "W fits over A and T");
     __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
 
     ChunkGeo g;
@@ -632,15 +630,6 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
     const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);
 
-    // K^T fragments of this wave's 16 columns (the B operand of W), issued first.
-    bf8 kt[2][2];
-    {
-        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int pl = 0; pl < 2; ++pl) kt[ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(w, ks, 2, pl, lane));
-    }
     v4 kk[3], qk[3];
     if (w < 4) {
         uint16_t ra = 0, rb = 0;
@@ -688,6 +677,20 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
             *reinterpret_cast<float2*>(&V_s[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
     }
     lds_barrier();
+    // K^T fragments of row tiles 2 (w & 3) and 2 (w & 3) + 1 (the A operand of W^T below),
+    // issued here so that they do not queue ahead of the raw products and the x rows.
+    const int kw = w & 3;
+    bf8 kt[2][2][2];
+    {
+        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl)
+                    kt[t][ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(2 * kw + t, ks, 2, pl, lane));
+    }
     if (w < 4) am_head(kk, qk, G_s, B_s, A_s, M_s, w, li, lg4);
     lds_barrier();
 
@@ -744,84 +747,99 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         lds_barrier();
     }
 
-    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32, one
-    // accumulator set live at a time): wave w takes columns 16 w .. +15, all four 16-row
-    // tiles. The k index (token s) runs in kperm order, the order of the K^T fragments that
-    // are W's B operand: lane (li, lg4) of k-step ks holds tokens 32 ks + 4 lg4 .. +3 (the
-    // 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block 2 ks + 1). T[t][s] = 0 for
-    // s > t: tile mt needs the k-steps up to mt / 2, and the blocks of T above the block
-    // diagonal (never written) are read as zeros.
+    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32): wave w
+    // takes columns 16 w .. +15, all four 16-row (token) tiles. The k index (token s) runs in
+    // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens
+    // 32 ks + 4 lg4 .. +3 (the 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block
+    // 2 ks + 1). T[t][s] = 0 for s > t: tile mt needs the k-steps up to mt / 2, and the blocks
+    // of T above the block diagonal (never written) are read as zeros.
     const int col = 16 * w + li;
-    auto t_gemm = [&](bool is_w, v4 (&acc)[4]) {
+    // Row tile mt of diag(sc) T^T... as an MFMA operand: lane (li, lg4) holds sc_s T[16 mt + li][s]
+    // at the tokens s of k-step ks (zero above the diagonal blocks), split.
+    auto t_frag = [&](const float* sc, int mt, int ks, bf8& h, bf8& l) {
+        const int s0 = 32 * ks + 4 * lg4;
+        const v4 sc0 = *reinterpret_cast<const v4*>(sc + s0), sc1 = *reinterpret_cast<const v4*>(sc + s0 + 16);
+        const float* tr = T_s + (16 * mt + li) * kTS + s0;
+        const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16);
+        const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
+        float av[8];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[mt] = v4{0.f, 0.f, 0.f, 0.f};
+        for (int e = 0; e < 4; ++e) {
+            av[e] = live0 ? t0[e] * sc0[e] : 0.0f;
+            av[e + 4] = live1 ? t1[e] * sc1[e] : 0.0f;
+        }
+        split8(av, h, l);
+    };
+    {
+        // U: T diag(beta) as the A operand, the wave's V columns as the B operand; the
+        // accumulator of tile mt holds U[16 mt + 4 lg4 + r][col], stored as U^T rows.
+        v4 uacc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) uacc[mt] = v4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int s0 = 32 * ks + 4 * lg4;
-            const v4 sc0 = *reinterpret_cast<const v4*>((is_w ? BG_s : B_s) + s0);
-            const v4 sc1 = *reinterpret_cast<const v4*>((is_w ? BG_s : B_s) + s0 + 16);
-            bf8 bh, bl;
-            if (is_w) {
-                bh = kt[ks][0];
-                bl = kt[ks][1];
-            } else {
-                float bv[8];
+            float bv[8];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    bv[e] = V_s[s0 + e][col];
-                    bv[e + 4] = V_s[s0 + 16 + e][col];
-                }
-                split8(bv, bh, bl);
+            for (int e = 0; e < 4; ++e) {
+                bv[e] = V_s[s0 + e][col];
+                bv[e + 4] = V_s[s0 + 16 + e][col];
             }
+            bf8 bh, bl;
+            split8(bv, bh, bl);
 #pragma unroll
             for (int mt = 2 * ks; mt < 4; ++mt) {
-                const float* tr = T_s + (16 * mt + li) * kTS + s0;
-                const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16);
-                const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
-                float av[8];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    av[e] = live0 ? t0[e] * sc0[e] : 0.0f;
-                    av[e + 4] = live1 ? t1[e] * sc1[e] : 0.0f;
-                }
                 bf8 ah, al;
-                split8(av, ah, al);
-                acc[mt] = mfma_bf16(ah, bh, acc[mt]);
-                acc[mt] = mfma_bf16(ah, bl, acc[mt]);
-                acc[mt] = mfma_bf16(al, bh, acc[mt]);
+                t_frag(B_s, mt, ks, ah, al);
+                uacc[mt] = mfma_bf16(ah, bh, uacc[mt]);
+                uacc[mt] = mfma_bf16(ah, bl, uacc[mt]);
+                uacc[mt] = mfma_bf16(al, bh, uacc[mt]);
             }
         }
-    };
-    {
-        v4 uacc[4];
-        t_gemm(false, uacc);
-        // U^T rows (column j of U: 4 consecutive tokens per lane and tile).
         float* Ut = p.ws.Ut + ch * kD * kChunk;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
             *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
     }
-    v4 wacc[4];
-    t_gemm(true, wacc);
-    lds_barrier();                         // A and T are read: W takes their place
+    {
+        // W^T = K^T diag(beta Gam) T^T, wave w taking W^T row tiles 2 kw, 2 kw + 1 (k-step kw of
+        // the chain's W fragments) for token tiles 2 (w >> 2), 2 (w >> 2) + 1: the K^T fragments
+        // as the A operand and diag(beta Gam) T^T as the B operand, so the accumulator of (row
+        // tile 2 kw + t, token tile mt) holds W[16 mt + li][32 kw + 16 t + 4 lg4 + r], r = 0..3:
+        // entries 4 t + r of lane (li, lg4) of the chain's fragment (mt, kw) of -W, which the
+        // wave then stores whole (negated, split) straight from the accumulators.
+        v4 wacc[2][2];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) W_s[16 * mt + 4 * lg4 + r][col] = wacc[mt][r];
-    lds_barrier();
-    // -W as fragments (4 x 4 x 64 = 1024 units, two per thread): negated, so the chain's
-    // D = U - W S accumulates from U.
-    uint16_t* Wf = p.ws.Wf + ch * kFragW;
+            for (int j = 0; j < 2; ++j) wacc[t][j] = v4{0.f, 0.f, 0.f, 0.f};
+        const int mt0 = 2 * (w >> 2);
 #pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-        const int u = tid + rep * kChunkThreads;
-        const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-        const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
-        float x[8];
-        const v4 a = *reinterpret_cast<const v4*>(&W_s[row][k0]), b = *reinterpret_cast<const v4*>(&W_s[row][k0 + 16]);
+        for (int ks = 0; ks < 2; ++ks) {
+            if (2 * ks > mt0 + 1) continue;                     // T is zero there (wave-uniform)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { x[e] = -a[e]; x[e + 4] = -b[e]; }
-        store_frag(Wf, m, ks, 4, ln, x);
+            for (int j = 0; j < 2; ++j) {
+                bf8 bh, bl;
+                t_frag(BG_s, mt0 + j, ks, bh, bl);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    wacc[t][j] = mfma_bf16(kt[t][ks][0], bh, wacc[t][j]);
+                    wacc[t][j] = mfma_bf16(kt[t][ks][0], bl, wacc[t][j]);
+                    wacc[t][j] = mfma_bf16(kt[t][ks][1], bh, wacc[t][j]);
+                }
+            }
+        }
+        uint16_t* Wf = p.ws.Wf + ch * kFragW;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float x[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                x[r] = -wacc[0][j][r];
+                x[4 + r] = -wacc[1][j][r];
+            }
+            store_frag(Wf, mt0 + j, kw, 4, lane, x);
+        }
     }
 }
 // ---------------------------------------------------------------------------------------
