@@ -66,7 +66,7 @@ struct Ws {
                          // inclusive cumulative log decay G (padded rows repeat the last)
     uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
-    v4* raw;             // [NC][h_k][4][3][2][64] raw K K^T, Q K^T triangle blocks (accumulator layout)
+    v4* raw;             // [NC][h_k][4][3][2][64] raw K K^T, (Q K^T)^T triangle blocks (accumulator layout)
 };
 constexpr int kWsSections = 10;
 
@@ -400,10 +400,14 @@ __device__ __forceinline__ float qk_f32(const uint8_t* planes, int t, int ch) {
            bf16_to_f32(*reinterpret_cast<const uint16_t*>(planes + kQKPlane + o));
 }
 
-// The 10 blocks of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes i = w, w+4, w+8.
+// The 10 blocks (br, bc) of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes
+// i = w, w+4, w+8. The order gives each wave whole 32-column halves of block rows: wave 0
+// (1,0) (1,1) (0,0), wave 1 (2,0) (2,1) (2,2), wave 2 (3,0) (3,1), wave 3 (3,2) (3,3), so
+// its first two blocks make one M fragment (block row br, k-step bc / 2), and waves 0, 1
+// also hold the diagonal block whose right neighbour is zero.
 __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
-    br = i < 1 ? 0 : i < 3 ? 1 : i < 6 ? 2 : 3;
-    bc = i - br * (br + 1) / 2;
+    br = (0x8f9f9 >> (2 * i)) & 3;                      // 1 2 3 3 1 2 3 3 0 2
+    bc = (0x8d580 >> (2 * i)) & 3;                      // 0 0 0 2 1 1 1 3 0 2
 }
 
 // C += X (16 x 16 at x, row stride xs) * Y (16 x 16 at y, row stride ys) on fp32 MFMA
@@ -421,29 +425,66 @@ __device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, f
 }
 
 // A and M of one v head from the raw products of this wave's triangle blocks (waves 0-3):
-// A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s) for s < t, M[t][s] = exp(G_t - G_s) (q_t . k_s)
-// for s <= t, zero above the diagonal inside the diagonal blocks. The blocks above the
-// diagonal are never written (nothing reads them). Branch-free; the decay uses the hardware
-// exp (relative error <= 4e-6 down to the fp32 underflow of exp(G_t - G_s)).
+// A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s) for s < t into LDS (the inverse's input), and
+// M[t][s] = exp(G_t - G_s) (q_t . k_s) for s <= t straight into the chain's M fragments.
+// The raw K K^T block (br, bc) holds (t = 16 br + 4 lg4 + r, s = 16 bc + li); the raw Q K^T
+// block arrives transposed, (s = 16 bc + 4 lg4 + r, t = 16 br + li), which is the fragment
+// layout: entries 4 (bc & 1) + r of lane (li, lg4) of fragment (br, bc / 2). The blocks above
+// the diagonal of A are never written (nothing reads them); M's are written as zeros.
+// Branch-free; the decay uses the hardware exp (relative error <= 4e-6 down to the fp32
+// underflow of exp(G_t - G_s)).
 __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], const float* G, const float* Bt,
-                                        float* A_s, float* M_s, int w, int li, int lg4) {
+                                        float* A_s, uint16_t* Mf, int w, int lane) {
+    const int li = lane & 15, lg4 = lane >> 4;
+    float mv[3][4];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         const int i = w + 4 * j;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mv[j][r] = 0.0f;
         if (i >= 10) continue;
         int br, bc;
         tri_block(i, br, bc);
-        const int t0 = 16 * br + 4 * lg4, s = 16 * bc + li;
-        const v4 gt = *reinterpret_cast<const v4*>(G + t0), bt = *reinterpret_cast<const v4*>(Bt + t0);
-        const float gs = G[s];
+        {
+            const int t0 = 16 * br + 4 * lg4, s = 16 * bc + li;
+            const v4 gt = *reinterpret_cast<const v4*>(G + t0), bt = *reinterpret_cast<const v4*>(Bt + t0);
+            const float gs = G[s];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t0 + r;
-            const float e = __expf(fminf(gt[r] - gs, 0.0f));    // used for s <= t only
-            M_s[t * kTS + s] = s <= t ? e * qk[j][r] : 0.0f;
-            A_s[t * kTS + s] = s < t ? bt[r] * e * kk[j][r] : 0.0f;
+            for (int r = 0; r < 4; ++r) {
+                const int t = t0 + r;
+                const float e = __expf(fminf(gt[r] - gs, 0.0f));    // used for s < t only
+                A_s[t * kTS + s] = s < t ? bt[r] * e * kk[j][r] : 0.0f;
+            }
+        }
+        {
+            const int s0 = 16 * bc + 4 * lg4, t = 16 * br + li;
+            const v4 gs = *reinterpret_cast<const v4*>(G + s0);
+            const float gt = G[t];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __expf(fminf(gt - gs[r], 0.0f));    // used for s <= t only
+                mv[j][r] = s0 + r <= t ? e * qk[j][r] : 0.0f;
+            }
         }
     }
+    // Blocks 0 and 1 of every wave: fragment (br, bc / 2) of the first. Block 2 of waves 0 and
+    // 1 (a diagonal block, right neighbour zero); waves 2 and 3 write the zero fragments of
+    // block rows 0 and 1 at k-step 1.
+    int br, bc;
+    tri_block(w, br, bc);
+    float x[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { x[r] = mv[0][r]; x[4 + r] = mv[1][r]; }
+    store_frag(Mf, br, bc >> 1, 2, lane, x);
+    if (w < 2) {
+        tri_block(w + 8, br, bc);
+    } else {
+        br = w - 2;
+        bc = 2;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { x[r] = mv[2][r]; x[4 + r] = 0.0f; }
+    store_frag(Mf, br, bc >> 1, 2, lane, x);
 }
 
 // The chunk-local work runs as two kernels, so that each holds a fraction of the registers and
@@ -488,7 +529,8 @@ __device__ __forceinline__ void v_unit(const Layer& L, int NC, int id, int& c, i
 }
 
 // Raw triangle products: per (chunk, q/k head), wave w (0..3) of the triangle and its block
-// slot j (0..2, block i = w + 4 j), the K K^T then the Q K^T accumulator, one 16-byte v4 per
+// slot j (0..2, block i = w + 4 j), the K K^T then the transposed Q K^T accumulator (K of
+// block bc times Q of block br, so that it lands in M's fragment layout), one 16-byte v4 per
 // lane: [NC][h_k][4][3][2][64] v4.
 __device__ __forceinline__ size_t raw_at(size_t cs, int w, int j, int kind, int lane) {
     return ((((cs * 4 + w) * 3 + j) * 2 + kind) * kWave + lane);
@@ -540,9 +582,11 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
     lds_barrier();
 
     if (w < 4) {
-        // Raw K K^T and Q K^T of this wave's triangle blocks (16x16x32 split-bf16 MFMA,
+        // Raw K K^T and (Q K^T)^T of this wave's triangle blocks (16x16x32 split-bf16 MFMA,
         // operands straight from the planes: lane (li, lg4) supplies channels
-        // 32 ks + 8 lg4 .. +7 of token row li for both operands), then stored.
+        // 32 ks + 8 lg4 .. +7 of token row li for both operands), then stored. The A and B
+        // register layouts are mirror images, so swapping the operands of Q K^T gives its
+        // transpose.
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int i = w + 4 * j;
@@ -561,11 +605,11 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
                 const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
                 const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
                 kk = mfma_bf16(akh, bkh, kk);
-                qk = mfma_bf16(aqh, bkh, qk);
+                qk = mfma_bf16(bkh, aqh, qk);
                 kk = mfma_bf16(akh, bkl, kk);
-                qk = mfma_bf16(aqh, bkl, qk);
+                qk = mfma_bf16(bkl, aqh, qk);
                 kk = mfma_bf16(akl, bkh, kk);
-                qk = mfma_bf16(aql, bkh, qk);
+                qk = mfma_bf16(bkh, aql, qk);
             }
             p.ws.raw[raw_at(cs, w, j, 0, lane)] = kk;
             p.ws.raw[raw_at(cs, w, j, 1, lane)] = qk;
@@ -613,9 +657,8 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
     float (*V_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);        // v rows
     float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
-    float* M_s = A_s + kChunk * kTS;                                   // M, then T
-    float* T_s = M_s;
-    float* P_s = M_s + kChunk * kTS;                                   // [3][16][17]
+    float* T_s = A_s + kChunk * kTS;                                   // [64][kTS]
+    float* P_s = T_s + kChunk * kTS;                                   // [3][16][17]
     __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
 
     ChunkGeo g;
@@ -691,25 +734,8 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
                 for (int pl = 0; pl < 2; ++pl)
                     kt[t][ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(2 * kw + t, ks, 2, pl, lane));
     }
-    if (w < 4) am_head(kk, qk, G_s, B_s, A_s, M_s, w, li, lg4);
+    if (w < 4) am_head(kk, qk, G_s, B_s, A_s, p.ws.Mf + ch * kFragM, w, lane);
     lds_barrier();
-
-    // M as fragments (4 x 2 fragments x 64 lanes: one unit per thread); the blocks above
-    // the diagonal are zero.
-    {
-        uint16_t* Mf = p.ws.Mf + ch * kFragM;
-        const int m = w >> 1, ks = w & 1;
-        const int row = 16 * m + li, k0 = 32 * ks + 4 * lg4;            // kperm halves
-        float x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int hb = 0; hb < 2; ++hb) {                              // 16-column block 2 ks + hb
-            if (2 * ks + hb > m) continue;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) x[4 * hb + e] = M_s[row * kTS + k0 + 16 * hb + e];
-        }
-        store_frag(Mf, m, ks, 2, lane, x);
-    }
-    lds_barrier();                         // M_s is read: T takes its place
 
     // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane = 16 b +
     // column c).
