@@ -360,19 +360,6 @@ __device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nk
     *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 1, lane)) = lo;
 }
 
-// A fragment whose planes are already split (hi and lo bf16 bit patterns).
-__device__ __forceinline__ void store_frag_planes(uint16_t* base, int m, int ks, int nks, int lane,
-                                                  const uint16_t (&h)[8], const uint16_t (&l)[8]) {
-    u4x hv, lv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        hv[i] = (uint32_t)h[2 * i] | ((uint32_t)h[2 * i + 1] << 16);
-        lv[i] = (uint32_t)l[2 * i] | ((uint32_t)l[2 * i + 1] << 16);
-    }
-    *reinterpret_cast<u4x*>(base + frag_at(m, ks, nks, 0, lane)) = hv;
-    *reinterpret_cast<u4x*>(base + frag_at(m, ks, nks, 1, lane)) = lv;
-}
-
 // Fragment sizes in bf16 elements: (rows/16) x (k/32) fragments x 2 planes x 512.
 constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (W, Q)
 constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (M)
@@ -393,6 +380,13 @@ constexpr int kChunkThreads = 512;
 constexpr int kQKPlane = kChunk * 256;                   // bytes per plane
 __device__ __forceinline__ int qk_off(int t, int ch) {
     return t * 256 + ((((ch >> 3) ^ (t & 15))) << 4) + ((ch & 7) << 1);
+}
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef short v4s __attribute__((ext_vector_type(4)));
+// Transposing 8-byte LDS read of 16-bit elements (gfx950 ds_read_b64_tr_b16).
+__device__ __forceinline__ uint2 lds_tr16(const lds_u8* a) {
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)a));
 }
 __device__ __forceinline__ float qk_f32(const uint8_t* planes, int t, int ch) {
     const int o = qk_off(t, ch);
@@ -619,17 +613,22 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
         // from the planes into split fragments, k in accumulator row order (kperm).
         const int t4 = tid - 4 * kWave;
         uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
-        for (int u = t4; u < 8 * 2 * kWave; u += 4 * kWave) {
-            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 1, ks = f & 1;
-            const int row = 16 * m + (ln & 15);
-            uint16_t xh[8], xl[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int o = qk_off(32 * ks + kperm(ln >> 4, e), row);
-                xh[e] = *reinterpret_cast<const uint16_t*>(Kp + o);
-                xl[e] = *reinterpret_cast<const uint16_t*>(Kp + kQKPlane + o);
-            }
-            store_frag_planes(Ktf, m, ks, 2, ln, xh, xl);
+        // K^T with the transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group,
+        // lane j receives element j & 3 of the 8-byte reads of lanes (j >> 2) + 4 e, e = 0..3.
+        // Lane i of lane group g reads channels 16 m + 4 (i & 3) .. +3 of token
+        // 32 ks + 4 g + (i >> 2) (then of the token 16 later), so it receives channel 16 m + i
+        // at tokens 32 ks + 4 g + e (+ 16): entries e (4 + e) of its kperm fragment chunk.
+        // Each wave takes whole fragments (m, ks), f = 2 m + ks = w - 4, w, w + 4, w + 8.
+        const int ip = lane & 15, lgr = lane >> 4;
+        const lds_u8* K3 = (const lds_u8*)Kp;
+        for (int f = w - 4; f < 8 * 2; f += 4) {
+            const int m = f >> 1, ks = f & 1;
+            const int t0 = 32 * ks + 4 * lgr + (ip >> 2), c0 = 16 * m + 4 * (ip & 3);
+            const int oa = qk_off(t0, c0), ob = qk_off(t0 + 16, c0);
+            const uint2 ha = lds_tr16(K3 + oa), hb = lds_tr16(K3 + ob);
+            const uint2 la = lds_tr16(K3 + kQKPlane + oa), lb = lds_tr16(K3 + kQKPlane + ob);
+            *reinterpret_cast<u4x*>(Ktf + frag_at(m, ks, 2, 0, lane)) = u4x{ha.x, ha.y, hb.x, hb.y};
+            *reinterpret_cast<u4x*>(Ktf + frag_at(m, ks, 2, 1, lane)) = u4x{la.x, la.y, lb.x, lb.y};
         }
         uint16_t* Qf = p.ws.Qf + cs * kFragW;
         for (int u = t4; u < 4 * 4 * kWave; u += 4 * kWave) {
@@ -905,8 +904,6 @@ constexpr int kChainLds = 4 * kOpsBytes + 2 * kHandBytes + kChainSink;   // 156,
 constexpr int kWarmAhead = 2;                           // chunks warmed ahead of their copy
 constexpr int kWarmLoadsW = 9;                          // warm-up loads per chunk: W-copy wave
 constexpr int kWarmLoadsK = 10;                         //                          K^T-copy wave
-
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 
 __device__ __forceinline__ bf8 lds_frag(const uint8_t* lds, int off, int lane) {
     return *reinterpret_cast<const bf8*>(lds + off + lane * 16);
