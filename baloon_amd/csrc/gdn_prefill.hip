@@ -418,6 +418,28 @@ __device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, f
     for (int r = 0; r < 4; ++r) z[(4 * (lane >> 4) + r) * zs + (lane & 15)] = scale * c[r];
 }
 
+// 16x16x16 bf16 MFMA operands: A lane l holds A[l%16][4 (l/16) + e], B lane l holds
+// B[4 (l/16) + e][l%16], e = 0..3, and the accumulator's lane l holds C[4 (l/16) + r][l%16],
+// so an accumulator split to bf16 is the next product's B operand as it stands.
+typedef short bf4 __attribute__((ext_vector_type(4)));
+struct Split4 { bf4 h, l; };
+__device__ __forceinline__ Split4 split4(const v4& x) {
+    uint32_t h0, l0, h1, l1;
+    split2(x[0], x[1], h0, l0);
+    split2(x[2], x[3], h1, l1);
+    return Split4{__builtin_bit_cast(bf4, uint2{h0, h1}), __builtin_bit_cast(bf4, uint2{l0, l1})};
+}
+// c += A B on split operands (hi hi + hi lo + lo hi).
+__device__ __forceinline__ v4 mfma16_split(const Split4& a, const Split4& b, v4 c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.h, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.h, b.l, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.l, b.h, c, 0, 0, 0);
+}
+// A operand of the 16 x 16 block at (r0, c0) of an LDS matrix with row stride kTS, times s.
+__device__ __forceinline__ Split4 block_a(const float* m, int r0, int c0, int lane, float s) {
+    return split4(s * *reinterpret_cast<const v4*>(m + (r0 + (lane & 15)) * kTS + c0 + 4 * (lane >> 4)));
+}
+
 // A and M of one v head from the raw products of this wave's triangle blocks (waves 0-3):
 // A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s) for s < t into LDS (the inverse's input), and
 // M[t][s] = exp(G_t - G_s) (q_t . k_s) for s <= t straight into the chain's M fragments.
@@ -648,9 +670,10 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
 // beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
 // compute the v rows | A and M (waves 0-3) | M fragments | the four 16 x 16 diagonal blocks
 // of T by substitution (wave 0), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj
-// in three dependency levels of fp32 MFMA block products | U = (T diag beta) V, wave w
-// taking columns 16 w .. +15, U^T stored from the MFMA layout | W^T = K^T diag(beta Gam) T^T,
-// whose accumulators are the chain's -W fragments as they stand, stored from registers.
+// in three dependency levels of fp32 MFMA block products (waves 0-2), while waves 4-7 solve
+// (I + A) U = diag(beta) V by block forward substitution with the diagonal blocks, U^T
+// stored from the MFMA layout | W^T = K^T diag(beta Gam) T^T, whose accumulators are the
+// chain's -W fragments as they stand, stored from registers.
 template <int DC>
 __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p) {
     __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
@@ -756,8 +779,40 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     lds_barrier();
     // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
     // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
+    // Meanwhile waves 4-7 solve (I + A) U = diag(beta) V by block forward substitution, which
+    // needs only A and the diagonal blocks T_ii: U_i = T_ii (beta_i V_i - sum_{k<i} A_ik U_k),
+    // wave 4 + wu taking columns 32 wu .. 32 wu + 31 (two 16-column tiles); token block 0
+    // and 1 at level 1, 2 at level 2, 3 at level 3, each stored as U^T rows when done.
+    Split4 us[4][2];                         // U_k split, token block k, column tile
+    auto u_block = [&](int i) {
+        const int wu = w - 4;
+        float* Ut = p.ws.Ut + ch * kD * kChunk;
+        Split4 aik[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (k < i) aik[k] = block_a(A_s, 16 * i, 16 * k, lane, -1.0f);
+        const Split4 tii = block_a(T_s, 16 * i, 16 * i, lane, 1.0f);
+        const v4 bt = *reinterpret_cast<const v4*>(B_s + 16 * i + 4 * lg4);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int col = 32 * wu + 16 * c + li;
+            v4 y;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) y[r] = bt[r] * V_s[16 * i + 4 * lg4 + r][col];
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (k < i) y = mfma16_split(aik[k], us[k][c], y);
+            const v4 x = mfma16_split(tii, split4(y), v4{0.f, 0.f, 0.f, 0.f});
+            us[i][c] = split4(x);
+            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * i + 4 * lg4) = x;
+        }
+    };
 #pragma unroll
     for (int lev = 1; lev <= 3; ++lev) {
+        if (w >= 4) {
+            if (lev == 1) u_block(0);
+            u_block(lev);
+        }
         if (w < 4 - lev) {
             const int j = w, i = w + lev;
             v4 pc = {0.f, 0.f, 0.f, 0.f};
@@ -772,14 +827,12 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         lds_barrier();
     }
 
-    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32): wave w
-    // takes columns 16 w .. +15, all four 16-row (token) tiles. The k index (token s) runs in
+    // W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32). The k index (token s) runs in
     // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens
     // 32 ks + 4 lg4 .. +3 (the 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block
     // 2 ks + 1). T[t][s] = 0 for s > t: tile mt needs the k-steps up to mt / 2, and the blocks
     // of T above the block diagonal (never written) are read as zeros.
-    const int col = 16 * w + li;
-    // Row tile mt of diag(sc) T^T... as an MFMA operand: lane (li, lg4) holds sc_s T[16 mt + li][s]
+    // Row tile mt of diag(sc) T^T as an MFMA operand: lane (li, lg4) holds sc_s T[16 mt + li][s]
     // at the tokens s of k-step ks (zero above the diagonal blocks), split.
     auto t_frag = [&](const float* sc, int mt, int ks, bf8& h, bf8& l) {
         const int s0 = 32 * ks + 4 * lg4;
@@ -795,37 +848,6 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         }
         split8(av, h, l);
     };
-    {
-        // U: T diag(beta) as the A operand, the wave's V columns as the B operand; the
-        // accumulator of tile mt holds U[16 mt + 4 lg4 + r][col], stored as U^T rows.
-        v4 uacc[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) uacc[mt] = v4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int s0 = 32 * ks + 4 * lg4;
-            float bv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                bv[e] = V_s[s0 + e][col];
-                bv[e + 4] = V_s[s0 + 16 + e][col];
-            }
-            bf8 bh, bl;
-            split8(bv, bh, bl);
-#pragma unroll
-            for (int mt = 2 * ks; mt < 4; ++mt) {
-                bf8 ah, al;
-                t_frag(B_s, mt, ks, ah, al);
-                uacc[mt] = mfma_bf16(ah, bh, uacc[mt]);
-                uacc[mt] = mfma_bf16(ah, bl, uacc[mt]);
-                uacc[mt] = mfma_bf16(al, bh, uacc[mt]);
-            }
-        }
-        float* Ut = p.ws.Ut + ch * kD * kChunk;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
-    }
     {
         // W^T = K^T diag(beta Gam) T^T, wave w taking W^T row tiles 2 kw, 2 kw + 1 (k-step kw of
         // the chain's W fragments) for token tiles 2 (w >> 2), 2 (w >> 2) + 1: the K^T fragments
