@@ -27,8 +27,9 @@
 //                  all the v heads mapped to the q/k head, stored raw; K^T and Q written as
 //                  split-bf16 MFMA fragments
 //   v_kernel       per (chunk, v head): decay factors and beta, v rows, A and M from the raw
-//                  products, T = (I + A)^-1 by a blocked inverse (fp32 MFMA block products),
-//                  U = T diag(beta) V and W = T diag(beta Gam) K; the chain's operands W
+//                  products, T = (I + A)^-1 (diagonal blocks by substitution, the rest by
+//                  block forward substitution), U = T diag(beta) V by block forward
+//                  substitution and W = T diag(beta Gam) K; the chain's operands W
 //                  (negated, so the chain's D accumulates from U) and M as split-bf16
 //                  fragments, U^T in fp32
 //   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
@@ -37,9 +38,9 @@
 //                  two waves copy the next chunk's W and the current chunk's K^T into LDS
 //                  with direct loads and warm L2 ahead; before the first chunk the K^T
 //                  wave writes the new rolling conv history of the pair's share of channels.
-// Every dense product except the inverse's block products runs on split-bf16 MFMA (three
-// bf16 products per fp32 product, ~2^-16 relative error); the chunked result stays within
-// ~1e-5 (state) of the token-by-token recurrence in double.
+// Every dense product runs on split-bf16 MFMA (three bf16 products per fp32 product, ~2^-16
+// relative error); only the 16 x 16 diagonal blocks of T are inverted in fp32 arithmetic.
+// The chunked result stays within ~1e-5 (state) of the token-by-token recurrence in double.
 #include "gdn_common.h"
 
 namespace ixg {
@@ -47,10 +48,6 @@ namespace {
 
 constexpr int kChunk = 64;
 constexpr int kPlanThreads = 1024;
-
-__device__ __forceinline__ v4 mfma4(float a, float b, v4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // ---------------------------------------------------------------------------------------
 // Workspace layout (host and device agree through this struct)
@@ -404,20 +401,6 @@ __device__ __forceinline__ void tri_block(int i, int& br, int& bc) {
     bc = (0x8d580 >> (2 * i)) & 3;                      // 0 0 0 2 1 1 1 3 0 2
 }
 
-// C += X (16 x 16 at x, row stride xs) * Y (16 x 16 at y, row stride ys) on fp32 MFMA
-// (four 16x16x4 steps). Lane l supplies X[l%16][4k + l/16] and Y[4k + l/16][l%16]; C is in
-// the MFMA layout (c[r] = C[4 (l/16) + r][l%16]).
-__device__ __forceinline__ v4 mm16(const float* x, int xs, const float* y, int ys, v4 c, int lane) {
-    const int r16 = lane & 15, k4 = lane >> 4;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) c = mfma4(x[r16 * xs + 4 * k + k4], y[(4 * k + k4) * ys + r16], c);
-    return c;
-}
-__device__ __forceinline__ void put16(float* z, int zs, const v4& c, int lane, float scale) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) z[(4 * (lane >> 4) + r) * zs + (lane & 15)] = scale * c[r];
-}
-
 // 16x16x16 bf16 MFMA operands: A lane l holds A[l%16][4 (l/16) + e], B lane l holds
 // B[4 (l/16) + e][l%16], e = 0..3, and the accumulator's lane l holds C[4 (l/16) + r][l%16],
 // so an accumulator split to bf16 is the next product's B operand as it stands.
@@ -438,6 +421,32 @@ __device__ __forceinline__ v4 mfma16_split(const Split4& a, const Split4& b, v4 
 // A operand of the 16 x 16 block at (r0, c0) of an LDS matrix with row stride kTS, times s.
 __device__ __forceinline__ Split4 block_a(const float* m, int r0, int c0, int lane, float s) {
     return split4(s * *reinterpret_cast<const v4*>(m + (r0 + (lane & 15)) * kTS + c0 + 4 * (lane >> 4)));
+}
+
+// Column block J of T = (I + A)^-1 below the diagonal, by forward substitution on the
+// identity's block column: T_kj = -T_kk sum_{m=J}^{k-1} A_km T_mj, k = J+1..3, from the
+// diagonal blocks T_kk already in T_s. Each block is chained to the next product in
+// registers (its accumulator, split, is the B operand) and stored to T_s when done.
+template <int J>
+__device__ __forceinline__ void t_column(const float* A_s, float* T_s, int lane) {
+    const int li = lane & 15, lg4 = lane >> 4;
+    Split4 xs[4];
+    {
+        v4 tj;                                            // T_JJ as a B operand
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tj[e] = T_s[(16 * J + 4 * lg4 + e) * kTS + 16 * J + li];
+        xs[J] = split4(tj);
+    }
+#pragma unroll
+    for (int k = J + 1; k < 4; ++k) {
+        v4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int m = J; m < k; ++m) acc = mfma16_split(block_a(A_s, 16 * k, 16 * m, lane, -1.0f), xs[m], acc);
+        const v4 x = mfma16_split(block_a(T_s, 16 * k, 16 * k, lane, 1.0f), split4(acc), v4{0.f, 0.f, 0.f, 0.f});
+        xs[k] = split4(x);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) T_s[(16 * k + 4 * lg4 + r) * kTS + 16 * J + li] = x[r];
+    }
 }
 
 // A and M of one v head from the raw products of this wave's triangle blocks (waves 0-3):
@@ -668,19 +677,18 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
 
 // v_kernel: grid (NC, h_v), 512 threads; workgroup = (chunk, v head). Phases: decay scan and
 // beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
-// compute the v rows | A and M (waves 0-3) | M fragments | the four 16 x 16 diagonal blocks
-// of T by substitution (wave 0), then the off-diagonal blocks T_ij = -T_ii sum_k A_ik T_kj
-// in three dependency levels of fp32 MFMA block products (waves 0-2), while waves 4-7 solve
-// (I + A) U = diag(beta) V by block forward substitution with the diagonal blocks, U^T
-// stored from the MFMA layout | W^T = K^T diag(beta Gam) T^T, whose accumulators are the
-// chain's -W fragments as they stand, stored from registers.
+// compute the v rows | A (to LDS) and M (to its fragments) (waves 0-3) | the four 16 x 16
+// diagonal blocks of T by substitution (wave 0) | the blocks of T below them
+// by forward substitution on the identity's block columns (waves 0-2), while waves 4-7
+// solve (I + A) U = diag(beta) V the same way, U^T stored from the MFMA layout |
+// W^T = K^T diag(beta Gam) T^T, whose accumulators are the chain's -W fragments as they
+// stand, stored from registers.
 template <int DC>
 __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS + 3 * 16 * 17];
+    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS];
     float (*V_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);        // v rows
     float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
     float* T_s = A_s + kChunk * kTS;                                   // [64][kTS]
-    float* P_s = T_s + kChunk * kTS;                                   // [3][16][17]
     __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
 
     ChunkGeo g;
@@ -777,55 +785,42 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
     }
     lds_barrier();
-    // Off-diagonal blocks: level 1 (1,0) (2,1) (3,2); level 2 (2,0) (3,1); level 3 (3,0).
-    // T_ij = -T_ii P with P = sum_{k=j}^{i-1} A_ik T_kj (P through the wave's LDS scratch).
-    // Meanwhile waves 4-7 solve (I + A) U = diag(beta) V by block forward substitution, which
-    // needs only A and the diagonal blocks T_ii: U_i = T_ii (beta_i V_i - sum_{k<i} A_ik U_k),
-    // wave 4 + wu taking columns 32 wu .. 32 wu + 31 (two 16-column tiles); token block 0
-    // and 1 at level 1, 2 at level 2, 3 at level 3, each stored as U^T rows when done.
-    Split4 us[4][2];                         // U_k split, token block k, column tile
-    auto u_block = [&](int i) {
+    // T below the diagonal blocks: wave j (0..2) runs column block j by forward substitution
+    // (t_column). Meanwhile waves 4-7 solve (I + A) U = diag(beta) V the same way, which
+    // needs only A and the diagonal blocks: U_i = T_ii (beta_i V_i - sum_{k<i} A_ik U_k),
+    // wave 4 + wu taking columns 32 wu .. 32 wu + 31 (two 16-column tiles), each block's U^T
+    // rows stored when done. Split-bf16 products on the 16x16x16 MFMA throughout.
+    if (w == 0) t_column<0>(A_s, T_s, lane);
+    else if (w == 1) t_column<1>(A_s, T_s, lane);
+    else if (w == 2) t_column<2>(A_s, T_s, lane);
+    else if (w >= 4) {
         const int wu = w - 4;
         float* Ut = p.ws.Ut + ch * kD * kChunk;
-        Split4 aik[3];
+        Split4 us[4][2];                                  // U_k split, token block k, column tile
 #pragma unroll
-        for (int k = 0; k < 3; ++k)
-            if (k < i) aik[k] = block_a(A_s, 16 * i, 16 * k, lane, -1.0f);
-        const Split4 tii = block_a(T_s, 16 * i, 16 * i, lane, 1.0f);
-        const v4 bt = *reinterpret_cast<const v4*>(B_s + 16 * i + 4 * lg4);
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const int col = 32 * wu + 16 * c + li;
-            v4 y;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) y[r] = bt[r] * V_s[16 * i + 4 * lg4 + r][col];
+        for (int i = 0; i < 4; ++i) {
+            Split4 aik[3];
 #pragma unroll
             for (int k = 0; k < 3; ++k)
-                if (k < i) y = mfma16_split(aik[k], us[k][c], y);
-            const v4 x = mfma16_split(tii, split4(y), v4{0.f, 0.f, 0.f, 0.f});
-            us[i][c] = split4(x);
-            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * i + 4 * lg4) = x;
-        }
-    };
+                if (k < i) aik[k] = block_a(A_s, 16 * i, 16 * k, lane, -1.0f);
+            const Split4 tii = block_a(T_s, 16 * i, 16 * i, lane, 1.0f);
+            const v4 bt = *reinterpret_cast<const v4*>(B_s + 16 * i + 4 * lg4);
 #pragma unroll
-    for (int lev = 1; lev <= 3; ++lev) {
-        if (w >= 4) {
-            if (lev == 1) u_block(0);
-            u_block(lev);
+            for (int c = 0; c < 2; ++c) {
+                const int col = 32 * wu + 16 * c + li;
+                v4 y;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) y[r] = bt[r] * V_s[16 * i + 4 * lg4 + r][col];
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+                    if (k < i) y = mfma16_split(aik[k], us[k][c], y);
+                const v4 x = mfma16_split(tii, split4(y), v4{0.f, 0.f, 0.f, 0.f});
+                us[i][c] = split4(x);
+                *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * i + 4 * lg4) = x;
+            }
         }
-        if (w < 4 - lev) {
-            const int j = w, i = w + lev;
-            v4 pc = {0.f, 0.f, 0.f, 0.f};
-            for (int k = j; k < i; ++k)
-                pc = mm16(A_s + (16 * i) * kTS + 16 * k, kTS, T_s + (16 * k) * kTS + 16 * j, kTS, pc, lane);
-            float* Pw = P_s + w * 16 * 17;
-            put16(Pw, 17, pc, lane, 1.0f);
-            __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): this wave's P stores done
-            const v4 tc = mm16(T_s + (16 * i) * kTS + 16 * i, kTS, Pw, 17, v4{0.f, 0.f, 0.f, 0.f}, lane);
-            put16(T_s + (16 * i) * kTS + 16 * j, kTS, tc, lane, -1.0f);
-        }
-        lds_barrier();
     }
+    lds_barrier();
 
     // W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32). The k index (token s) runs in
     // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens

@@ -128,6 +128,32 @@ def test_extreme_gates(frac):
     np.testing.assert_array_equal(ob, bf16.from_f32(o))
 
 
+@pytest.mark.parametrize("beta_logit", [None, 30.0])
+def test_no_decay(beta_logit):
+    # Every gate logit at -30: softplus(a + dt_bias) ~ 1e-13, so the decay is 1 to fp32
+    # precision and A = beta (k_t . k_s) keeps its full weight across the whole chunk; the
+    # blocks of T = (I + A)^-1 below the diagonal are then as large as they get (with
+    # beta = 1 too in the second case). Several chunks, two sequences.
+    cfg = oracle.make_cfg()
+    seed = inputs.seed_for(3) + 41
+    cu = np.asarray([0, 200, 333], np.int32)
+    p = inputs.layer_params(cfg, seed)
+    tok = dict(inputs.token_inputs(cfg, seed, 333))
+    tok["a"] = bf16.from_f32(np.full(tok["a"].shape, -30.0, np.float32))
+    if beta_logit is not None:
+        tok["b"] = bf16.from_f32(np.full(tok["b"].shape, beta_logit, np.float32))
+    st = inputs.initial_states(cfg, seed, 2)
+    cs, s, o, ob = gpu_prefill(cfg, cu, tok, p, st)
+    rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    rel = oracle.rel_err(s, rs)
+    assert rel <= TOL_STATE_REL, f"state rel err {rel}"
+    err = float(np.max(np.abs(o - ro)))
+    assert err <= TOL_O_ABS, f"o abs err {err}"
+    np.testing.assert_array_equal(ob, bf16.from_f32(o))
+    print(f"no decay, beta logit {beta_logit}: state rel err {rel:.3g}, o abs err {err:.3g}")
+
+
 def test_zero_initial_state_config3_shape_short():
     check(oracle.make_cfg(), [0, 300], inputs.seed_for(3), state_std=0.0, conv_std=0.0)
 
