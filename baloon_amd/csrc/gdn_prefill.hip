@@ -786,43 +786,14 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     }
     lds_barrier();
     // T below the diagonal blocks: wave j (0..2) runs column block j by forward substitution
-    // (t_column). Meanwhile waves 4-7 solve (I + A) U = diag(beta) V the same way, which
-    // needs only A and the diagonal blocks: U_i = T_ii (beta_i V_i - sum_{k<i} A_ik U_k),
-    // wave 4 + wu taking columns 32 wu .. 32 wu + 31 (two 16-column tiles), each block's U^T
-    // rows stored when done. Split-bf16 products on the 16x16x16 MFMA throughout.
+    // (t_column), split-bf16 products on the 16x16x16 MFMA.
     if (w == 0) t_column<0>(A_s, T_s, lane);
     else if (w == 1) t_column<1>(A_s, T_s, lane);
     else if (w == 2) t_column<2>(A_s, T_s, lane);
-    else if (w >= 4) {
-        const int wu = w - 4;
-        float* Ut = p.ws.Ut + ch * kD * kChunk;
-        Split4 us[4][2];                                  // U_k split, token block k, column tile
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            Split4 aik[3];
-#pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (k < i) aik[k] = block_a(A_s, 16 * i, 16 * k, lane, -1.0f);
-            const Split4 tii = block_a(T_s, 16 * i, 16 * i, lane, 1.0f);
-            const v4 bt = *reinterpret_cast<const v4*>(B_s + 16 * i + 4 * lg4);
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                const int col = 32 * wu + 16 * c + li;
-                v4 y;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) y[r] = bt[r] * V_s[16 * i + 4 * lg4 + r][col];
-#pragma unroll
-                for (int k = 0; k < 3; ++k)
-                    if (k < i) y = mfma16_split(aik[k], us[k][c], y);
-                const v4 x = mfma16_split(tii, split4(y), v4{0.f, 0.f, 0.f, 0.f});
-                us[i][c] = split4(x);
-                *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * i + 4 * lg4) = x;
-            }
-        }
-    }
     lds_barrier();
 
-    // W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32). The k index (token s) runs in
+    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32), every
+    // wave taking a share of both of the same size. The k index (token s) runs in
     // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens
     // 32 ks + 4 lg4 .. +3 (the 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block
     // 2 ks + 1). T[t][s] = 0 for s > t: tile mt needs the k-steps up to mt / 2, and the blocks
@@ -844,8 +815,41 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         split8(av, h, l);
     };
     {
+        // U: T diag(beta) as the A operand, the V columns 16 w .. 16 w + 15 as the B operand;
+        // the accumulator of token tile mt holds U[16 mt + 4 lg4 + r][col], stored as U^T rows.
+        const int col = 16 * w + li;
+        v4 uacc[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) uacc[mt] = v4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int s0 = 32 * ks + 4 * lg4;
+            float bv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                bv[e] = V_s[s0 + e][col];
+                bv[e + 4] = V_s[s0 + 16 + e][col];
+            }
+            bf8 bh, bl;
+            split8(bv, bh, bl);
+#pragma unroll
+            for (int mt = 2 * ks; mt < 4; ++mt) {
+                bf8 ah, al;
+                t_frag(B_s, mt, ks, ah, al);
+                uacc[mt] = mfma_bf16(ah, bh, uacc[mt]);
+                uacc[mt] = mfma_bf16(ah, bl, uacc[mt]);
+                uacc[mt] = mfma_bf16(al, bh, uacc[mt]);
+            }
+        }
+        float* Ut = p.ws.Ut + ch * kD * kChunk;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+    }
+    {
         // W^T = K^T diag(beta Gam) T^T, wave w taking W^T row tiles 2 kw, 2 kw + 1 (k-step kw of
-        // the chain's W fragments) for token tiles 2 (w >> 2), 2 (w >> 2) + 1: the K^T fragments
+        // the chain's W fragments) for token tiles 0 and 3 (waves 0-3) or 1 and 2 (waves 4-7),
+        // three (token tile, k-step) pairs each: the K^T fragments
         // as the A operand and diag(beta Gam) T^T as the B operand, so the accumulator of (row
         // tile 2 kw + t, token tile mt) holds W[16 mt + li][32 kw + 16 t + 4 lg4 + r], r = 0..3:
         // entries 4 t + r of lane (li, lg4) of the chain's fragment (mt, kw) of -W, which the
@@ -855,14 +859,14 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int j = 0; j < 2; ++j) wacc[t][j] = v4{0.f, 0.f, 0.f, 0.f};
-        const int mt0 = 2 * (w >> 2);
+        const int mts[2] = {w < 4 ? 0 : 1, w < 4 ? 3 : 2};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            if (2 * ks > mt0 + 1) continue;                     // T is zero there (wave-uniform)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
+                if (2 * ks > mts[j]) continue;                  // T is zero there (wave-uniform)
                 bf8 bh, bl;
-                t_frag(BG_s, mt0 + j, ks, bh, bl);
+                t_frag(BG_s, mts[j], ks, bh, bl);
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     wacc[t][j] = mfma_bf16(kt[t][ks][0], bh, wacc[t][j]);
@@ -880,7 +884,7 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
                 x[r] = -wacc[0][j][r];
                 x[4 + r] = -wacc[1][j][r];
             }
-            store_frag(Wf, mt0 + j, kw, 4, lane, x);
+            store_frag(Wf, mts[j], kw, 4, lane, x);
         }
     }
 }
