@@ -988,22 +988,30 @@ __device__ __forceinline__ void chain_copy(lds_u8* dst, const uint16_t* frags, i
     for (int i = 0; i < 32; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, dst + i * kPlane, 16, 0, 0);
 }
 
-// W fragments (row tiles m = 0..3, both planes) of k-step ks from slot q.
-__device__ __forceinline__ void chain_w_frags(const uint8_t* lds, int q, int ks, int lane, bf8 (&f)[4][2]) {
+// This lane's address in an LDS area at byte offset off, made opaque to the compiler: reads
+// and writes at base + (a constant below 64 KiB) then use the instruction's immediate offset,
+// where the folded address of an area above 64 KiB would cost an add per access.
+__device__ __forceinline__ lds_u8* lane_base(uint8_t* lds, int off, int lane) {
+    lds_u8* b = (lds_u8*)lds + off + lane * 16;
+    __asm__ volatile("" : "+v"(b));
+    return b;
+}
+// W fragments (row tiles m = 0..3, both planes) of k-step ks from the slot at wq (lane base).
+__device__ __forceinline__ void chain_w_frags(const lds_u8* wq, int ks, bf8 (&f)[4][2]) {
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const int o = chain_w_slot(q) + (m * 4 + ks) * 2 * kPlane;
-        f[m][0] = lds_frag(lds, o, lane);
-        f[m][1] = lds_frag(lds, o + kPlane, lane);
+        const int o = (m * 4 + ks) * 2 * kPlane;
+        f[m][0] = *(const __attribute__((address_space(3))) bf8*)(wq + o);
+        f[m][1] = *(const __attribute__((address_space(3))) bf8*)(wq + o + kPlane);
     }
 }
-// K^T fragments (row tiles 4 g .. 4 g + 3, both planes) of k-step ks from slot q.
-__device__ __forceinline__ void chain_kt_frags(const uint8_t* lds, int q, int ks, int g, int lane, bf8 (&f)[4][2]) {
+// K^T fragments (row tiles 4 g .. 4 g + 3, both planes) of k-step ks from the slot at kq.
+__device__ __forceinline__ void chain_kt_frags(const lds_u8* kq, int ks, int g, bf8 (&f)[4][2]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int o = chain_k_slot(q) + ((4 * g + j) * 2 + ks) * 2 * kPlane;
-        f[j][0] = lds_frag(lds, o, lane);
-        f[j][1] = lds_frag(lds, o + kPlane, lane);
+        const int o = ((4 * g + j) * 2 + ks) * 2 * kPlane;
+        f[j][0] = *(const __attribute__((address_space(3))) bf8*)(kq + o);
+        f[j][1] = *(const __attribute__((address_space(3))) bf8*)(kq + o + kPlane);
     }
 }
 // acc[j] += A_j B for four row tiles, split products; the products go tile by tile within
@@ -1065,24 +1073,30 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
     v4 dg2, dg3;                       // Dg row tiles 2, 3, split at the start of part b
     bf8 R0[4][2], R1[4][2], R2[4][2];
 
+    // Lane bases of the two W, K^T and hand-over slots.
+    lds_u8* const wb[2] = {lane_base(lds, chain_w_slot(0), lane), lane_base(lds, chain_w_slot(1), lane)};
+    lds_u8* const kb[2] = {lane_base(lds, chain_k_slot(0), lane), lane_base(lds, chain_k_slot(1), lane)};
+    lds_u8* const hb[2] = {lane_base(lds, chain_h_slot(0), lane), lane_base(lds, chain_h_slot(1), lane)};
+    typedef __attribute__((address_space(3))) bf8 lds_bf8;
+    typedef __attribute__((address_space(3))) v4 lds_v4;
     auto put_s = [&](int q, int ks) {
-        lds_put(lds, chain_h_slot(q) + (2 * ks) * kPlane, lane, sh[ks]);
-        lds_put(lds, chain_h_slot(q) + (2 * ks + 1) * kPlane, lane, sl[ks]);
+        *(lds_bf8*)(hb[q] + (2 * ks) * kPlane) = sh[ks];
+        *(lds_bf8*)(hb[q] + (2 * ks + 1) * kPlane) = sl[ks];
     };
     // Part b, row tiles 0-3 (K^T k-steps 0, 1 of slot qp in R0, R1); R2 and then R0 take
     // the row tiles 4-7.
     auto part_b_lo = [&](int qp) {
-        chain_kt_frags(lds, qp, 0, 0, lane, R0);
-        chain_kt_frags(lds, qp, 1, 0, lane, R1);
+        chain_kt_frags(kb[qp], 0, 0, R0);
+        chain_kt_frags(kb[qp], 1, 0, R1);
         split_tiles(dg2, dg3, dh[1], dl[1]);
         __builtin_amdgcn_sched_barrier(0);
         mfma4_split(R0, dh[0], dl[0], S);
         __builtin_amdgcn_sched_barrier(0);
-        chain_kt_frags(lds, qp, 0, 1, lane, R2);
+        chain_kt_frags(kb[qp], 0, 1, R2);
         __builtin_amdgcn_sched_barrier(0);
         mfma4_split(R1, dh[1], dl[1], S);
         __builtin_amdgcn_sched_barrier(0);
-        chain_kt_frags(lds, qp, 1, 1, lane, R0);
+        chain_kt_frags(kb[qp], 1, 1, R0);
         __builtin_amdgcn_sched_barrier(0);
     };
     // Part b, row tiles 4-7; with A, the split and hand-over of S row tiles 0-3 (final
@@ -1092,14 +1106,14 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
         if (A) {
             split_tiles(S[0], S[1], sh[0], sl[0]);
             put_s(q, 0);
-            chain_w_frags(lds, q, 0, lane, R1);
+            chain_w_frags(wb[q], 0, R1);
         }
         __builtin_amdgcn_sched_barrier(0);
         mfma4_split(R0, dh[1], dl[1], S + 4);
         if (A) {
             split_tiles(S[2], S[3], sh[1], sl[1]);
             put_s(q, 1);
-            chain_w_frags(lds, q, 1, lane, R2);
+            chain_w_frags(wb[q], 1, R2);
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -1111,7 +1125,7 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
         put_s(q, 2);
         S[0] *= gam;
         S[1] *= gam;
-        chain_w_frags(lds, q, 2, lane, R0);
+        chain_w_frags(wb[q], 2, R0);
         __builtin_amdgcn_sched_barrier(0);
         // W k-step 1 (R2); S row tiles 6, 7 split; S row tiles 2, 3 scaled; W k-step 3 -> R1.
         mfma4_split(R2, sh[1], sl[1], U);
@@ -1119,7 +1133,7 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
         put_s(q, 3);
         S[2] *= gam;
         S[3] *= gam;
-        chain_w_frags(lds, q, 3, lane, R1);
+        chain_w_frags(wb[q], 3, R1);
         __builtin_amdgcn_sched_barrier(0);
         // W k-steps 2, 3 of row tiles 0, 1 (final after this); S row tiles 4-7 scaled.
         mfma2_split(R0, sh[2], sl[2], U);
@@ -1141,12 +1155,12 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
         }
 #pragma unroll
         for (int m = 0; m < 2; ++m)
-            *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = U[m];
+            *(lds_v4*)(hb[q] + kHandS + m * kPlane) = U[m];
         split_tiles(E[0] * U[0], E[1] * U[1], dh[0], dl[0]);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 2; m < 4; ++m)
-            *reinterpret_cast<v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16) = U[m];
+            *(lds_v4*)(hb[q] + kHandS + m * kPlane) = U[m];
         dg2 = E[2] * U[2];
         dg3 = E[3] * U[3];
         __builtin_amdgcn_sched_barrier(0);
@@ -1159,8 +1173,8 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
     put_s(0, 0);
     split_tiles(S[2], S[3], sh[1], sl[1]);
     put_s(0, 1);
-    chain_w_frags(lds, 0, 0, lane, R1);
-    chain_w_frags(lds, 0, 1, lane, R2);
+    chain_w_frags(wb[0], 0, R1);
+    chain_w_frags(wb[0], 1, R2);
     __builtin_amdgcn_sched_barrier(0);
     part_a(0);
     for (int c = c_begin + 1; c < c_end; ++c) {
