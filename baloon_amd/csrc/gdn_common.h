@@ -66,9 +66,10 @@ __device__ __forceinline__ float conv_eval(const Layer& L, const float* hist, fl
 }
 
 // Log decay -exp(A_log) * softplus(a + dt_bias); the decay is exp() of it.
-__device__ __forceinline__ float log_gate(const Layer& L, int h, float a) {
-    return -expf(L.A_log[h]) * softplus_f(a + L.dt_bias[h]);
+__device__ __forceinline__ float log_gate(float A_log, float dt_bias, float a) {
+    return -expf(A_log) * softplus_f(a + dt_bias);
 }
+__device__ __forceinline__ float log_gate(const Layer& L, int h, float a) { return log_gate(L.A_log[h], L.dt_bias[h], a); }
 
 // Sum over the 32 lanes of each half wave, result in all of them.
 __device__ __forceinline__ float half_sum(float v) { return pair_sum16(row_sum16(v)); }

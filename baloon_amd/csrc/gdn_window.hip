@@ -115,6 +115,13 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
             xk[t] = *reinterpret_cast<const uint32_t*>(p.x + ((size_t)bseq * K + min(t, K - 1)) * L.C + ch);
     }
 
+    // Gate inputs, one token per thread of the last kMaxWindow, and the head's decay
+    // parameters: loaded by every thread (clamped addresses) ahead of the state.
+    const int gt = tid - (kThreads - kMaxWindow);
+    const size_t ab = ((size_t)bseq * K + min(max(gt, 0), K - 1)) * L.h_v + h;
+    const uint16_t a_in = p.a[ab], b_in = p.b[ab];
+    const float a_log = L.A_log[h], dt_b = L.dt_bias[h];
+
     const v4f* tile = reinterpret_cast<const v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
     const int j0 = hf * kHalf + 2 * kPairs * w + half;
     v4f s[kPairs];
@@ -142,13 +149,9 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
             }
         }
     }
-    if (tid >= kThreads - kMaxWindow) {                       // gates: one thread per token
-        const int t = tid - (kThreads - kMaxWindow);
-        if (t < K) {
-            const size_t ab = ((size_t)bseq * K + t) * L.h_v + h;
-            g_s[t] = expf(log_gate(L, h, bf16_to_f32(p.a[ab])));
-            b_s[t] = sigmoid_f(bf16_to_f32(p.b[ab]));
-        }
+    if (gt >= 0 && gt < K) {                                  // gates: one thread per token
+        g_s[gt] = expf(log_gate(a_log, dt_b, bf16_to_f32(a_in)));
+        b_s[gt] = sigmoid_f(bf16_to_f32(b_in));
     }
     lds_barrier();
 
@@ -198,9 +201,10 @@ __global__ void __launch_bounds__(kThreads) window_verify_kernel(const WindowPar
 //   d_t = beta_t (v_t - G_t (S^T k_t) - sum_{s<t} r(t, s) (k_t . k_s) d_s)
 //   o_t = G_t (S^T q_t) + sum_{s<=t} r(t, s) (q_t . k_s) d_s
 // (k, q normalised; q with its scale). The state enters only through the 2K products
-// S^T k_t and S^T q_t: one split-bf16 MFMA product per wave, the state as the A operand
-// loaded from HBM straight into the fragments -- lane (li, lg) of wave w holds column
-// j = 64 hf + 16 w + li at key rows 32 ks + kperm(lg, e) -- and never stored. The K x K
+// S^T k_t and S^T q_t: one split-bf16 MFMA product per wave with the state as the A operand
+// (lane (li, lg) of wave w holds column j = 64 hf + 16 w + li at key rows 32 ks + kperm(lg, e)),
+// loaded from HBM in whole lines, passed through the wave's own LDS tile into that layout,
+// and never stored. The K x K
 // products k_t . k_s and q_t . k_s come from the same token fragments. Each column then runs
 // the K-step recurrence above in fp32. Outputs agree with K ix_gdn_decode calls to fp32
 // rounding (not bit for bit); the record is computed exactly as window_verify_kernel computes
@@ -217,6 +221,11 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
     __shared__ float sq_s[KMAX], sk_s[KMAX], g_s[KMAX], b_s[KMAX];
     __shared__ float kk_s[KMAX][KP], qk_s[KMAX][KP];         // k_t . k_s, q_t . k_s
     __shared__ float sk_t[kHalf][KP], sq_t[kHalf][KP];       // S^T k_t, S^T q_t per column
+    // Each wave's 16 state columns, 64 rows at a time, column-major with rows padded to SR
+    // floats: the coalesced loads write it and the fragment reads take it back out, both
+    // without bank conflicts.
+    constexpr int SR = 64 + 4;
+    __shared__ __align__(16) float st_s[kThreads / kWave][16 * SR];
 
     const Layer& L = p.L;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
@@ -246,23 +255,23 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
         for (int t = 0; t < KMAX; ++t)
             xk[t] = *reinterpret_cast<const uint32_t*>(p.x + ((size_t)bseq * K + min(t, K - 1)) * L.C + ch);
     }
-    // Gate inputs, one thread per token (loaded ahead of the state, by threads past the conv).
+    // Gate inputs, one token per thread of the last KMAX, and the head's decay parameters:
+    // loaded by every thread (clamped addresses) ahead of the state, so that no branch waits
+    // for them before the state loads go out and the gates do not wait for the state.
     const int gt = tid - (kThreads - KMAX);
-    uint16_t a_in = 0, b_in = 0;
-    if (gt >= 0 && gt < K) {
-        const size_t ab = ((size_t)bseq * K + gt) * L.h_v + h;
-        a_in = p.a[ab];
-        b_in = p.b[ab];
-    }
+    const size_t ab = ((size_t)bseq * K + min(max(gt, 0), K - 1)) * L.h_v + h;
+    const uint16_t a_in = p.a[ab], b_in = p.b[ab];
+    const float a_log = L.A_log[h], dt_b = L.dt_bias[h];
 
-    // State fragments (k-steps ks = 0..3, the two runs of 4 key rows of kperm).
-    const float* colp = p.state + (((size_t)bseq * L.h_v + h) * kD + hf * kHalf + 16 * w + li) * kD + 4 * lg;
-    v4f sf[4][2];
+    // The wave's 16 state columns in whole 128-byte lines: load 4 rh + c4 brings column
+    // 16 w + 4 c4 + lg, rows 64 rh + 4 li .. 64 rh + 4 li + 3, to lane (li, lg), i.e. four
+    // 256-byte runs per instruction. The fragment layout (one column per li) is reached
+    // through the wave's LDS tile in the product loop.
+    const float* wcol = p.state + (((size_t)bseq * L.h_v + h) * kD + hf * kHalf + 16 * w + lg) * kD + 4 * li;
+    v4f sraw[8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        sf[ks][0] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(colp + 32 * ks));
-        sf[ks][1] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(colp + 32 * ks + 16));
-    }
+    for (int i = 0; i < 8; ++i)
+        sraw[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(wcol + 4 * (i & 3) * kD + 64 * (i >> 2)));
 
     // Phase 1: conv outputs, squared norms (waves 0 and 1) and gates of every token.
     if (conv_thread) {
@@ -286,19 +295,10 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
         }
     }
     if (gt >= 0 && gt < K) {
-        g_s[gt] = expf(log_gate(L, h, bf16_to_f32(a_in)));
+        g_s[gt] = expf(log_gate(a_log, dt_b, bf16_to_f32(a_in)));
         b_s[gt] = sigmoid_f(bf16_to_f32(b_in));
     }
     lds_barrier();
-
-    // The record, exactly as window_verify_kernel writes it: it depends on phase 1 only, so
-    // it is written here, where its stores overlap the products and the recurrence below.
-    for (int t = 0; t < K; ++t) {
-        const size_t row = (size_t)bseq * K + t;
-        if (rec_k && tid < kD) p.rec.k[(row * L.h_k + src) * kD + tid] = k_s[t][tid] * (1.0f / sqrtf(sk_s[t] + L.l2_eps));
-        if (tid < kHalf) p.rec.v[(row * L.h_v + h) * kD + hf * kHalf + tid] = v_s[t][tid];
-        if (hf == 0 && tid == 0) { p.rec.g[row * L.h_v + h] = g_s[t]; p.rec.bt[row * L.h_v + h] = b_s[t]; }
-    }
 
     // Token fragments: the normalised k_t and q_t (the decode kernel's inverse norms) at this
     // lane's key rows. Up to 8 tokens share one 16-wide operand tile: column n < K is k_n,
@@ -319,8 +319,18 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
     const float s1 = tok1 ? (kShared ? 1.0f / sqrtf(sk_s[row1] + L.l2_eps) : L.q_scale / sqrtf(sq_s[row1] + L.l2_eps))
                           : 0.0f;
     const float* base1 = kShared ? k_s[row1] : q_s[row1];
+    float* tile = st_s[w];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+        if ((ks & 1) == 0) {                                    // rows 32 ks .. 32 ks + 63 into the tile
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) *reinterpret_cast<v4f*>(tile + (4 * c4 + lg) * SR + 4 * li) = sraw[2 * ks + c4];
+            wave_lds_sync();
+        }
+        const int r0 = 32 * (ks & 1) + 4 * lg;                  // this lane's rows within the tile
+        const v4f st0 = *reinterpret_cast<const v4f*>(tile + li * SR + r0);
+        const v4f st1 = *reinterpret_cast<const v4f*>(tile + li * SR + r0 + 16);
+        if (ks & 1) wave_lds_sync();                            // read before the next rows are written
         float x0[8], x1[8], sx[8];
         const int i0 = 32 * ks + 4 * lg;                        // kperm: rows i0..i0+3, i0+16..i0+19
         const v4f a0 = *reinterpret_cast<const v4f*>(base0 + i0), a1 = *reinterpret_cast<const v4f*>(base0 + i0 + 16);
@@ -331,8 +341,8 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
             x0[e + 4] = a1[e] * s0;
             x1[e] = c0[e] * s1;
             x1[e + 4] = c1[e] * s1;
-            sx[e] = sf[ks][0][e];
-            sx[e + 4] = sf[ks][1][e];
+            sx[e] = st0[e];
+            sx[e + 4] = st1[e];
         }
         bf8 h0, l0, h1, l1, sh, sl;
         split8(x0, h0, l0);
@@ -346,6 +356,14 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
             if (w == 1) kk = mfma_split(h0, l0, h0, l0, kk);
             if (w == 2) qk = mfma_split(h1, l1, h0, l0, qk);
         }
+    }
+    // The record, exactly as window_verify_kernel writes it. Its stores go out once the state
+    // has been consumed: issued among the state loads, they would be waited for with them.
+    for (int t = 0; t < K; ++t) {
+        const size_t row = (size_t)bseq * K + t;
+        if (rec_k && tid < kD) p.rec.k[(row * L.h_k + src) * kD + tid] = k_s[t][tid] * (1.0f / sqrtf(sk_s[t] + L.l2_eps));
+        if (tid < kHalf) p.rec.v[(row * L.h_v + h) * kD + hf * kHalf + tid] = v_s[t][tid];
+        if (hf == 0 && tid == 0) { p.rec.g[row * L.h_v + h] = g_s[t]; p.rec.bt[row * L.h_v + h] = b_s[t]; }
     }
     // Accumulator element r of lane (li, lg) is row 4 lg + r, column li.
 #pragma unroll

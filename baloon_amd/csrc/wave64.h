@@ -60,6 +60,15 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Orders one wave's LDS accesses across its lanes: reads issued after this point see the
+// writes the wave's other lanes issued before it. A wave's LDS operations execute in issue
+// order, so this only keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
 // Double-precision 64-lane sum, result in every lane (xor butterfly on ds_swizzle/bpermute).
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
