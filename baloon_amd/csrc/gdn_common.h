@@ -7,6 +7,7 @@
 // (gate from A_log/dt_bias, beta = sigmoid(b), optional SiLU after the conv, the
 // contiguous head map) are selected by ix_gdn_cfg.
 #pragma once
+#include <atomic>
 #include "ix_gdn.h"
 #include "wave64.h"
 
@@ -129,6 +130,20 @@ inline OutGate make_out_gate(const ix_gdn_out_gate* g) {
         o.y_q8_1 = static_cast<uint8_t*>(g->y_q8_1);
     }
     return o;
+}
+
+// Compute units of the current device, queried once per device (256 on MI355X).
+inline int device_cu_count() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cached[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 // q8_1 block (36 bytes: half d, half s, int8 qs[32]; the activation format of the Q8_0 product,
