@@ -34,6 +34,9 @@ constexpr int kThreads = 256;
 constexpr int kHalf = 64;                                 // columns per workgroup
 constexpr int kPairs = kHalf / 2 / (kThreads / kWave);    // 8 column pairs per wave
 constexpr int kMaxWindow = 16;
+// Extra LDS a capped commit launch reserves: with the kernel's own 12 KiB, more than a fifth of
+// a CU's 160 KiB.
+constexpr unsigned kCommitLdsReserve = 24000;
 
 struct WinRec {
     float* k;       // [B*K][h_k][128]
@@ -619,7 +622,13 @@ extern "C" hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, 
     if (e != hipSuccess) return e;
     if (!accepted) return hipErrorInvalidValue;
     p.accepted = accepted;
+    // With at least 8 workgroups per CU to run (B >= 32 at h_v = 32), the launch reserves LDS that
+    // no code touches, so that at most four workgroups share a CU (the decode's slab kernel does
+    // the same with two): B = 64 47.5 against 48.1 us, B = 128 89.0 against 90.5; equal at
+    // B = 32, slower at B = 16.
+    const long long nwg = 2LL * cfg->h_v * B;
+    const unsigned lds = nwg >= 8LL * ixg::device_cu_count() ? ixg::kCommitLdsReserve : 0;
     hipLaunchKernelGGL(ixg::window_commit_kernel, dim3((unsigned)(2 * cfg->h_v), (unsigned)B), dim3(ixg::kThreads),
-                       0, s, p);
+                       lds, s, p);
     return hipGetLastError();
 }
