@@ -426,7 +426,10 @@ __device__ __forceinline__ Split4 block_a(const float* m, int r0, int c0, int la
 // Column block J of T = (I + A)^-1 below the diagonal, by forward substitution on the
 // identity's block column: T_kj = -T_kk sum_{m=J}^{k-1} A_km T_mj, k = J+1..3, from the
 // diagonal blocks T_kk already in T_s. Each block is chained to the next product in
-// registers (its accumulator, split, is the B operand) and stored to T_s when done.
+// registers (its accumulator, split, is the B operand) and stored to T_s when done, at the
+// mirrored block position (J, k): T shares its array with A (A's diagonal blocks are
+// overwritten by T's in place, its blocks above the diagonal are never written), so T[t][s]
+// of block (k, J), J <= k, sits at row 16 J + t % 16, column 16 k + s % 16.
 template <int J>
 __device__ __forceinline__ void t_column(const float* A_s, float* T_s, int lane) {
     const int li = lane & 15, lg4 = lane >> 4;
@@ -445,7 +448,7 @@ __device__ __forceinline__ void t_column(const float* A_s, float* T_s, int lane)
         const v4 x = mfma16_split(block_a(T_s, 16 * k, 16 * k, lane, 1.0f), split4(acc), v4{0.f, 0.f, 0.f, 0.f});
         xs[k] = split4(x);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) T_s[(16 * k + 4 * lg4 + r) * kTS + 16 * J + li] = x[r];
+        for (int r = 0; r < 4; ++r) T_s[(16 * J + 4 * lg4 + r) * kTS + 16 * k + li] = x[r];
     }
 }
 
@@ -678,17 +681,18 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
 // v_kernel: grid (NC, h_v), 512 threads; workgroup = (chunk, v head). Phases: decay scan and
 // beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
 // compute the v rows | A (to LDS) and M (to its fragments) (waves 0-3) | the four 16 x 16
-// diagonal blocks of T by substitution (wave 0) | the blocks of T below them
-// by forward substitution on the identity's block columns (waves 0-2), while waves 4-7
-// solve (I + A) U = diag(beta) V the same way, U^T stored from the MFMA layout |
-// W^T = K^T diag(beta Gam) T^T, whose accumulators are the chain's -W fragments as they
-// stand, stored from registers.
+// diagonal blocks of T by substitution (wave 0) | the blocks of T below them by forward
+// substitution on the identity's block columns (waves 0-2) | U = T diag(beta) V (U^T stored
+// from the MFMA layout) and W^T = K^T diag(beta Gam) T^T, whose accumulators are the chain's
+// -W fragments as they stand, stored from registers, split evenly over the eight waves.
+// T shares its LDS array with A, which keeps the workgroup at 51 KiB of LDS and 78 VGPRs:
+// three workgroups per CU.
 template <int DC>
-__global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[kChunk * kKS + 2 * kChunk * kTS];
+__global__ void __launch_bounds__(kChunkThreads, 6) v_kernel(const PrefillParams p) {
+    __shared__ __align__(16) float lds[kChunk * kKS + kChunk * kTS];
     float (*V_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);        // v rows
     float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
-    float* T_s = A_s + kChunk * kTS;                                   // [64][kTS]
+    float* T_s = A_s;                  // T over A: diagonal blocks in place, the others mirrored
     __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
 
     ChunkGeo g;
@@ -750,20 +754,6 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
             *reinterpret_cast<float2*>(&V_s[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
     }
     lds_barrier();
-    // K^T fragments of row tiles 2 (w & 3) and 2 (w & 3) + 1 (the A operand of W^T below),
-    // issued here so that they do not queue ahead of the raw products and the x rows.
-    const int kw = w & 3;
-    bf8 kt[2][2][2];
-    {
-        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int pl = 0; pl < 2; ++pl)
-                    kt[t][ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(2 * kw + t, ks, 2, pl, lane));
-    }
     if (w < 4) am_head(kk, qk, G_s, B_s, A_s, p.ws.Mf + ch * kFragM, w, lane);
     lds_barrier();
 
@@ -792,6 +782,22 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     else if (w == 2) t_column<2>(A_s, T_s, lane);
     lds_barrier();
 
+    // K^T fragments of row tiles 2 (w & 3) and 2 (w & 3) + 1 (the A operand of W^T below),
+    // loaded here, so that the U product below hides their latency: held from the first
+    // barrier on, they kept 32 more registers live through the inverse (90 VGPRs, two
+    // workgroups per CU instead of three).
+    const int kw = w & 3;
+    bf8 kt[2][2][2];
+    {
+        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl)
+                    kt[t][ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(2 * kw + t, ks, 2, pl, lane));
+    }
     // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32), every
     // wave taking a share of both of the same size. The k index (token s) runs in
     // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens
@@ -803,8 +809,10 @@ __global__ void __launch_bounds__(kChunkThreads) v_kernel(const PrefillParams p)
     auto t_frag = [&](const float* sc, int mt, int ks, bf8& h, bf8& l) {
         const int s0 = 32 * ks + 4 * lg4;
         const v4 sc0 = *reinterpret_cast<const v4*>(sc + s0), sc1 = *reinterpret_cast<const v4*>(sc + s0 + 16);
-        const float* tr = T_s + (16 * mt + li) * kTS + s0;
-        const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16);
+        // T[16 mt + li][s] of blocks J = 2 ks, 2 ks + 1 (mirrored storage; the reads of blocks
+        // above the diagonal land in A and are discarded below).
+        const float* tr = T_s + (32 * ks + li) * kTS + 16 * mt + 4 * lg4;
+        const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16 * kTS);
         const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
         float av[8];
 #pragma unroll
