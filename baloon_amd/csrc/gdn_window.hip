@@ -224,10 +224,10 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
     __shared__ float sq_s[KMAX], sk_s[KMAX], g_s[KMAX], b_s[KMAX];
     __shared__ float kk_s[KMAX][KP], qk_s[KMAX][KP];         // k_t . k_s, q_t . k_s
     __shared__ float sk_t[kHalf][KP], sq_t[kHalf][KP];       // S^T k_t, S^T q_t per column
-    // Each wave's 16 state columns, 64 rows at a time, column-major with rows padded to SR
-    // floats: the coalesced loads write it and the fragment reads take it back out, both
-    // without bank conflicts.
-    constexpr int SR = 64 + 4;
+    // Each wave's 16 state columns, 32 rows (one k-step) at a time, column-major with rows
+    // padded to SR floats: the coalesced loads write it and the fragment reads take it back
+    // out, both without bank conflicts.
+    constexpr int SR = 32 + 4;
     __shared__ __align__(16) float st_s[kThreads / kWave][16 * SR];
 
     const Layer& L = p.L;
@@ -266,15 +266,15 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
     const uint16_t a_in = p.a[ab], b_in = p.b[ab];
     const float a_log = L.A_log[h], dt_b = L.dt_bias[h];
 
-    // The wave's 16 state columns in whole 128-byte lines: load 4 rh + c4 brings column
-    // 16 w + 4 c4 + lg, rows 64 rh + 4 li .. 64 rh + 4 li + 3, to lane (li, lg), i.e. four
-    // 256-byte runs per instruction. The fragment layout (one column per li) is reached
-    // through the wave's LDS tile in the product loop.
-    const float* wcol = p.state + (((size_t)bseq * L.h_v + h) * kD + hf * kHalf + 16 * w + lg) * kD + 4 * li;
+    // The wave's 16 state columns in whole 128-byte lines: load 2 ks + c8 brings column
+    // 16 w + 8 c8 + lane / 8, rows 32 ks + 4 (lane % 8) .. + 3, i.e. eight whole lines per
+    // instruction. The fragment layout (one column per li) is reached through the wave's
+    // LDS tile in the product loop.
+    const float* wcol = p.state + (((size_t)bseq * L.h_v + h) * kD + hf * kHalf + 16 * w + (lane >> 3)) * kD + 4 * (lane & 7);
     v4f sraw[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        sraw[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(wcol + 4 * (i & 3) * kD + 64 * (i >> 2)));
+        sraw[i] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(wcol + 8 * (i & 1) * kD + 32 * (i >> 1)));
 
     // Phase 1: conv outputs, squared norms (waves 0 and 1) and gates of every token.
     if (conv_thread) {
@@ -325,15 +325,14 @@ __global__ void __launch_bounds__(kThreads, KMAX <= 8 ? 5 : 1) window_mfma_kerne
     float* tile = st_s[w];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-        if ((ks & 1) == 0) {                                    // rows 32 ks .. 32 ks + 63 into the tile
+        // Rows 32 ks .. 32 ks + 31 into the tile, then this lane's fragment rows back out.
 #pragma unroll
-            for (int c4 = 0; c4 < 4; ++c4) *reinterpret_cast<v4f*>(tile + (4 * c4 + lg) * SR + 4 * li) = sraw[2 * ks + c4];
-            wave_lds_sync();
-        }
-        const int r0 = 32 * (ks & 1) + 4 * lg;                  // this lane's rows within the tile
-        const v4f st0 = *reinterpret_cast<const v4f*>(tile + li * SR + r0);
-        const v4f st1 = *reinterpret_cast<const v4f*>(tile + li * SR + r0 + 16);
-        if (ks & 1) wave_lds_sync();                            // read before the next rows are written
+        for (int c8 = 0; c8 < 2; ++c8)
+            *reinterpret_cast<v4f*>(tile + (8 * c8 + (lane >> 3)) * SR + 4 * (lane & 7)) = sraw[2 * ks + c8];
+        wave_lds_sync();
+        const v4f st0 = *reinterpret_cast<const v4f*>(tile + li * SR + 4 * lg);
+        const v4f st1 = *reinterpret_cast<const v4f*>(tile + li * SR + 4 * lg + 16);
+        wave_lds_sync();                                        // read before the next rows are written
         float x0[8], x1[8], sx[8];
         const int i0 = 32 * ks + 4 * lg;                        // kperm: rows i0..i0+3, i0+16..i0+19
         const v4f a0 = *reinterpret_cast<const v4f*>(base0 + i0), a1 = *reinterpret_cast<const v4f*>(base0 + i0 + 16);
