@@ -19,7 +19,9 @@
 // Kernels, chosen by the launcher:
 //  * slab_kernel (a workspace of per-group counters is given): one workgroup per
 //    (sequence, v head, 64-column half tile), 4096 workgroups at B=64 for a short,
-//    well-balanced stream. Every workgroup evaluates the q/k conv of its q/k head
+//    well-balanced stream (512 threads instead of 256 when the grid does not fill the
+//    CUs, B <= 4 at h_v = 32, so that each wave runs 4 column pairs instead of 8: B=1
+//    replays at 3.98-4.01 against 4.13-4.25 us per token). Every workgroup evaluates the q/k conv of its q/k head
 //    read-only; the conv history of those channels is written back by the last workgroup
 //    of the (sequence, q/k head) group to finish reading it, found with one atomic counter
 //    per group. The counter is reset by that workgroup, so the workspace is all zeros
@@ -44,7 +46,8 @@ namespace {
 constexpr int kThreads = 256;                        // 4 waves
 constexpr int kMaxHeadsPerGroup = 16;                // v heads per q/k head
 constexpr int kHalfCols = 64;                        // columns per slab_kernel workgroup
-constexpr int kPairsPerWave = kHalfCols / 2 / (kThreads / kWave);   // 8 column pairs
+constexpr int kSmallGridThreads = 512;               // slab workgroup size when the grid is below the CU count
+constexpr int kPairsPerWave = kHalfCols / 2 / (kThreads / kWave);   // 8 column pairs (head kernel)
 
 struct DecodeParams {
     Layer L;
@@ -117,11 +120,14 @@ __device__ __forceinline__ float column_update(const DecodeParams& p, v4f s, v4f
 
 
 // ---------------------------------------------------------------------------------------
-// slab_kernel: grid (2 h_v, B); workgroup = (sequence bseq, v head h, half tile hf)
+// slab_kernel: grid (2 h_v, B); workgroup = (sequence bseq, v head h, half tile hf) of NT
+// threads (kThreads, or kSmallGridThreads when the grid does not fill the CUs: more waves
+// share the 32 column pairs, so each runs fewer of them in series)
 // ---------------------------------------------------------------------------------------
-template <int DC>
-__global__ void __launch_bounds__(kThreads)
+template <int DC, int NT>
+__global__ void __launch_bounds__(NT)
 slab_kernel(const DecodeParams p, const DecodeWs ws) {
+    constexpr int kPW = kHalfCols / 2 / (NT / kWave);         // column pairs per wave
     __shared__ __align__(16) float q_s[kD], k_s[kD], v_s[kHalfCols];
     int* __restrict__ counters = ws.group;
     __shared__ float scal_s[2], gb_s[2];
@@ -148,12 +154,12 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
     const size_t ab = (size_t)bseq * L.h_v + h;
     const uint16_t a_in = p.a[ab], b_in = p.b[ab];
 
-    // State: wave w owns columns hf*64 + 16 w + 2 u + half, u = 0..7.
+    // State: wave w owns columns hf*64 + 2 kPW w + 2 u + half, u = 0..kPW-1.
     v4f* tile = reinterpret_cast<v4f*>(p.state + ((size_t)bseq * L.h_v + h) * kD * kD) + i4;
-    const int j0 = hf * kHalfCols + 2 * kPairsPerWave * w + half;
-    v4f s[kPairsPerWave];
+    const int j0 = hf * kHalfCols + 2 * kPW * w + half;
+    v4f s[kPW];
 #pragma unroll
-    for (int u = 0; u < kPairsPerWave; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
+    for (int u = 0; u < kPW; ++u) s[u] = __builtin_nontemporal_load(tile + (size_t)(j0 + 2 * u) * (kD / 4));
 
     uint32_t nh[DC - 1];
     float y0 = 0.0f, y1 = 0.0f;
@@ -167,7 +173,7 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
         const float r = wave_sum(fmaf(y0, y0, y1 * y1));
         if (lane == 0) scal_s[w] = r;
     }
-    if (tid == kThreads - 1) {
+    if (tid == NT - 1) {
         gb_s[0] = expf(log_gate(L, h, bf16_to_f32(a_in)));
         gb_s[1] = sigmoid_f(bf16_to_f32(b_in));
     }
@@ -191,7 +197,7 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
     const float g = gb_s[0], bt = gb_s[1];
     const size_t ob = ((size_t)bseq * L.h_v + h) * kD;
 #pragma unroll
-    for (int u = 0; u < kPairsPerWave; ++u) {
+    for (int u = 0; u < kPW; ++u) {
         const int j = j0 + 2 * u;
         column_update(p, s[u], tile + (size_t)j * (kD / 4), kr, qr, v_s[j - hf * kHalfCols], g, bt, kq, ob + j, i4 == 0);
     }
@@ -434,11 +440,21 @@ void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, const De
     } else if (ws && every_src_used(cfg)) {
         const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
         const long long nwg = 2LL * cfg->h_v * B;
-        const unsigned lds = nwg >= (long long)kSlabCapPerCu * device_cu_count() ? kSlabLdsReserve : 0;
-        switch (cfg->d_conv) {
-            case 2: hipLaunchKernelGGL(slab_kernel<2>, grid, block, lds, s, p, *ws); break;
-            case 3: hipLaunchKernelGGL(slab_kernel<3>, grid, block, lds, s, p, *ws); break;
-            default: hipLaunchKernelGGL(slab_kernel<4>, grid, block, lds, s, p, *ws); break;
+        const int cus = device_cu_count();
+        const unsigned lds = nwg >= (long long)kSlabCapPerCu * cus ? kSlabLdsReserve : 0;
+        if (nwg <= cus) {                                     // B <= 4 at h_v = 32
+            constexpr int NT = kSmallGridThreads;
+            switch (cfg->d_conv) {
+                case 2: hipLaunchKernelGGL((slab_kernel<2, NT>), grid, dim3(NT), 0, s, p, *ws); break;
+                case 3: hipLaunchKernelGGL((slab_kernel<3, NT>), grid, dim3(NT), 0, s, p, *ws); break;
+                default: hipLaunchKernelGGL((slab_kernel<4, NT>), grid, dim3(NT), 0, s, p, *ws); break;
+            }
+        } else {
+            switch (cfg->d_conv) {
+                case 2: hipLaunchKernelGGL((slab_kernel<2, kThreads>), grid, block, lds, s, p, *ws); break;
+                case 3: hipLaunchKernelGGL((slab_kernel<3, kThreads>), grid, block, lds, s, p, *ws); break;
+                default: hipLaunchKernelGGL((slab_kernel<4, kThreads>), grid, block, lds, s, p, *ws); break;
+            }
         }
     } else {
         const dim3 grid((unsigned)cfg->h_k, (unsigned)B);
