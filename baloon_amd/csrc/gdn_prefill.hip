@@ -591,15 +591,17 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
         conv_load<DC>(p, g, g.lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
         float y0[kConvTok], y1[kConvTok];
         conv_run<DC>(L, in, y0, y1);
-        // All 16 row sums first (independent, so their shuffle latencies overlap).
+        // The 16 row sums in one reduce-scatter: lane l holds the sum of row l >> 2, so one
+        // rsqrt gives every row's factor, which each row then reads from lane 4 t.
         float ss[kConvTok];
 #pragma unroll
-        for (int t = 0; t < kConvTok; ++t) ss[t] = wave_sum(fmaf(y0[t], y0[t], y1[t] * y1[t]));
+        for (int t = 0; t < kConvTok; ++t) ss[t] = fmaf(y0[t], y0[t], y1[t] * y1[t]);
         const float scale = isk ? 1.0f : L.q_scale;
+        const float inv_l = scale * rsqrtf(sum16_scatter(ss, lane) + L.l2_eps);
         uint8_t* dst = isk ? Kp : Qp;
 #pragma unroll
         for (int t = 0; t < kConvTok; ++t) {
-            const float inv = scale * rsqrtf(ss[t] + L.l2_eps);
+            const float inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_l), 4 * t));
             uint32_t hi = 0, lo = 0;
             if (t < nt) split2(y0[t] * inv, y1[t] * inv, hi, lo);
             const int o = qk_off(tb + t, c2);

@@ -51,6 +51,36 @@ __device__ __forceinline__ float wave_sum(float v) {
     return pair_sum32(pair_sum16(row_sum16(v)));
 }
 
+// Sixteen 64-lane sums at once, as a reduce-scatter: at lane distance 32, 16, 8 and 4 each
+// step exchanges half of the remaining partial sums with the partner lane (which keeps the
+// other half), so no partial sum is formed twice; the last two steps add within each quad.
+// Lane l returns the total of v[l >> 2] (bit 5 of l picks bit 3 of the index, bit 4 bit 2,
+// bit 3 bit 1, bit 2 bit 0). About 60 instructions against 16 x 8 for separate sums.
+__device__ __forceinline__ float sum16_scatter(const float (&v)[16], int lane) {
+    float a[8], b[4], c[2];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {            // lanes 0-31 keep index t, lanes 32-63 t + 8
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[t]), __float_as_uint(v[t + 8]), false, false);
+        a[t] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {            // even rows keep index j, odd rows j + 4
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]), __float_as_uint(a[j + 4]), false, false);
+        b[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool h8 = lane & 8, h4 = lane & 4;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {            // lanes i ^ 8 within each row
+        const float own = h8 ? b[k + 2] : b[k], send = h8 ? b[k] : b[k + 2];
+        c[k] = own + dpp_f32<kDppRowRor8>(send);
+    }
+    const float own = h4 ? c[1] : c[0], send = h4 ? c[0] : c[1];
+    float d = own + dpp_f32<kDppRowHalfMirror>(send);     // lanes i and 7 - i of each 8
+    d += dpp_f32<kDppQuadXor1>(d);
+    d += dpp_f32<kDppQuadXor2>(d);
+    return d;
+}
+
 // Workgroup barrier that orders LDS accesses only. __syncthreads() also orders global
 // memory, which makes every wave wait for all of its outstanding global loads (vmcnt(0))
 // before the barrier -- including loads issued early on purpose to prefetch later work.
