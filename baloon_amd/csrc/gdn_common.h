@@ -132,12 +132,20 @@ inline OutGate make_out_gate(const ix_gdn_out_gate* g) {
     return o;
 }
 
-// Compute units of the current device, queried once per device (256 on MI355X).
-inline int device_cu_count() {
+// Compute units of the device that stream s launches on (the calling thread's current device
+// for the null stream), queried once per device (256 on MI355X).
+inline int device_cu_count(hipStream_t s) {
     constexpr int kMaxDev = 64;
     static std::atomic<int> cached[kMaxDev];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+    if (s) {
+        hipDevice_t d = 0;
+        if (hipStreamGetDevice(s, &d) != hipSuccess) return 256;
+        dev = (int)d;
+    } else if (hipGetDevice(&dev) != hipSuccess) {
+        return 256;
+    }
+    if (dev < 0 || dev >= kMaxDev) return 256;
     int n = cached[dev].load(std::memory_order_relaxed);
     if (n <= 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
@@ -155,7 +163,13 @@ inline int device_cu_count() {
 // function, so the same fp32 values give the same bytes, division included
 // (src/ix_q81_div.h:1-9). The inputs are finite. All 64 lanes of the wave must call it (its
 // reductions stay within each half wave); a half wave that passes blk == nullptr stores nothing.
+// Range: d and s are stored as fp16, so both are clamped to its largest finite value, 65504,
+// before the conversion. A block whose d would exceed it (max|v| > 127 * 65504, about 8.3e6)
+// is quantised with d = 65504 and its codes saturate at +-127; below that bound the clamps
+// change nothing. The reference names such a clamp (q8_1_finite, src/ix_q81_div.h:9) without
+// defining it, so this rule is this library's own.
 constexpr int kQ81Bytes = 36;
+constexpr float kHalfMax = 65504.0f;
 __device__ __forceinline__ void q81_store(float v, int lane, uint8_t* blk) {
     float amax = fabsf(v), sum = v;
 #pragma unroll
@@ -163,12 +177,13 @@ __device__ __forceinline__ void q81_store(float v, int lane, uint8_t* blk) {
         amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
         sum = sum + __shfl_xor(sum, off, kWave);
     }
-    const float d = amax / 127.0f;
-    const int q = d == 0.0f ? 0 : (int)roundf(v / d);
+    const float d = fminf(amax / 127.0f, kHalfMax);
+    const int q = d == 0.0f ? 0 : (int)fminf(fmaxf(roundf(v / d), -127.0f), 127.0f);
     if (!blk) return;
     blk[4 + (lane & 31)] = (uint8_t)(int8_t)q;
     if ((lane & 31) == 0) {
-        const uint32_t hd = __builtin_bit_cast(uint16_t, (_Float16)d), hs = __builtin_bit_cast(uint16_t, (_Float16)sum);
+        const float sc = fminf(fmaxf(sum, -kHalfMax), kHalfMax);
+        const uint32_t hd = __builtin_bit_cast(uint16_t, (_Float16)d), hs = __builtin_bit_cast(uint16_t, (_Float16)sc);
         *reinterpret_cast<uint32_t*>(blk) = hd | (hs << 16);
     }
 }

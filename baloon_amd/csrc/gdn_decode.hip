@@ -34,6 +34,20 @@
 //    channel and tile of the group; race free by ownership. It has the gated variant too.
 // The gated norm's sum of squares is the same two wave sums (columns 0..63, 64..127) in the
 // head and group kernels, so they give the same bits.
+//
+// The group counter hand-off (slab and head kernels) rests on three facts, none of which is
+// a guarantee of the HIP memory model (the counter add is a relaxed atomic with no
+// release/acquire pairing, which at agent scope would wait for the state loads kept in
+// flight across it):
+//  1. Each member consumes its q/k conv-history loads before its LDS-only barrier: their
+//     values feed the conv outputs that it stores to LDS ahead of that barrier, so the wave
+//     has waited for those loads before it reaches the barrier.
+//  2. The compiler keeps the global atomic add after the s_barrier (tests/test_codegen.py
+//     checks this in the built code of every slab and head kernel), and a wave issues its
+//     instructions in order, so the add is performed after the member's history reads.
+//  3. The last member's history writes follow its add (they need its result), and the
+//     next call on the stream starts after this kernel has ended.
+// So the last arrival rewrites the history only after every member has read it.
 // State loads use nontemporal hints and are issued right after the conv inputs so that
 // HBM latency overlaps the conv; the state is streamed once per token.
 #include "gdn_common.h"
@@ -181,8 +195,9 @@ slab_kernel(const DecodeParams p, const DecodeWs ws) {
     // their loads are complete: an LDS-only barrier, which leaves the state loads in flight.
     lds_barrier();
 
-    // Every thread's reads of the q/k conv history are complete: count this workgroup in.
-    // The result is needed only after the column updates, so its round trip overlaps them.
+    // Every thread's reads of the q/k conv history are complete (fact 1 of the hand-off in
+    // the file header): count this workgroup in. The result is needed only after the column
+    // updates, so its round trip overlaps them.
     int old = 0;
     if (tid == 0) old = atomicAdd(counters + (size_t)bseq * L.h_k + src, 1);
     const float inv_q = L.q_scale / sqrtf(scal_s[0] + L.l2_eps);
@@ -440,7 +455,7 @@ void launch_decode(const ix_gdn_cfg* cfg, int B, const DecodeParams& p, const De
     } else if (ws && every_src_used(cfg)) {
         const dim3 grid((unsigned)(2 * cfg->h_v), (unsigned)B);
         const long long nwg = 2LL * cfg->h_v * B;
-        const int cus = device_cu_count();
+        const int cus = device_cu_count(s);
         const unsigned lds = nwg >= (long long)kSlabCapPerCu * cus ? kSlabLdsReserve : 0;
         if (nwg <= cus) {                                     // B <= 4 at h_v = 32
             constexpr int NT = kSmallGridThreads;
@@ -473,7 +488,7 @@ extern "C" int ix_gdn_channels(const ix_gdn_cfg* c) {
     return c ? 2 * c->h_k * c->d_k + c->h_v * c->d_v : 0;
 }
 
-extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.4.0 gfx950"; }
+extern "C" const char* ix_gdn_version(void) { return "ixgdn 0.5.0 gfx950"; }
 
 // Shared validation of the fused layer description (also used by the prefill).
 extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c) {
@@ -577,14 +592,12 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 int* g_scratch_dev[kMaxDevices];                         // device address of `scratch`, per GPU
 
-__global__ void __launch_bounds__(256) scratch_clear_kernel(int* p, int n) {
-    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
-}
-
-// The current device's copy of `scratch`. On the first call on a device: its address (the
-// host-side name is only a stand-in for it), then a fill kernel on stream s that zeroes it
-// (it also starts zeroed at load; the kernels leave every counter at zero again).
-hipError_t noalloc_counters(hipStream_t s, int** out) {
+// The current device's copy of `scratch`: its address, taken on the first call on a device
+// (the host-side name is only a stand-in for it). The array is zero when the code object is
+// loaded (static storage), and every kernel that counts in it resets each counter it used
+// to zero, so it is all zero between calls; no call clears it, so nothing but the decode
+// kernel itself is enqueued (also when the first call happens under graph capture).
+hipError_t noalloc_counters(int** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
@@ -594,8 +607,6 @@ hipError_t noalloc_counters(hipStream_t s, int** out) {
         void* ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, s, static_cast<int*>(ptr), kNoAllocMaxGroups);
-        if ((e = hipGetLastError()) != hipSuccess) return e;
         g_scratch_dev[dev] = static_cast<int*>(ptr);
     }
     *out = g_scratch_dev[dev];
@@ -616,7 +627,7 @@ extern "C" hipError_t ix_gdn_decode_noalloc(const ix_gdn_cfg* cfg, int B, const 
         return hipGetLastError();
     }
     int* counters = nullptr;
-    if ((e = noalloc_counters(s, &counters)) != hipSuccess) return e;
+    if ((e = noalloc_counters(&counters)) != hipSuccess) return e;
     const ixg::DecodeWs ws{counters};
     ixg::launch_decode<false>(cfg, B, p, &ws, s);
     return hipGetLastError();

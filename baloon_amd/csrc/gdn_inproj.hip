@@ -64,6 +64,12 @@ __device__ __forceinline__ void store_out(const InProj& p, int row, int col, flo
     if (p.y) p.y[(size_t)row * p.N + col] = v;
 }
 
+// s_waitcnt that waits until at most N vector memory operations are outstanding, in the
+// gfx9-family field layout (gfx950 here: vmcnt in bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their maximum); another target would need its own encoding.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "wait_vmcnt encodes gfx950 s_waitcnt fields"
+#endif
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");

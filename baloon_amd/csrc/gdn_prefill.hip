@@ -1275,6 +1275,10 @@ __device__ __forceinline__ void chain_warm(const PrefillParams& p, lds_u8* sink,
 
 // s_waitcnt that waits until at most N vector memory operations are outstanding (gfx9
 // encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
+// The field layout is gfx9-family (gfx950 here); another target would need its own encoding.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "wait_vmcnt encodes gfx950 s_waitcnt fields"
+#endif
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");

@@ -626,7 +626,7 @@ extern "C" hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, 
     // the same with two): B = 64 47.5 against 48.1 us, B = 128 89.0 against 90.5; equal at
     // B = 32, slower at B = 16.
     const long long nwg = 2LL * cfg->h_v * B;
-    const unsigned lds = nwg >= 8LL * ixg::device_cu_count() ? ixg::kCommitLdsReserve : 0;
+    const unsigned lds = nwg >= 8LL * ixg::device_cu_count(s) ? ixg::kCommitLdsReserve : 0;
     hipLaunchKernelGGL(ixg::window_commit_kernel, dim3((unsigned)(2 * cfg->h_v), (unsigned)B), dim3(ixg::kThreads),
                        lds, s, p);
     return hipGetLastError();

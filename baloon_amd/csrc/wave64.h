@@ -8,6 +8,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+// Every kernel here is written for gfx950 alone: wave64, the gfx950 MFMA shapes and
+// transposing LDS reads, hand-encoded s_waitcnt fields, and a decode counter hand-off that
+// relies on this target's in-order wave issue (see gdn_decode.hip).
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "libixgdn device code targets gfx950 only"
+#endif
+
 namespace ixg {
 
 constexpr int kWave = 64;

@@ -138,8 +138,9 @@ hipError_t ix_gdn_decode(const ix_gdn_cfg* cfg, int B, const uint16_t* x, uint16
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
  * reference. It runs the kernel ix_gdn_decode runs with a workspace, with the group counters
  * in a library-owned static device array (one copy per GPU, 256 KiB, held until the process
- * ends; found and cleared on the first call on each device) instead of a caller workspace,
- * and calls no allocating routine. Requires B * h_k <= 65536 (else hipErrorInvalidValue,
+ * ends; zero when the library is loaded, its address looked up on the first call on each
+ * device) instead of a caller workspace, and calls no allocating routine; each call enqueues
+ * the decode kernel only, so it may be captured into a HIP graph, first call included. Requires B * h_k <= 65536 (else hipErrorInvalidValue,
  * before any launch). Every call in this process on one GPU shares that GPU's array, which
  * each call leaves all zero: calls that overlap on one GPU (on two streams, or from two host
  * threads) race, so the caller must order them, e.g. on one stream. Arguments otherwise as
@@ -276,8 +277,10 @@ hipError_t ix_mmvq_q8_0(const void* weights, const void* x_q8_1, float* y, int n
  * for each 32 consecutive values, d = max|x| / 127 (IEEE division), qs = roundf(x / d) (0 when
  * d is 0), s = the sum of the 32 values in xor-butterfly order (16, 8, 4, 2, 1),
  * d and s stored as fp16 (RNE). The gated calls' y_q8_1 output goes through the same device
- * function, so it equals this quantiser applied to their fp32 y, byte for byte. Requires
- * n > 0, n % 32 == 0, 4-byte aligned x and y_q8_1, finite x. */
+ * function, so it equals this quantiser applied to their fp32 y, byte for byte. d and s are
+ * clamped to fp16's largest finite value 65504 before the conversion (a block with
+ * max|x| > 127 * 65504 gets d = 65504 and codes saturated at +-127; smaller blocks are
+ * unaffected). Requires n > 0, n % 32 == 0, 4-byte aligned x and y_q8_1, finite x. */
 hipError_t ix_q8_1_quantize(const float* x, void* y_q8_1, long long n, hipStream_t s IX_GDN_DEFAULT_STREAM);
 
 /* Output width N of the layer's input projection: C + h_v*d_v + 2*h_v (x | z | a | b), or 0
@@ -294,10 +297,17 @@ hipError_t ix_gdn_in_proj(const ix_gdn_cfg* cfg, int B, int hidden, const uint16
                           uint16_t* x, uint16_t* z, uint16_t* a, uint16_t* b, float* y,
                           hipStream_t s IX_GDN_DEFAULT_STREAM);
 
-/* Library version string. */
+/* Library version string ("ixgdn 0.5.0 gfx950"). 0.5.0: ix_gdn_out_gate ends with y_q8_1, so
+ * callers compiled against an older header must be rebuilt. */
 const char* ix_gdn_version(void);
 
 #ifdef __cplusplus
+}
+/* The reference declares its Q8_0 launcher in namespace ix_mmvq (src/ix_mmvq_wave.cu:120-123),
+ * and its caller spells it ix_mmvq::ix_mmvq_q8_0 (tests/test_mmvq_wave.cu:46); that spelling
+ * names the C-linkage entry point above. */
+namespace ix_mmvq {
+using ::ix_mmvq_q8_0;
 }
 #endif
 #endif /* IX_GDN_H */

@@ -94,6 +94,9 @@ def q8_0_ref(wd, wq, xd, xq):
     return y, sc
 
 
+HALF_MAX = np.float32(65504.0)        # largest finite fp16 value
+
+
 def q8_1_quantize(x) -> np.ndarray:
     """fp32 values [n] (n % 32 == 0) -> q8_1 bytes [n / 32 * 36], per 32 consecutive values:
     d = max|x| / 127 in fp32 (IEEE division, src/ix_q81_div.h:8-9), qs = roundf(x / d) with the
@@ -104,20 +107,26 @@ def q8_1_quantize(x) -> np.ndarray:
     Pinning: the division and rounding rule is the reference's (ix_q81_div.h); the block
     layout its Q8_0 product's (src/ix_mmvq_wave.cu:20-24); the q = 0 rule and the s term are
     ggml's. The Q8_0 product reads only d and qs, so s is "parity unpinned" against the
-    reference (checked here against a float64 sum and the butterfly order only)."""
+    reference (checked here against a float64 sum and the butterfly order only).
+    Range: d is clamped to fp16's largest finite value 65504 (with the codes then saturating
+    at +-127) and s to [-65504, 65504] before the fp16 conversion; below max|x| = 127 * 65504
+    the clamps change nothing. The reference names such a clamp (q8_1_finite,
+    ix_q81_div.h:9) without defining it: this rule is the library's own, parity unpinned,
+    pinned by the known answers in tests/test_oracle_proj.py."""
     x = np.asarray(x, np.float32).reshape(-1, 32)
     amax = np.abs(x).max(axis=1)
-    d = (amax / np.float32(127.0)).astype(np.float32)
-    with np.errstate(divide="ignore", invalid="ignore"):
+    d = np.minimum((amax / np.float32(127.0)).astype(np.float32), HALF_MAX).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         t = (x / d[:, None]).astype(np.float32)
         r = np.sign(t).astype(np.float64) * np.floor(np.abs(t).astype(np.float64) + 0.5)
-    q = np.where(d[:, None] == 0, 0.0, r).astype(np.int8)
+    q = np.where(d[:, None] == 0, 0.0, np.clip(r, -127.0, 127.0)).astype(np.int8)
     s = x.copy()
     idx = np.arange(32)
-    for off in (16, 8, 4, 2, 1):
-        s = (s + s[:, idx ^ off]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        for off in (16, 8, 4, 2, 1):
+            s = (s + s[:, idx ^ off]).astype(np.float32)
     dh = d.astype(np.float16).view(np.uint16)[:, None]
-    sh = s[:, 0].astype(np.float16).view(np.uint16)[:, None]
+    sh = np.clip(s[:, 0], -HALF_MAX, HALF_MAX).astype(np.float16).view(np.uint16)[:, None]
     return pack_q8_1(dh, q[:, None, :], sh)
 
 

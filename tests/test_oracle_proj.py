@@ -104,3 +104,30 @@ def test_q8_1_quantize_bounds_and_sum():
     # fp32 summation error, then one fp16 rounding (relative 2^-11, or half the subnormal step)
     tol = 32 * 2.0 ** -23 * np.abs(x).astype(np.float64).sum(axis=1) + np.abs(ref) * 2.0 ** -11 + 2.0 ** -25
     assert (np.abs(s.view(np.float16).astype(np.float64) - ref) <= tol).all()
+
+
+def test_q8_1_quantize_range_clamps():
+    # Block 0: max|x| = 1e7, so max|x| / 127 = 78740.16 exceeds fp16's 65504: d is stored as
+    # 65504 and the codes saturate (1e7 / 65504 = 152.7 -> 127, 3 * 65504 -> 3 exactly); the sum
+    # 1e7 - 1e7 + 196512 = 196512 is stored as 65504, not inf. Block 1: a sum past fp32's range
+    # (two 3e38) is stored as 65504 too. Block 2: max|x| = 127 * 65504 exactly, the largest
+    # block the clamp leaves alone (d = 65504 from the division itself, codes unsaturated).
+    x = np.zeros(96, np.float32)
+    x[:4] = [1e7, -1e7, 3 * 65504.0, -65504.0 * 0.5]
+    x[32:34] = [3e38, 3e38]
+    x[64:66] = [127 * 65504.0, -2 * 65504.0]
+    d, s, q = proj.q8_1_unpack(proj.q8_1_quantize(x))
+    h = d.view(np.float16)
+    assert np.isfinite(h).all() and np.isfinite(s.view(np.float16)).all()
+    assert h[0] == np.float16(65504.0) and h[1] == np.float16(65504.0) and h[2] == np.float16(65504.0)
+    np.testing.assert_array_equal(q[0][:4], [127, -127, 3, -1])            # -0.5 rounds away from zero
+    assert s.view(np.float16)[0] == np.float16(65504.0) and s.view(np.float16)[1] == np.float16(65504.0)
+    np.testing.assert_array_equal(q[1][:2], [127, 127])
+    np.testing.assert_array_equal(q[2][:2], [127, -2])
+    # below the bound nothing changes: the unclamped rule on a block with max|x| = 8e6
+    y = np.zeros(32, np.float32)
+    y[:3] = [8e6, -4e6, 1.0]
+    dy, _, qy = proj.q8_1_unpack(proj.q8_1_quantize(y))
+    d32 = np.float32(8e6) / np.float32(127.0)
+    assert dy[0] == d32.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(qy[0][:3], [127, np.int8(np.round(np.float32(-4e6) / d32)), 0])

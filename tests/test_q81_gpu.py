@@ -41,6 +41,13 @@ def test_quantize_matches_oracle(nb):
         x[2, :4] = [127.0, 2.5, -2.5, -0.5]                            # exact ties: d = 1
         x[3] = 0.0
         x[3, :2] = [1e-44, -1e-45]                                     # d = max/127 underflows to 0
+    if nb > 6:
+        x[4] = 0.0
+        x[4, :4] = [1e7, -1e7, 3 * 65504.0, -0.5 * 65504.0]            # d clamped to 65504, codes saturate
+        x[5] = 0.0
+        x[5, :2] = [3e38, 3e38]                                        # fp32 sum overflows: s clamped
+        x[6] = 0.0
+        x[6, :2] = [127 * 65504.0, -2 * 65504.0]                       # the largest unclamped d
     got = quantize(dev(x.reshape(-1)))
     want = proj.q8_1_quantize(x.reshape(-1))
     np.testing.assert_array_equal(got, want)

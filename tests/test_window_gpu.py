@@ -112,6 +112,8 @@ def window_case(cfg, B, K, accepted, seed, extreme=False, mode="exact"):
     (1, [1, 0, -2, 7, 1, 1]),
     (8, [8, 5, 0, 13, 3, -1]),
     (16, [16, 3, 0, 16, 15, 7]),                      # the largest window
+    (5, [5, 2, 0, 7, 5, 1]),                          # size class 8 partly filled (k and q share a tile)
+    (12, [12, 9, 0, 13, 4, 12]),                      # size class 16 partly filled (separate k, q tiles)
 ])
 @pytest.mark.parametrize("mode", MODES)
 def test_window_verify_and_commit(K, accepted, mode):

@@ -6,8 +6,14 @@ state must be bit-identical to ix_gdn_decode with a workspace, and within the de
 tolerances of the double oracle (fp32 o within 1e-3 absolute, state max|d|/max|ref| <= 1e-4,
 conv state bit-exact). Two no-allocation calls run back to back, the second on a smaller
 batch: the first call must leave the shared counters at zero for the second to be right.
+In a fresh process (tests/noalloc_graph_child.py) the library's first call is made under
+HIP graph capture; the graph's replays must match eager ix_gdn_decode bit for bit, and eager
+no-allocation calls must leave the device's free memory unchanged.
 """
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -76,3 +82,11 @@ def test_noalloc_rejects_batches_beyond_its_array():
     args = (p, p, p, p, p, p, p, p, None, None, None)
     assert L.ix_gdn_decode_noalloc(ctypes.byref(big), 32769, *args) == bx.HIP_ERROR_INVALID_VALUE
     assert L.ix_gdn_decode_noalloc(ctypes.byref(bx.make_cfg(d_k=64)), 1, *args) == bx.HIP_ERROR_INVALID_VALUE
+
+
+def test_noalloc_first_call_under_graph_capture_in_a_fresh_process():
+    child = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_graph_child.py")
+    r = subprocess.run([sys.executable, "-u", child], capture_output=True, text=True, timeout=110)
+    print(r.stdout)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr
+    assert r.stdout.count("bit-identical to eager ix_gdn_decode") == 3
