@@ -34,7 +34,7 @@ EXPORTS = (
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
     "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_decode_window_mfma", "ix_gdn_commit_window",
     "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
-    "ix_gdn_version", "ix_gdn_decode_noalloc", "ix_q8_1_quantize",
+    "ix_gdn_version", "ix_gdn_decode_noalloc", "ix_q8_1_quantize", "ix_gdn_commit_window_layers",
 )
 
 
@@ -113,6 +113,7 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_version": ([], ctypes.c_char_p),
         "ix_gdn_decode_noalloc": ([P, I, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_q8_1_quantize": ([P, P, LL, P], I),
+        "ix_gdn_commit_window_layers": ([P, I, I, I, P, P, P, P, P, P], I),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -262,6 +263,35 @@ def ix_gdn_commit_window(cfg: Cfg, B, K, accepted, x, record, conv_state, state,
     """Advance each sequence's states by its accepted prefix of the verified window."""
     return lib().ix_gdn_commit_window(ctypes.byref(cfg), B, K, _ptr(accepted), _ptr(x), _ptr(record),
                                       _ptr(conv_state), _ptr(state), _stream(s))
+
+
+def layer_pointer_table(tensors):
+    """Device array (int64 tensor on the GPU) of the device pointers of a list of tensors, the
+    per-layer table ix_gdn_commit_window_layers reads."""
+    import torch
+    ptrs = [_ptr(t) or 0 for t in tensors]
+    return torch.tensor(ptrs, dtype=torch.int64).cuda()
+
+
+def ix_gdn_commit_window_layers(cfg: Cfg, B, K, accepted, xs, records, conv_states, states, s=None) -> int:
+    """ix_gdn_commit_window for every layer in one launch. xs, records, conv_states and states
+    are the per-layer pointer tables (int64 device tensors, see layer_pointer_table), which
+    must stay alive until the launch has run, or per-layer lists of tensors: then the tables
+    are built here and the call waits for its launch, so that they outlive it."""
+    import torch
+
+    def is_table(v):
+        return isinstance(v, torch.Tensor) and v.dtype == torch.int64 and v.dim() == 1
+    built = not all(is_table(v) for v in (xs, records, conv_states, states))
+    tx, tr, tc, ts = (v if is_table(v) else layer_pointer_table(v) for v in (xs, records, conv_states, states))
+    n = tx.numel()
+    if not (tr.numel() == tc.numel() == ts.numel() == n):
+        return HIP_ERROR_INVALID_VALUE
+    rc = lib().ix_gdn_commit_window_layers(ctypes.byref(cfg), n, B, K, _ptr(accepted), _ptr(tx), _ptr(tr),
+                                           _ptr(tc), _ptr(ts), _stream(s))
+    if built and rc == HIP_SUCCESS:
+        torch.cuda.synchronize()
+    return rc
 
 
 # ---- projections ----------------------------------------------------------------------------

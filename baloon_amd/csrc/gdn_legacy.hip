@@ -9,97 +9,86 @@
 //
 // The step is the only kernel with real traffic. The reference sweeps each state column
 // twice with one thread per column (2 reads + 2 writes per element, 128 dependent strided
-// loads per thread). Here one 256-thread workgroup owns a head: every state element is
-// loaded once into registers with coalesced row loads, both contractions S^T k and S^T q
-// are reduced in one sweep (in-thread, then across the four waves through LDS), and the
-// element is written once:
-//   u = g S^T k,  d = beta (v - u),  S' = g S + k d^T,  o = S'^T q = g S^T q + d (k . q).
+// loads per thread) and launches ceil(S/64) x h_v 64-thread blocks. Here the columns of a
+// head are independent units of the update,
+//   u_j = g S_j . k,  d_j = beta (v_j - u_j),  S_j' = g S_j + d_j k,  o_j = g S_j . q + d_j (k . q)
+// (the output identity gives both contractions in one sweep), so a 256-thread workgroup
+// owns a 32-column slice of one head: each thread holds one column of every eighth row in
+// registers (every wave load is two 128-byte row segments), each element is read once and
+// written once, and the two column sums are reduced in-thread and then over the slice's 8
+// row groups through LDS. At the reference's shapes (S = 128, h_v = 48) that is 192
+// workgroups instead of 48.
 #include "ix_gdn.h"
 #include "wave64.h"
 
 namespace ixg {
 namespace {
 
-constexpr int kStepThreads = 256;                     // 4 waves per head
-constexpr int kStepWaves = kStepThreads / kWave;
+constexpr int kStepThreads = 256;
 constexpr int kStepMaxS = 128;
-constexpr int kStepRows = kStepMaxS / kStepWaves;     // rows per thread (row i = wave + 4*m)
-constexpr int kStepCols = kStepMaxS / kWave;          // columns per lane (j = lane + 64*c)
+constexpr int kStepSlice = 32;                               // columns per workgroup
+constexpr int kStepGroups = kStepThreads / kStepSlice;       // 8 row groups
+constexpr int kStepRows = kStepMaxS / kStepGroups;           // 16 rows per thread (i = r + 8 m)
 
 __global__ void __launch_bounds__(kStepThreads)
 step_kernel(float* __restrict__ state, const float* __restrict__ q, const float* __restrict__ k,
             const float* __restrict__ v, const float* __restrict__ gate, const float* __restrict__ beta,
             float* __restrict__ o, int S, int h_k, int h_v) {
     __shared__ float ks[kStepMaxS], qs[kStepMaxS];
-    __shared__ float red[2][kStepWaves][kStepMaxS];
-    __shared__ float kq_part[kStepWaves];
+    __shared__ float red[2][kStepGroups][kStepSlice];
+    __shared__ float kq_part[kStepThreads / kWave];
 
     const int h = blockIdx.x;
     const int src = h % h_k;                           // modulo head pairing, src/ix_gdn.cu:38
     const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+    const int jj = tid & (kStepSlice - 1), r = tid / kStepSlice;
+    const int j = blockIdx.y * kStepSlice + jj;
+    const bool col = j < S;
     const size_t row_stride = (size_t)h_v * S;         // layout [S][h_v][S], src/ix_gdn.cu:47-48
-    float* base = state + (size_t)h * S;
+    float* base = state + (size_t)h * S + j;
 
     // Issue every state load of this thread first; they overlap the staging below.
-    float s[kStepRows][kStepCols];
+    float s[kStepRows];
 #pragma unroll
     for (int m = 0; m < kStepRows; ++m) {
-        const int i = w + kStepWaves * m;
-#pragma unroll
-        for (int c = 0; c < kStepCols; ++c) {
-            const int j = lane + kWave * c;
-            s[m][c] = (i < S && j < S) ? base[(size_t)i * row_stride + j] : 0.0f;
-        }
+        const int i = r + kStepGroups * m;
+        s[m] = (col && i < S) ? base[(size_t)i * row_stride] : 0.0f;
     }
     if (tid < S) { ks[tid] = k[(size_t)src * S + tid]; qs[tid] = q[(size_t)src * S + tid]; }
     const float g = expf(gate[h]);                     // decay, src/ix_gdn.cu:40
     const float bt = beta[h];
+    const float vj = col ? v[(size_t)h * S + j] : 0.0f;
     __syncthreads();
 
-    // k . q (needed for the output identity); wave w covers indices w*64 .. w*64+63.
+    // k . q for the output identity: wave w covers indices 64 w .. 64 w + 63.
     {
-        const int i = tid;
-        float p = (i < S && i < kStepMaxS) ? ks[i] * qs[i] : 0.0f;
-        p = wave_sum(p);
-        if (lane == 0) kq_part[w] = p;
+        const float p = (tid < S) ? ks[tid] * qs[tid] : 0.0f;
+        const float t = wave_sum(p);
+        if (lane == 0) kq_part[w] = t;
     }
-
-    float ak[kStepCols], aq[kStepCols];
-#pragma unroll
-    for (int c = 0; c < kStepCols; ++c) { ak[c] = 0.0f; aq[c] = 0.0f; }
+    float ak = 0.0f, aq = 0.0f;
 #pragma unroll
     for (int m = 0; m < kStepRows; ++m) {
-        const int i = w + kStepWaves * m;
+        const int i = r + kStepGroups * m;
         const float ki = (i < S) ? ks[i] : 0.0f, qi = (i < S) ? qs[i] : 0.0f;
-#pragma unroll
-        for (int c = 0; c < kStepCols; ++c) { ak[c] = fmaf(s[m][c], ki, ak[c]); aq[c] = fmaf(s[m][c], qi, aq[c]); }
+        ak = fmaf(s[m], ki, ak);
+        aq = fmaf(s[m], qi, aq);
     }
-#pragma unroll
-    for (int c = 0; c < kStepCols; ++c) { red[0][w][lane + kWave * c] = ak[c]; red[1][w][lane + kWave * c] = aq[c]; }
+    red[0][r][jj] = ak;
+    red[1][r][jj] = aq;
     __syncthreads();
 
-    const float kq = kq_part[0] + kq_part[1] + kq_part[2] + kq_part[3];
-    float d[kStepCols];
+    float A = 0.0f, Bq = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kStepCols; ++c) {
-        const int j = lane + kWave * c;
-        const float A = red[0][0][j] + red[0][1][j] + red[0][2][j] + red[0][3][j];
-        const float Bq = red[1][0][j] + red[1][1][j] + red[1][2][j] + red[1][3][j];
-        const float vj = (j < S) ? v[(size_t)h * S + j] : 0.0f;
-        d[c] = (vj - g * A) * bt;
-        if (w == 0 && j < S) o[(size_t)h * S + j] = fmaf(d[c], kq, g * Bq);
-    }
+    for (int g8 = 0; g8 < kStepGroups; ++g8) { A += red[0][g8][jj]; Bq += red[1][g8][jj]; }
+    const float kq = (kq_part[0] + kq_part[1]) + (kq_part[2] + kq_part[3]);
+    const float d = (vj - g * A) * bt;
+    if (r == 0 && col) o[(size_t)h * S + j] = fmaf(d, kq, g * Bq);
+    if (!col) return;
 #pragma unroll
     for (int m = 0; m < kStepRows; ++m) {
-        const int i = w + kStepWaves * m;
-        if (i < S) {
-            const float ki = ks[i];
-#pragma unroll
-            for (int c = 0; c < kStepCols; ++c) {
-                const int j = lane + kWave * c;
-                if (j < S) base[(size_t)i * row_stride + j] = fmaf(ki, d[c], s[m][c] * g);
-            }
-        }
+        const int i = r + kStepGroups * m;
+        if (i < S) base[(size_t)i * row_stride] = fmaf(ks[i], d, s[m] * g);
     }
 }
 
@@ -164,8 +153,9 @@ extern "C" {
 hipError_t ix_gdn_step(float* state, const float* q, const float* k, const float* v, const float* gate,
                        const float* beta, float* o, int S, int h_k, int h_v, hipStream_t s) {
     if (S <= 0 || h_k <= 0 || h_v <= 0 || S > ixg::kStepMaxS) return hipErrorInvalidValue;  // src/ix_gdn.cu:110
-    hipLaunchKernelGGL(ixg::step_kernel, dim3((unsigned)h_v), dim3(ixg::kStepThreads), 0, s,
-                       state, q, k, v, gate, beta, o, S, h_k, h_v);
+    const dim3 grid((unsigned)h_v, (unsigned)((S + ixg::kStepSlice - 1) / ixg::kStepSlice));
+    hipLaunchKernelGGL(ixg::step_kernel, grid, dim3(ixg::kStepThreads), 0, s, state, q, k, v, gate, beta, o, S, h_k,
+                       h_v);
     return hipGetLastError();
 }
 

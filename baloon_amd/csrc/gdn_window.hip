@@ -45,7 +45,7 @@ struct WinRec {
     float* bt;      // [B*K][h_v]
 };
 
-inline size_t rec_layout(int B, int K, int h_k, int h_v, size_t (&off)[4]) {
+__host__ __device__ inline size_t rec_layout(int B, int K, int h_k, int h_v, size_t (&off)[4]) {
     const size_t rows = (size_t)B * K;
     const size_t sz[4] = {rows * h_k * kD * 4, rows * h_v * kD * 4, rows * h_v * 4, rows * h_v * 4};
     size_t at = 0;
@@ -53,7 +53,7 @@ inline size_t rec_layout(int B, int K, int h_k, int h_v, size_t (&off)[4]) {
     return at;
 }
 
-inline WinRec rec_bind(void* base, int B, int K, int h_k, int h_v) {
+__host__ __device__ inline WinRec rec_bind(void* base, int B, int K, int h_k, int h_v) {
     size_t off[4];
     rec_layout(B, K, h_k, h_v, off);
     char* c = static_cast<char*>(base);
@@ -429,13 +429,14 @@ void launch_window_mfma(const ix_gdn_cfg* cfg, int B, const WindowParams& p, hip
 // ---------------------------------------------------------------------------------------
 // commit: grid (2 h_v, B)
 // ---------------------------------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowParams p) {
+// One workgroup's share of a commit: v head h, half tile hf, sequence bseq of the layer whose
+// x, conv state, state and record p holds.
+__device__ __forceinline__ void commit_tile(const WindowParams& p, int h, int hf, int bseq) {
     __shared__ __align__(16) float k_s[kMaxWindow][kD], v_s[kMaxWindow][kHalf];
     __shared__ float g_s[kMaxWindow], b_s[kMaxWindow];
     const Layer& L = p.L;
     const int tid = threadIdx.x, w = tid / kWave, lane = tid & (kWave - 1);
     const int half = lane >> 5, i4 = lane & 31;
-    const int hf = blockIdx.x & 1, h = blockIdx.x >> 1, bseq = blockIdx.y;
     const int src = src_of(L, h);
     const int n = min(max(p.accepted[bseq], 0), p.K);
     if (n == 0) return;                                      // nothing accepted: both states stay
@@ -529,6 +530,36 @@ __global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowPar
     }
 #pragma unroll
     for (int u = 0; u < kPairs; ++u) __builtin_nontemporal_store(s[u], tile + (size_t)(j0 + 2 * u) * (kD / 4));
+}
+
+__global__ void __launch_bounds__(kThreads) window_commit_kernel(const WindowParams p) {
+    commit_tile(p, blockIdx.x >> 1, blockIdx.x & 1, blockIdx.y);
+}
+
+// Per-layer buffers of a multi-layer commit: device arrays of n_layers pointers each.
+struct LayerPtrs {
+    const uint16_t* const* x;
+    const void* const* record;
+    uint16_t* const* conv_state;
+    float* const* state;
+};
+
+// grid (2 h_v, B, n_layers): blockIdx.z picks the layer, whose pointers come from the device
+// arrays; the work of each (layer, head, half tile, sequence) is the single-layer commit's.
+// A layer whose pointers are null or misaligned (state 16 bytes, record 256 bytes) is skipped.
+__global__ void __launch_bounds__(kThreads) window_commit_layers_kernel(const WindowParams base, const LayerPtrs lp,
+                                                                      int B) {
+    const int l = blockIdx.z;
+    WindowParams p = base;
+    p.x = lp.x[l];
+    p.conv_state = lp.conv_state[l];
+    p.state = lp.state[l];
+    void* rec = const_cast<void*>(lp.record[l]);
+    if (!p.x || !p.conv_state || !p.state || !rec || (reinterpret_cast<uintptr_t>(p.state) & 15) ||
+        (reinterpret_cast<uintptr_t>(rec) & 255))
+        return;
+    p.rec = rec_bind(rec, B, p.K, p.L.h_k, p.L.h_v);
+    commit_tile(p, blockIdx.x >> 1, blockIdx.x & 1, blockIdx.y);
 }
 
 }  // namespace
@@ -629,5 +660,27 @@ extern "C" hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, 
     const unsigned lds = nwg >= 8LL * ixg::device_cu_count(s) ? ixg::kCommitLdsReserve : 0;
     hipLaunchKernelGGL(ixg::window_commit_kernel, dim3((unsigned)(2 * cfg->h_v), (unsigned)B), dim3(ixg::kThreads),
                        lds, s, p);
+    return hipGetLastError();
+}
+
+extern "C" hipError_t ix_gdn_commit_window_layers(const ix_gdn_cfg* cfg, int n_layers, int B, int K,
+                                                  const int32_t* accepted, const uint16_t* const* x,
+                                                  const void* const* record, uint16_t* const* conv_state,
+                                                  float* const* state, hipStream_t s) {
+    const hipError_t e = ix_gdn_check_cfg_(cfg);
+    if (e != hipSuccess) return e;
+    if (n_layers <= 0 || n_layers > 65535 || B <= 0 || B > 65535 || K <= 0 || K > ixg::kMaxWindow)
+        return hipErrorInvalidValue;
+    if (cfg->head_map == IX_GDN_HEAD_MOD && cfg->h_v < cfg->h_k) return hipErrorInvalidValue;
+    if (!accepted || !x || !record || !conv_state || !state) return hipErrorInvalidValue;
+    ixg::WindowParams p{};
+    p.L = ixg::make_layer(cfg, nullptr, nullptr, nullptr);
+    p.K = K;
+    p.accepted = accepted;
+    const ixg::LayerPtrs lp{x, record, conv_state, state};
+    const long long nwg = 2LL * cfg->h_v * B * n_layers;
+    const unsigned lds = nwg >= 8LL * ixg::device_cu_count(s) ? ixg::kCommitLdsReserve : 0;
+    hipLaunchKernelGGL(ixg::window_commit_layers_kernel, dim3((unsigned)(2 * cfg->h_v), (unsigned)B, (unsigned)n_layers),
+                       dim3(ixg::kThreads), lds, s, p, lp, B);
     return hipGetLastError();
 }

@@ -61,10 +61,11 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true",
                     help="skip the single-core CPU samples (the multi-core replays, which gate the run, always run)")
     ap.add_argument("--legs", default="all",
-                    help="comma-separated subset of decode,gated,window,in_proj,latency,prefill,ceiling for "
+                    help="comma-separated subset of decode,gated,window,in_proj,latency,prefill,prefill_varlen,"
+                         "legacy,ceiling for "
                          "profiling passes; the result line needs all of them (the default)")
     a = ap.parse_args()
-    known = ("decode", "gated", "window", "in_proj", "latency", "prefill", "ceiling")
+    known = ("decode", "gated", "window", "in_proj", "latency", "prefill", "prefill_varlen", "legacy", "ceiling")
     a.legs = set(known) if a.legs == "all" else set(a.legs.split(","))
     if not a.legs <= set(known):
         ap.error(f"--legs: unknown {sorted(a.legs - set(known))}")
@@ -305,6 +306,70 @@ class CpuBaselineLeg:
         e_o = self.check_bf16_out("prefill o", o_gpu, o)
         return dict(state_rel_err=rel, o_err=e_o)
 
+    def varlen_data(self):
+        """Configuration 4's packed prefill inputs (seed 0x6D4E0004): 32 sequences of lengths
+        U[1, 2048], initial states N(0, 0.02)."""
+        if "varlen_data" not in self.record:
+            inp, cfg = self.inputs, self.cfg
+            seed = inp.seed_for(4)
+            cu = inp.varlen(seed, 32, 1, 2048)
+            T = int(cu[-1])
+            self.record["varlen_data"] = dict(cu=cu, T=T, params=inp.layer_params(cfg, seed),
+                                              tokens=inp.token_inputs(cfg, seed, T),
+                                              st0=inp.initial_states(cfg, seed, 32))
+        return self.record["varlen_data"]
+
+    def gate_prefill_varlen(self, V, cs_gpu, st_gpu, o_gpu):
+        p, tok, st0 = V["params"], V["tokens"], V["st0"]
+        t0 = time.perf_counter()
+        cs, st, o = self.oracle.prefill(self.cfg, V["cu"], tok["x"], st0["conv_state"], p["w"], tok["a"], tok["b"],
+                                        p["A_log"], p["dt_bias"], st0["state"], nthreads=self.nt)
+        sec = time.perf_counter() - t0
+        self.record["prefill_varlen"] = dict(tokens_per_s=V["T"] / sec, sec=sec)
+        self.check_equal("varlen prefill conv state", cs_gpu, cs)
+        rel = self.check_state("varlen prefill", st_gpu, st)
+        e_o = self.check_bf16_out("varlen prefill o", o_gpu, o)
+        return dict(state_rel_err=rel, o_err=e_o)
+
+    def legacy_data(self):
+        """The reference acceptance test's shapes (tests/test_gdn.cu:16-55): step S=128,
+        h_k=16, h_v=48; conv over 8192+5 channels, d_conv 4; l2 33 x 128; out_norm 48 x 128;
+        beta over 48 heads; the test's distributions, from the portable generator."""
+        g = self.inputs.Gen(0x6D4E0100)
+        S, hk, hv, C, dc = 128, 16, 48, 8192 + 5, 4
+        return dict(
+            S=S, hk=hk, hv=hv, C=C, dc=dc,
+            st=g.normal_f32(1, (S * hv * S,), 0.1), q=g.normal_f32(2, (hk * S,), 0.1),
+            k=g.normal_f32(3, (hk * S,), 0.1), v=g.normal_f32(4, (hv * S,)),
+            gate=-np.abs(g.normal_f32(5, (hv,))), beta=(0.5 + 0.4 * np.tanh(g.normal(6, (hv,)))).astype(np.float32),
+            cs=g.normal_f32(7, (C * (dc - 1),)), x=g.normal_f32(8, (C,)), w=g.normal_f32(9, (C * dc,)),
+            l2=g.normal_f32(10, (33 * 128,)), o=g.normal_f32(11, (hv * S,)), z=g.normal_f32(12, (hv * S,)),
+            nrm=(1.0 + 0.1 * g.normal(13, (S,))).astype(np.float32), b=g.normal_f32(14, (hv,), 3.0))
+
+    def gate_legacy(self, L, got):
+        """The reference test's norm max|gpu - ref| <= tol * max|ref| and tolerances
+        (tests/test_gdn.cu:10-13, :30-31, :40-41, :46, :51, :55)."""
+        o_ = self.oracle
+        errs = {}
+
+        def rel(name, g, r, tol):
+            r = np.asarray(r, np.float64)
+            e = float(np.max(np.abs(np.asarray(g, np.float64) - r)) / max(float(np.max(np.abs(r))), 1e-30))
+            errs[name] = e
+            if not e <= tol:
+                self.fail(f"legacy {name}: rel err {e:.3g} > {tol}")
+
+        rs, ro = o_.step(L["st"], L["q"], L["k"], L["v"], L["gate"], L["beta"], L["S"], L["hk"], L["hv"])
+        rel("step.o", got["step_o"], ro, 1e-4)
+        rel("step.state", got["step_st"], rs, 1e-4)
+        rcs, rout = o_.conv_step(L["cs"], L["x"], L["w"], L["C"], L["dc"])
+        rel("conv.out", got["conv_out"], rout, 1e-5)
+        self.check_equal("legacy conv.state", got["conv_cs"], rcs)
+        rel("l2", got["l2"], o_.l2_norm(L["l2"], 33, 128, 1e-6), 1e-6)
+        rel("out_norm", got["out_norm"], o_.out_norm(L["o"], L["z"], L["nrm"], L["hv"], L["S"], 1e-6), 1e-5)
+        rel("beta", got["beta"], o_.beta_gate(L["b"]), 1e-6)
+        return errs
+
     def cpu_prefill_1core(self, D, Tp=256):
         cfg, inp = self.cfg, self.inputs
         st0 = inp.initial_states(cfg, inp.seed_for(3), 1, state_std=0.0, conv_std=0.0)
@@ -418,8 +483,26 @@ def window_leg(args, D, W, O, K=4, iters=64):
     torch.cuda.synchronize()
     gate = O.gate_window(D, W, B, K, to_host(o), to_host(layers[0]["cs"]), state_host(layers[0]["state"]),
                          o_exact=o_exact)
+    # one launch committing the window in all L layers (ix_gdn_commit_window_layers): checked
+    # bit for bit against one ix_gdn_commit_window per layer on copies of the states first
+    copies = [dict(cs=Ly["cs"].clone(), st=Ly["state"].clone()) for Ly in layers]
+    for Cp in copies:
+        bx.check("ix_gdn_commit_window", bx.ix_gdn_commit_window(cfg, B, K, acc, x, rec, Cp["cs"], Cp["st"], stream))
+    t_x, t_rec = bx.layer_pointer_table([x] * L), bx.layer_pointer_table([rec] * L)
+    t_cs, t_st = bx.layer_pointer_table([Ly["cs"] for Ly in layers]), bx.layer_pointer_table([Ly["state"] for Ly in layers])
+
+    def commit_layers(i):
+        return bx.ix_gdn_commit_window_layers(cfg, B, K, acc, t_x, t_rec, t_cs, t_st, stream)
+
+    bx.check("ix_gdn_commit_window_layers", commit_layers(0))
+    torch.cuda.synchronize()
+    for l, Cp in enumerate(copies):
+        O.check_equal(f"commit_window_layers layer {l} conv state", to_host(layers[l]["cs"]), to_host(Cp["cs"]))
+        O.check_equal(f"commit_window_layers layer {l} state", to_host(layers[l]["state"]), to_host(Cp["st"]))
+    del copies
     out = {}
-    for name, fn in (("verify", verify), ("verify_exact", verify_exact), ("commit", commit)):
+    for name, fn in (("verify", verify), ("verify_exact", verify_exact), ("commit", commit),
+                     ("commit_layers", commit_layers)):
         for i in range(8):
             bx.check(name, fn(i))
         out[name] = timed(stream, fn, iters) * 1e6 / iters
@@ -429,6 +512,9 @@ def window_leg(args, D, W, O, K=4, iters=64):
     return dict(K=K, B=B, verify_us=round(out["verify"], 2), verify_exact_us=round(out["verify_exact"], 2),
                 commit_us=round(out["commit"], 2), verify_state_gbs=round(sb / out["verify"] / 1e3, 1),
                 commit_state_gbs=round(2 * sb / out["commit"] / 1e3, 1),
+                commit_layers=dict(layers=L, us=round(out["commit_layers"], 2),
+                                   state_gbs=round(2 * sb * L / out["commit_layers"] / 1e3, 1),
+                                   note="one ix_gdn_commit_window_layers launch for all layers"),
                 us_per_token_window=round((out["verify"] + out["commit"]) / K, 2), check=gate)
 
 
@@ -557,6 +643,93 @@ def prefill_leg(O, T=4096, iters=10):
                 workspace_mib=round(need / 2 ** 20, 1), check=check)
 
 
+def prefill_varlen_leg(O, iters=5):
+    """Configuration 4's prefill as serving batches it: 32 sequences of lengths U[1, 2048]
+    (35,129 tokens) packed by cu_seqlens into one ix_gdn_prefill call, initial states
+    N(0, 0.02). Each timed call gets its own copy of the initial states, prepared before the
+    timed region; the last timed call's outputs and states are checked against the CPU
+    replay."""
+    import torch
+
+    import baloon_amd as bx
+
+    cfg = bx.make_cfg()
+    V = O.varlen_data()
+    p, tok, T, n = V["params"], V["tokens"], V["T"], len(V["cu"]) - 1
+    w, A_log, dt = to_dev(p["w"]), to_dev(p["A_log"]), to_dev(p["dt_bias"])
+    x, a, b = to_dev(tok["x"]), to_dev(tok["a"]), to_dev(tok["b"])
+    cu = to_dev(V["cu"])
+    warm = 1
+    st0, cs0 = state_dev(V["st0"]["state"]), to_dev(V["st0"]["conv_state"])
+    sts = [st0.clone() for _ in range(warm + iters)]
+    css = [cs0.clone() for _ in range(warm + iters)]
+    o = torch.empty(T, cfg.h_v, 128, dtype=torch.bfloat16, device="cuda")
+    need = bx.ix_gdn_prefill_workspace_size(cfg, n, T)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def run(i):
+        return bx.ix_gdn_prefill(cfg, n, T, cu, x, css[i], w, a, b, A_log, dt, sts[i], None, o, ws, need, stream)
+
+    for i in range(warm):
+        bx.check("ix_gdn_prefill", run(i))
+    sec = timed(stream, lambda i: run(warm + i), iters) / iters
+    tflops = PREFILL_FLOP_PER_TOKEN * T / sec / 1e12
+    check = O.gate_prefill_varlen(V, to_host(css[-1]), state_host(sts[-1]), to_host(o))
+    del ws, sts, css
+    torch.cuda.empty_cache()
+    return dict(n_seq=n, T=T, tokens_per_s=round(T / sec, 1), us_per_call=round(sec * 1e6, 1),
+                mfma=dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
+                          frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)),
+                workspace_mib=round(need / 2 ** 20, 1), check=check)
+
+
+def legacy_leg(O, iters=200):
+    """The five reference launchers at the reference acceptance test's shapes
+    (tests/test_gdn.cu:16-55), microseconds per call (back-to-back calls between HIP events;
+    the step updates its state in place call after call). One call of each is checked first,
+    against the CPU oracle, with the test's norm and tolerances. The step's state traffic is
+    S * h_v * S fp32 read and written once: 6.29 MB per call."""
+    import torch
+
+    import baloon_amd as bx
+
+    L = O.legacy_data()
+    S, hk, hv, C, dc = L["S"], L["hk"], L["hv"], L["C"], L["dc"]
+    st, q, k, v, g, bt = (to_dev(L[n]) for n in ("st", "q", "k", "v", "gate", "beta"))
+    so = torch.empty(hv * S, dtype=torch.float32, device="cuda")
+    cs, x, w = to_dev(L["cs"]), to_dev(L["x"]), to_dev(L["w"])
+    cout = torch.empty(C, dtype=torch.float32, device="cuda")
+    l2 = to_dev(L["l2"])
+    o, z, nrm = to_dev(L["o"]), to_dev(L["z"]), to_dev(L["nrm"])
+    y = torch.empty(hv * S, dtype=torch.float32, device="cuda")
+    b = to_dev(L["b"])
+    stream = torch.cuda.current_stream()
+    calls = {
+        "step": lambda i: bx.ix_gdn_step(st, q, k, v, g, bt, so, S, hk, hv, stream),
+        "conv_step": lambda i: bx.ix_gdn_conv_step(cs, x, w, cout, C, dc, stream),
+        "l2_norm": lambda i: bx.ix_gdn_l2_norm(l2, 33, 128, 1e-6, stream),
+        "out_norm": lambda i: bx.ix_gdn_out_norm(o, z, nrm, y, hv, S, 1e-6, stream),
+        "beta_gate": lambda i: bx.ix_gdn_beta_gate(b, hv, stream),
+    }
+    for name, fn in calls.items():
+        bx.check(name, fn(0))
+    torch.cuda.synchronize()
+    check = O.gate_legacy(L, dict(step_o=to_host(so), step_st=to_host(st), conv_out=to_host(cout),
+                                  conv_cs=to_host(cs), l2=to_host(l2), out_norm=to_host(y), beta=to_host(b)))
+    us = {}
+    for name, fn in calls.items():
+        for i in range(5):
+            bx.check(name, fn(i))
+        us[name] = round(timed(stream, fn, iters) * 1e6 / iters, 2)
+    state_bytes = 2 * S * hv * S * 4
+    return dict(step_us=us["step"], step_state_gbs=round(state_bytes / us["step"] / 1e3, 1),
+                conv_step_us=us["conv_step"], l2_norm_us=us["l2_norm"], out_norm_us=us["out_norm"],
+                beta_gate_us=us["beta_gate"],
+                shapes="step S=128 h_k=16 h_v=48; conv C=8197 d_conv=4; l2 33x128; out_norm 48x128; beta 48",
+                check=check)
+
+
 def hbm_ceiling(nbuf=4, mib=128, iters=20):
     """Measured in-place read+write rate of the box: torch's x.mul_(1) over nbuf rotated
     128 MiB buffers (the decode state's traffic pattern, MALL defeated)."""
@@ -607,6 +780,10 @@ def partial_run(args, O):
         out["decode_b1_us_per_token"], out["decode_b1_us_per_token_graph"] = latency_leg(O)
     if "prefill" in args.legs:
         out["prefill"] = prefill_leg(O)
+    if "prefill_varlen" in args.legs:
+        out["prefill_varlen"] = prefill_varlen_leg(O)
+    if "legacy" in args.legs:
+        out["legacy"] = legacy_leg(O)
     if "ceiling" in args.legs:
         out["hbm_inplace_ceiling_gbs"] = hbm_ceiling()
     if O.failures:
@@ -629,7 +806,7 @@ def main():
     torch.cuda.synchronize()
     O = CpuBaselineLeg()
     legs = args.legs
-    if legs != {"decode", "gated", "window", "in_proj", "latency", "prefill", "ceiling"}:
+    if legs != {"decode", "gated", "window", "in_proj", "latency", "prefill", "prefill_varlen", "legacy", "ceiling"}:
         partial_run(args, O)
         return
     D = O.decode_data(args.batch, args.layers, args.inputs)
@@ -640,6 +817,8 @@ def main():
     ip = in_proj_leg(args, O)
     lat_eager, lat_graph = latency_leg(O)
     pf = prefill_leg(O)
+    pv = prefill_varlen_leg(O)
+    leg = legacy_leg(O)
     ceiling = hbm_ceiling()
 
     # the CPU replay of the timed decode sequence: the CPU baseline, and the decode gate
@@ -651,7 +830,9 @@ def main():
                        f"({args.layers} layers) in {O.record['decode']['sec']:.1f} s on {O.nt} threads "
                        "(oracle/gdn_oracle.c, double)"),
                prefill_tokens_per_s=round(O.record["prefill"]["tokens_per_s"], 1),
-               prefill_sample=f"one sequence of {pf['T']} tokens, token-by-token recurrence on {O.nt} threads")
+               prefill_sample=f"one sequence of {pf['T']} tokens, token-by-token recurrence on {O.nt} threads",
+               prefill_varlen_tokens_per_s=round(O.record["prefill_varlen"]["tokens_per_s"], 1),
+               prefill_varlen_sample=f"configuration 4's {pv['n_seq']} sequences ({pv['T']} tokens) on {O.nt} threads")
     if not args.no_cpu:
         v1, n1 = O.cpu_decode_1core(D, args)
         cpu.update(value_1core=round(v1, 1), sample_1core=f"{n1} steps of B={args.batch} on 1 thread",
@@ -695,6 +876,8 @@ def main():
         "spec_window": win,
         "in_proj": ip,
         "prefill": pf,
+        "prefill_varlen": pv,
+        "legacy": leg,
         "correctness": dict(gated="every leg checked against the CPU replay (oracle/); tolerances: fp32 o 1e-3 "
                                   "abs beyond bf16 rounding, state max|d|/max|ref| 1e-4, conv state bit-exact",
                             decode=dcheck),

@@ -238,6 +238,19 @@ hipError_t ix_gdn_commit_window(const ix_gdn_cfg* cfg, int B, int K, const int32
                                 const void* record, uint16_t* conv_state, float* state,
                                 hipStream_t s IX_GDN_DEFAULT_STREAM);
 
+/* Commit one window in every GDN layer of a model, in one launch (the upstream layer-batched
+ * commit the reference's project notes describe, STRATA_COMMITS_FULL.txt:3556; no counterpart
+ * in the reference's sources). accepted [B] as for ix_gdn_commit_window, shared by the
+ * layers; x, record, conv_state and state are DEVICE arrays of n_layers pointers, entry l
+ * being what ix_gdn_commit_window would take for layer l (each state 16-byte and each record
+ * 256-byte aligned; a layer whose pointers are null or misaligned is left untouched). The
+ * result is bit-identical to n_layers ix_gdn_commit_window calls. Requires 1 <= n_layers <=
+ * 65535 and the same description requirements as ix_gdn_commit_window. */
+hipError_t ix_gdn_commit_window_layers(const ix_gdn_cfg* cfg, int n_layers, int B, int K, const int32_t* accepted,
+                                       const uint16_t* const* x, const void* const* record,
+                                       uint16_t* const* conv_state, float* const* state,
+                                       hipStream_t s IX_GDN_DEFAULT_STREAM);
+
 /* ---------------------------------------------------------------------------------------
  * Projections feeding the layer
  * --------------------------------------------------------------------------------------- */

@@ -252,3 +252,20 @@ def test_q8_1_validation_without_launch():
     assert L.ix_q8_1_quantize(None, a, 64, None) == INVALID
     assert L.ix_q8_1_quantize(a + 2, a, 64, None) == INVALID      # fp32 alignment
     assert L.ix_q8_1_quantize(a, a + 2, 64, None) == INVALID      # block alignment
+
+
+def test_commit_layers_validation_without_launch():
+    # ix_gdn_commit_window_layers refuses bad counts and null tables before any launch.
+    cfg = bx.make_cfg()
+    L = bx.lib()
+    p = ctypes.c_void_p(1 << 20)
+    args = (p, p, p, p, p, None)
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(cfg), 0, 2, 4, *args) == bx.HIP_ERROR_INVALID_VALUE
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(cfg), 2, 2, 17, *args) == bx.HIP_ERROR_INVALID_VALUE
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(cfg), 2, 0, 4, *args) == bx.HIP_ERROR_INVALID_VALUE
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(cfg), 2, 2, 4, None, p, p, p, p, None) == \
+        bx.HIP_ERROR_INVALID_VALUE
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(cfg), 2, 2, 4, p, p, p, None, p, None) == \
+        bx.HIP_ERROR_INVALID_VALUE
+    assert L.ix_gdn_commit_window_layers(ctypes.byref(bx.make_cfg(d_k=64)), 2, 2, 4, *args) == \
+        bx.HIP_ERROR_INVALID_VALUE

@@ -173,3 +173,40 @@ def test_window_then_decode_continues():
         assert float(np.max(np.abs(host(od) - ro))) <= TOL_O_ABS
     np.testing.assert_array_equal(host(d_cs), rcs)
     assert oracle.rel_err(state_from_dev(d_st), rst) <= TOL_STATE_REL
+
+
+@pytest.mark.parametrize("kw", [dict(), dict(d_conv=3, h_k=2, h_v=6, head_map=1)])
+def test_commit_layers_matches_per_layer_commits(kw):
+    # ix_gdn_commit_window_layers over 4 layers (each with its own parameters, window inputs,
+    # record, conv state and state) must leave every layer bit-identical to one
+    # ix_gdn_commit_window call per layer; a fifth table entry with a null state is skipped.
+    torch = _torch()
+    cfg = bx.make_cfg(**kw)
+    B, K, nl = 6, 4, 4
+    acc = dev(np.array([0, 1, 2, 3, 4, 9], np.int32))
+    layers = []
+    for l in range(nl):
+        seed = inputs.seed_for(2) + 700 + 13 * l
+        p = inputs.layer_params(cfg, seed)
+        st = inputs.initial_states(cfg, seed, B)
+        tok = inputs.token_inputs(cfg, seed, B * K)
+        x, a, b = (dev(tok[n].reshape(B, K, -1)) for n in ("x", "a", "b"))
+        cs, s = dev(st["conv_state"]), state_to_dev(st["state"])
+        rec = torch.zeros(bx.ix_gdn_window_record_size(cfg, B, K), dtype=torch.uint8, device="cuda")
+        assert bx.ix_gdn_decode_window_mfma(cfg, B, K, x, cs, dev(p["w"]), a, b, dev(p["A_log"]),
+                                            dev(p["dt_bias"]), s, None, None, rec) == 0
+        layers.append(dict(x=x, rec=rec, cs1=cs.clone(), st1=s.clone(), cs2=cs.clone(), st2=s.clone()))
+    for L in layers:
+        assert bx.ix_gdn_commit_window(cfg, B, K, acc, L["x"], L["rec"], L["cs1"], L["st1"]) == 0
+    spare_cs, spare_x, spare_rec = layers[0]["cs2"].clone(), layers[0]["x"], layers[0]["rec"]
+    spare_before = host(spare_cs).copy()
+    tables = [bx.layer_pointer_table([L[n] for L in layers] + [extra])
+              for n, extra in (("x", spare_x), ("rec", spare_rec), ("cs2", spare_cs))]
+    st_table = torch.tensor([L["st2"].data_ptr() for L in layers] + [0], dtype=torch.int64).cuda()
+    assert bx.ix_gdn_commit_window_layers(cfg, B, K, acc, tables[0], tables[1], tables[2], st_table) == 0
+    torch.cuda.synchronize()
+    for l, L in enumerate(layers):
+        np.testing.assert_array_equal(host(L["cs2"]), host(L["cs1"]), err_msg=f"layer {l} conv state")
+        np.testing.assert_array_equal(host(L["st2"]), host(L["st1"]), err_msg=f"layer {l} state")
+    np.testing.assert_array_equal(host(spare_cs), spare_before, err_msg="the skipped entry was written")
+
