@@ -9,35 +9,33 @@
 // (d_k x d_v), unrolling S_t = g_t S_{t-1} + k_t d_t^T with
 // d_t = beta_t (v_t - g_t S_{t-1}^T k_t) gives
 //   A[t][s] = beta_t exp(G_t - G_s) (k_t . k_s)            (s < t)
-//   T       = (I + A)^-1                                    (unit lower triangular)
-//   W       = T diag(beta Gam) K,    U = T diag(beta) V     (64 x 128 each)
-//   D       = U - W S                                       (rows d_t)
+//   T'      = (I + A)^-1 diag(beta)                         (lower triangular)
+//   D       = T' (V - diag(Gam) K S)                        (rows d_t)
 //   M[t][s] = exp(G_t - G_s) (q_t . k_s)                    (s <= t)
 //   O       = diag(Gam) Q S + M D
 //   S'      = Gam_last S + K^T diag(exp(G_last - G_s)) D
-// Only differences G_t - G_s with t >= s are exponentiated, so no intermediate overflows
-// however strong the decay (Gam_t itself may underflow to 0, which is its correct value).
+// (D is the WY form's U - W S with U = T' V and W = T' diag(Gam) K, applied to S without
+// forming W.) Only differences G_t - G_s with t >= s are exponentiated, so no intermediate
+// overflows however strong the decay (Gam_t itself may underflow to 0, its correct value).
 //
 // Kernels, in stream order:
 //   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
 //                  the chunk table (sequence and first token of each chunk); not launched
 //                  for a single sequence, whose geometry the kernels derive from cu[0], cu[1]
-//   qk_kernel      per (chunk, q/k head): conv (history from conv_state at sequence starts)
-//                  and L2 norms of q and k; K K^T and Q K^T (lower block triangle) once for
-//                  all the v heads mapped to the q/k head, stored raw; K^T and Q written as
-//                  split-bf16 MFMA fragments
-//   v_kernel       per (chunk, v head): decay factors and beta, v rows, A and M from the raw
-//                  products, T = (I + A)^-1 (diagonal blocks by substitution, the rest by
-//                  block forward substitution), U = T diag(beta) V by block forward
-//                  substitution and W = T diag(beta Gam) K; the chain's operands W
-//                  (negated, so the chain's D accumulates from U) and M as split-bf16
-//                  fragments, U^T in fp32
+//   tri_kernel     per (chunk, q/k head): conv (history from conv_state at sequence starts,
+//                  which it also copies to the workspace) and L2 norms of q and k, the K K^T
+//                  and Q K^T lower block triangles once for all the v heads mapped to the q/k
+//                  head, then per v head the decay scan and beta, A and M, T = (I + A)^-1
+//                  (diagonal blocks by substitution, the rest by block forward substitution),
+//                  and T' = T diag(beta): written as split-bf16 MFMA fragments with M and the
+//                  decay factors -- 32.5 KiB per (chunk, v head), the chain's whole operand set
 //   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
-//                  One wave carries the strip in MFMA accumulators with no barrier on its
-//                  data path; four waves compute the outputs from the S and D it hands over;
-//                  two waves copy the next chunk's W and the current chunk's K^T into LDS
-//                  with direct loads and warm L2 ahead; before the first chunk the K^T
-//                  wave writes the new rolling conv history of the pair's share of channels.
+//                  One wave carries the strip in MFMA accumulators; one rebuilds the chunk's
+//                  normalised keys from x into LDS (the state wave reads them as K for K S and,
+//                  with transposing reads, as K^T for K^T Dg); one builds the strip's v columns
+//                  and copies T' into LDS; four compute the outputs, each rebuilding its 16 q
+//                  rows from x in registers. Before the first chunk the v wave writes the new
+//                  rolling conv history of the pair's share of channels.
 // Every dense product runs on split-bf16 MFMA (three bf16 products per fp32 product, ~2^-16
 // relative error); only the 16 x 16 diagonal blocks of T are inverted in fp32 arithmetic.
 // The chunked result stays within ~1e-5 (state) of the token-by-token recurrence in double.
@@ -56,16 +54,18 @@ struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
-    uint16_t* Wf;        // [NC][h_v] -W (64 x 128) as split-bf16 A fragments
-    float* Ut;           // [NC][h_v][128][64]  U transposed (column j of U is row j)
+    uint16_t* Tf;        // [NC][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
     uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
     float* G;            // [NC][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
                          // inclusive cumulative log decay G (padded rows repeat the last)
-    uint16_t* Ktf;       // [NC][h_k] K^T (128 x 64, zero beyond the chunk length) as fragments
-    uint16_t* Qf;        // [NC][h_k] Q (64 x 128, zero beyond the chunk length) as fragments
-    v4* raw;             // [NC][h_k][4][3][2][64] raw K K^T, (Q K^T)^T triangle blocks (accumulator layout)
+    uint8_t* Kp;         // [NC][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
+    uint16_t* Qf;        // [NC][h_k] Q (64 x 128) as split-bf16 A fragments
+    float* V;            // [NC][h_v][64][128] conv outputs of the v channels (zero past the chunk end)
 };
-constexpr int kWsSections = 10;
+constexpr int kWsSections = 9;
+constexpr int kPRow = 2 * 128 + 16;                     // key plane row: 128 bf16, 16 bytes of padding
+constexpr int kKPlane = 64 * kPRow;                     // one plane (hi or lo) of 64 keys
+constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 34,816 bytes
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -74,10 +74,9 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
     const size_t NC = (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq;
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
-        sizeof(float) * NC * c->h_v * kChunk * kD, sizeof(float) * NC * c->h_v * kChunk * kD,
-        sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * 2 * kChunk,
-        sizeof(float) * NC * c->h_k * kD * kChunk, sizeof(float) * NC * c->h_k * kChunk * kD,
-        sizeof(v4) * NC * c->h_k * 4 * 3 * 2 * kWave,
+        sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk * kChunk,
+        sizeof(float) * NC * c->h_v * 2 * kChunk, (size_t)kKSlot * NC * c->h_k, sizeof(uint16_t) * NC * c->h_k * 4 * 4 * 2 * 512,
+        sizeof(float) * NC * c->h_v * kChunk * 128,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -89,13 +88,12 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.seq_lo = reinterpret_cast<int32_t*>(base + off[0]);
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
     w.chunk_rec = reinterpret_cast<int4*>(base + off[2]);
-    w.Wf = reinterpret_cast<uint16_t*>(base + off[3]);
-    w.Ut = reinterpret_cast<float*>(base + off[4]);
-    w.Mf = reinterpret_cast<uint16_t*>(base + off[5]);
-    w.G = reinterpret_cast<float*>(base + off[6]);
-    w.Ktf = reinterpret_cast<uint16_t*>(base + off[7]);
-    w.Qf = reinterpret_cast<uint16_t*>(base + off[8]);
-    w.raw = reinterpret_cast<v4*>(base + off[9]);
+    w.Tf = reinterpret_cast<uint16_t*>(base + off[3]);
+    w.Mf = reinterpret_cast<uint16_t*>(base + off[4]);
+    w.G = reinterpret_cast<float*>(base + off[5]);
+    w.Kp = reinterpret_cast<uint8_t*>(base + off[6]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[7]);
+    w.V = reinterpret_cast<float*>(base + off[8]);
     return w;
 }
 
@@ -229,9 +227,10 @@ __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGe
 // lane, so that every x access of a wave is one 256-byte row segment. Tokens tb .. tb + n - 1
 // of the chunk (n wave-uniform, 1..16); the history of the first one comes from x or, before
 // the sequence start, from the sequence's conv state ([C][dc-1] per sequence: channel ch's
-// entries, then channel ch+1's). The loads and the arithmetic are separate steps, so that a
-// wave can issue the loads well before it needs the rows (and before stores it issues in
-// between, which its later waits would otherwise include).
+// entries, then channel ch+1's).
+// The loads and the arithmetic are separate steps, so that a wave can issue the loads well
+// before it needs the rows (and before stores it issues in between, which its later waits
+// would otherwise include).
 // ---------------------------------------------------------------------------------------
 constexpr int kConvTok = 16;
 
@@ -271,9 +270,8 @@ __device__ __forceinline__ float bf16_half(uint32_t word, int half) {
     return __uint_as_float(half ? (word & 0xffff0000u) : (word << 16));
 }
 
-template <int DC>
-__device__ __forceinline__ void conv_run(const Layer& L, ConvIn<DC> in, float (&y0)[kConvTok],
-                                         float (&y1)[kConvTok]) {
+template <int DC, bool SILU>
+__device__ __forceinline__ void conv_run(ConvIn<DC> in, float (&y0)[kConvTok], float (&y1)[kConvTok]) {
     // Pin the words here: the compiler would otherwise hoist their unpacking up to the loads,
     // which then wait for the data right after issue.
 #pragma unroll
@@ -298,7 +296,7 @@ __device__ __forceinline__ void conv_run(const Layer& L, ConvIn<DC> in, float (&
         for (int i = 0; i < DC - 1; ++i) { a0 = fmaf(h0[i], w0[i], a0); a1 = fmaf(h1[i], w1[i], a1); }
         a0 = fmaf(x0, w0[DC - 1], a0);
         a1 = fmaf(x1, w1[DC - 1], a1);
-        if (L.conv_act == IX_GDN_ACT_SILU) { a0 = a0 * sigmoid_f(a0); a1 = a1 * sigmoid_f(a1); }
+        if constexpr (SILU) { a0 = a0 * sigmoid_f(a0); a1 = a1 * sigmoid_f(a1); }
         y0[t] = a0;
         y1[t] = a1;
 #pragma unroll
@@ -310,8 +308,8 @@ __device__ __forceinline__ void conv_run(const Layer& L, ConvIn<DC> in, float (&
 
 // ---------------------------------------------------------------------------------------
 // commit: the rolling conv history of channel ch after sequence s, tokens lo .. lo+len-1
-// (len > 0); run by the chain kernel, which starts after the chunk kernel has read the old
-// history
+// (len > 0); run by the chain kernel, whose other reads of the old history go to the
+// workspace copy the chunk kernel made
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ void commit_history(const PrefillParams& p, int ch, int lo, int len, int s) {
     const Layer& L = p.L;
@@ -319,12 +317,14 @@ __device__ __forceinline__ void commit_history(const PrefillParams& p, int ch, i
     // extended history [old (dc-1 values) | the sequence's inputs]; the new history is its
     // last dc-1 entries, i.e. entries len .. len+dc-2. An entry below dc-1 is old history.
     const uint16_t o0 = st[0], o1 = L.dc > 2 ? st[1] : (uint16_t)0, o2 = L.dc > 3 ? st[2] : (uint16_t)0;
+    // Entries j >= dc-1 are not stored; their token index is clamped into the sequence, so
+    // that no load reaches past its last token.
     uint16_t nw[3];
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         const int ext = len + j;                               // index into the extended history
         const int pos = ext - (L.dc - 1);                      // token position when >= 0
-        nw[j] = pos >= 0 ? p.x[(size_t)(lo + pos) * L.C + ch] : (ext == 0 ? o0 : ext == 1 ? o1 : o2);
+        nw[j] = pos >= 0 ? p.x[(size_t)(lo + min(pos, len - 1)) * L.C + ch] : (ext == 0 ? o0 : ext == 1 ? o1 : o2);
     }
     st[0] = nw[0];
     if (L.dc > 2) st[1] = nw[1];
@@ -358,15 +358,12 @@ __device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nk
 }
 
 // Fragment sizes in bf16 elements: (rows/16) x (k/32) fragments x 2 planes x 512.
-constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (W, Q)
-constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (M)
-constexpr size_t kFragKt = 8 * 2 * 2 * 512;    // 128 x 64 (K^T)
+constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (T', M)
+constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (Q)
 
 // ---------------------------------------------------------------------------------------
-// chunk-local: grid (NC, h_k), 512 threads; workgroup = (chunk, q/k head) and, one after
-// the other, the v heads mapped to that q/k head
+// chunk-local work (tri_kernel): grid (NC, h_k), 512 threads; workgroup = (chunk, q/k head)
 // ---------------------------------------------------------------------------------------
-constexpr int kKS = kD + 4;          // padded LDS row stride of the K / Q / V tiles
 constexpr int kTS = kChunk + 4;      // row stride of the A / M / T tiles
 constexpr int kChunkThreads = 512;
 
@@ -384,11 +381,6 @@ typedef short v4s __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint2 lds_tr16(const lds_u8* a) {
     typedef __attribute__((address_space(3))) v4s lds_v4s;
     return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)a));
-}
-__device__ __forceinline__ float qk_f32(const uint8_t* planes, int t, int ch) {
-    const int o = qk_off(t, ch);
-    return bf16_to_f32(*reinterpret_cast<const uint16_t*>(planes + o)) +
-           bf16_to_f32(*reinterpret_cast<const uint16_t*>(planes + kQKPlane + o));
 }
 
 // The 10 blocks (br, bc) of the 4 x 4 lower block triangle, 16 x 16 each: wave w takes
@@ -515,72 +507,90 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
     store_frag(Mf, br, bc >> 1, 2, lane, x);
 }
 
-// The chunk-local work runs as two kernels, so that each holds a fraction of the registers and
-// LDS of a single one and two workgroups share a CU (one hides the other's load latency and
-// barriers):
-//   qk_kernel (chunk, q/k head): q and k rows (conv, L2 norm, q scale) as split-bf16 planes in
-//     LDS; the lower block triangle of K K^T and Q K^T on split-bf16 MFMA, stored raw in the
-//     accumulator layout for the v kernel; K^T and Q as the chain's fragments.
-//   v_kernel (chunk, v head): decay scan and beta; v rows (conv); A and M from the raw
-//     products; M fragments; T = (I + A)^-1 by a blocked inverse; U = T diag(beta) V and
-//     W = T diag(beta Gam) K on split-bf16 MFMA (K from the K^T fragments); U^T and -W
-//     fragments for the chain.
+// Row tile mt, k-step ks of T' = T diag(sc) as a split-bf16 A fragment: lane (li, lg4) holds
+// T[16 mt + li][s] sc_s at the tokens s = 32 ks + kperm(lg4, e), zero above the diagonal
+// blocks (T in its array shared with A: diagonal blocks in place, the others mirrored, so
+// T[t][s] of block (k, J), J <= k, sits at row 16 J + t % 16, column 16 k + s % 16; the reads
+// of blocks above the diagonal land in A and are discarded).
+__device__ __forceinline__ void t_frag(const float* T_s, const float* sc, int mt, int ks, int li, int lg4, bf8& h,
+                                       bf8& l) {
+    const int s0 = 32 * ks + 4 * lg4;
+    const v4 sc0 = *reinterpret_cast<const v4*>(sc + s0), sc1 = *reinterpret_cast<const v4*>(sc + s0 + 16);
+    const float* tr = T_s + (32 * ks + li) * kTS + 16 * mt + 4 * lg4;
+    const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16 * kTS);
+    const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
+    float av[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        av[e] = live0 ? t0[e] * sc0[e] : 0.0f;
+        av[e + 4] = live1 ? t1[e] * sc1[e] : 0.0f;
+    }
+    split8(av, h, l);
+}
+
+// Decay scan of one v head over the chunk's tokens (one wave, lane = token): the inclusive
+// cumulative log decay G and beta into LDS, the chain's decay factors exp(G_last - G_t) and
+// exp(G_t) to the workspace. Rows past the chunk end add nothing (G repeats its last value)
+// and have beta = 0.
+__device__ __forceinline__ void decay_scan(const PrefillParams& p, const ChunkGeo& g, int h, size_t ch, uint16_t ra,
+                                           uint16_t rb, float* G_s, float* B_s, int lane) {
+    const Layer& L = p.L;
+    const bool ok = lane < g.len;
+    float lgt = ok ? log_gate(L, h, bf16_to_f32(ra)) : 0.0f;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const float o = __shfl_up(lgt, off, kWave);
+        if (lane >= off) lgt += o;
+    }
+    G_s[lane] = lgt;
+    B_s[lane] = ok ? sigmoid_f(bf16_to_f32(rb)) : 0.0f;
+    const float glast = __shfl(lgt, kChunk - 1, kWave);
+    float* E = p.ws.G + ch * 2 * kChunk;
+    E[lane] = expf(glast - lgt);
+    E[kChunk + lane] = expf(lgt);
+}
+
+// ---------------------------------------------------------------------------------------
+// tri_kernel: grid (NC, h_k), 512 threads; workgroup = (chunk, q/k head).
+//   1. q rows (waves 0-3) and k rows (waves 4-7): conv and L2 norm into split-bf16 planes.
+//   2. Each group of four waves (waves 0-3, waves 4-7) forms the raw K K^T and (Q K^T)^T
+//      blocks of the lower block triangle in its registers (both groups the same blocks), and
+//      its first wave the decay scan of its first v head.
+//   3. Group g takes the mapped v heads g, g + 2, ...: A into its LDS array (the planes' space)
+//      and M to its fragments, the diagonal blocks of T = (I + A)^-1 by substitution (the
+//      group's first wave), the blocks below them by block forward substitution (three
+//      waves), then T' = T diag(beta) as fragments (two per wave).
+// At a sequence's first chunk the workgroup also copies the old conv history of its q/k
+// channels and of its v heads' channels to the workspace, where the chain reads it.
 // Every barrier orders LDS only, so no wave waits for its own global stores.
-
-// The v kernel's unit (chunk, v head) of 1-D workgroup id. Workgroups are dispatched to the
-// 8 XCDs round robin (id % 8), so ids are first made XCD-major (XCD x runs units
-// x * N/8 .. (x+1) * N/8 - 1, in order), and the units walk the v heads of one q/k head one
-// after the other within a chunk: the heads that share a q/k head read the same K^T fragments
-// and raw triangle blocks, and run back to back on one XCD, where the second reads hit L2.
-__device__ __forceinline__ void v_unit(const Layer& L, int NC, int id, int& c, int& h) {
-    const long long N = (long long)NC * L.h_v, per = N / 8;
-    const long long u = id < per * 8 ? (long long)(id % 8) * per + id / 8 : id;
-    c = (int)(u / L.h_v);
-    const int k = (int)(u % L.h_v);
-    if (L.head_map != IX_GDN_HEAD_MOD) {
-        h = k;                                   // h / per_src: a q/k head's v heads are adjacent
-        return;
-    }
-    // h mod h_k: q/k head s has v heads s, s + h_k, ...; the first h_v mod h_k heads have
-    // one more than the others.
-    const int lo = L.h_v / L.h_k, r = L.h_v % L.h_k, hi = lo + (r ? 1 : 0);
-    int s, m;
-    if (k < r * hi) {
-        s = k / hi;
-        m = k % hi;
-    } else {
-        const int k2 = k - r * hi;
-        s = r + k2 / lo;
-        m = k2 % lo;
-    }
-    h = s + m * L.h_k;
-}
-
-// Raw triangle products: per (chunk, q/k head), wave w (0..3) of the triangle and its block
-// slot j (0..2, block i = w + 4 j), the K K^T then the transposed Q K^T accumulator (K of
-// block bc times Q of block br, so that it lands in M's fragment layout), one 16-byte v4 per
-// lane: [NC][h_k][4][3][2][64] v4.
-__device__ __forceinline__ size_t raw_at(size_t cs, int w, int j, int kind, int lane) {
-    return ((((cs * 4 + w) * 3 + j) * 2 + kind) * kWave + lane);
-}
-
-template <int DC>
-__global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p) {
-    __shared__ __align__(16) uint8_t planes[4 * kQKPlane];     // k hi, k lo, q hi, q lo
-    uint8_t* Kp = planes;
-    uint8_t* Qp = planes + 2 * kQKPlane;
+// ---------------------------------------------------------------------------------------
+template <int DC, bool SILU>
+__global__ void __launch_bounds__(kChunkThreads) tri_kernel(const PrefillParams p) {
+    __shared__ __align__(16) uint8_t lds[4 * kQKPlane];   // k hi, k lo, q hi, q lo; then A/T of two heads
+    __shared__ __align__(16) float G_s[2][kChunk], B_s[2][kChunk];
+    uint8_t* Kp = lds;
+    uint8_t* Qp = lds + 2 * kQKPlane;
 
     ChunkGeo g;
     const int c = blockIdx.x;
     if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
     const int src = blockIdx.y;
-    if (mapped_count(L, src) == 0) return;                     // no v head reads this q/k head
+    const int nmap = mapped_count(L, src);
+    if (nmap == 0) return;                                     // no v head reads this q/k head
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int grp = w >> 2, gw = w & 3;
     const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
-    const size_t cs = (size_t)c * L.h_k + src;
-    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);   // this wave's rows
+    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);
+
+    // The gate inputs of the group's first v head, loaded first (lane = token, clamped rows).
+    uint16_t ra = 0, rb = 0;
+    if (gw == 0) {
+        const size_t ab = (size_t)(g.t0 + min(lane, g.len - 1)) * L.h_v + mapped_head(L, src, min(grp, nmap - 1));
+        ra = p.a[ab];
+        rb = p.b[ab];
+    }
 
     // q rows (waves 0-3) and k rows (waves 4-7), 16 tokens per wave: lane l carries channels
     // 2l, 2l+1, so every x access of a wave is a 256-byte row segment and each row's norm is
@@ -590,7 +600,7 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
         ConvIn<DC> in;
         conv_load<DC>(p, g, g.lo, isk ? k_channel(L, src, c2) : q_channel(L, src, c2), tb, nt, in);
         float y0[kConvTok], y1[kConvTok];
-        conv_run<DC>(L, in, y0, y1);
+        conv_run<DC, SILU>(in, y0, y1);
         // The 16 row sums in one reduce-scatter: lane l holds the sum of row l >> 2, so one
         // rsqrt gives every row's factor, which each row then reads from lane 4 t.
         float ss[kConvTok];
@@ -609,338 +619,203 @@ __global__ void __launch_bounds__(kChunkThreads) qk_kernel(const PrefillParams p
             *reinterpret_cast<uint32_t*>(dst + kQKPlane + o) = lo;
         }
     }
-    lds_barrier();
-
-    if (w < 4) {
-        // Raw K K^T and (Q K^T)^T of this wave's triangle blocks (16x16x32 split-bf16 MFMA,
-        // operands straight from the planes: lane (li, lg4) supplies channels
-        // 32 ks + 8 lg4 .. +7 of token row li for both operands), then stored. The A and B
-        // register layouts are mirror images, so swapping the operands of Q K^T gives its
-        // transpose.
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            const int i = w + 4 * j;
-            if (i >= 10) continue;
-            v4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk;
-            int br, bc;
-            tri_block(i, br, bc);
-            const int arow = 16 * br + li, brow = 16 * bc + li;
-#pragma unroll
-            for (int ks = 0; ks < kD / 32; ++ks) {
-                const int ch = 32 * ks + 8 * lg4, oa = qk_off(arow, ch), ob = qk_off(brow, ch);
-                const bf8 akh = *reinterpret_cast<const bf8*>(Kp + oa);
-                const bf8 akl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + oa);
-                const bf8 aqh = *reinterpret_cast<const bf8*>(Qp + oa);
-                const bf8 aql = *reinterpret_cast<const bf8*>(Qp + kQKPlane + oa);
-                const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
-                const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
-                kk = mfma_bf16(akh, bkh, kk);
-                qk = mfma_bf16(bkh, aqh, qk);
-                kk = mfma_bf16(akh, bkl, kk);
-                qk = mfma_bf16(bkl, aqh, qk);
-                kk = mfma_bf16(akl, bkh, kk);
-                qk = mfma_bf16(bkh, aql, qk);
-            }
-            p.ws.raw[raw_at(cs, w, j, 0, lane)] = kk;
-            p.ws.raw[raw_at(cs, w, j, 1, lane)] = qk;
-        }
-    } else {
-        // K^T (rows i, k = token t: 8 x 2 fragments) and Q (rows t, k = i: 4 x 4 fragments)
-        // from the planes into split fragments, k in accumulator row order (kperm).
-        const int t4 = tid - 4 * kWave;
-        uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
-        // K^T with the transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group,
-        // lane j receives element j & 3 of the 8-byte reads of lanes (j >> 2) + 4 e, e = 0..3.
-        // Lane i of lane group g reads channels 16 m + 4 (i & 3) .. +3 of token
-        // 32 ks + 4 g + (i >> 2) (then of the token 16 later), so it receives channel 16 m + i
-        // at tokens 32 ks + 4 g + e (+ 16): entries e (4 + e) of its kperm fragment chunk.
-        // Each wave takes whole fragments (m, ks), f = 2 m + ks = w - 4, w, w + 4, w + 8.
-        const int ip = lane & 15, lgr = lane >> 4;
-        const lds_u8* K3 = (const lds_u8*)Kp;
-        for (int f = w - 4; f < 8 * 2; f += 4) {
-            const int m = f >> 1, ks = f & 1;
-            const int t0 = 32 * ks + 4 * lgr + (ip >> 2), c0 = 16 * m + 4 * (ip & 3);
-            const int oa = qk_off(t0, c0), ob = qk_off(t0 + 16, c0);
-            const uint2 ha = lds_tr16(K3 + oa), hb = lds_tr16(K3 + ob);
-            const uint2 la = lds_tr16(K3 + kQKPlane + oa), lb = lds_tr16(K3 + kQKPlane + ob);
-            *reinterpret_cast<u4x*>(Ktf + frag_at(m, ks, 2, 0, lane)) = u4x{ha.x, ha.y, hb.x, hb.y};
-            *reinterpret_cast<u4x*>(Ktf + frag_at(m, ks, 2, 1, lane)) = u4x{la.x, la.y, lb.x, lb.y};
-        }
-        uint16_t* Qf = p.ws.Qf + cs * kFragW;
-        for (int u = t4; u < 4 * 4 * kWave; u += 4 * kWave) {
-            const int ln = u & (kWave - 1), f = u / kWave, m = f >> 2, ks = f & 3;
-            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
-            const int oa = qk_off(row, k0), ob = qk_off(row, k0 + 16);
-            const uint2 ah = *reinterpret_cast<const uint2*>(Qp + oa), bh = *reinterpret_cast<const uint2*>(Qp + ob);
-            const uint2 al = *reinterpret_cast<const uint2*>(Qp + kQKPlane + oa);
-            const uint2 bl = *reinterpret_cast<const uint2*>(Qp + kQKPlane + ob);
-            *reinterpret_cast<u4x*>(Qf + frag_at(m, ks, 4, 0, ln)) = u4x{ah.x, ah.y, bh.x, bh.y};
-            *reinterpret_cast<u4x*>(Qf + frag_at(m, ks, 4, 1, ln)) = u4x{al.x, al.y, bl.x, bl.y};
-        }
-    }
-}
-
-// v_kernel: grid (NC, h_v), 512 threads; workgroup = (chunk, v head). Phases: decay scan and
-// beta (wave 0, lane = token) and the raw products (waves 1-3 and 0) while waves 4-7 load and
-// compute the v rows | A (to LDS) and M (to its fragments) (waves 0-3) | the four 16 x 16
-// diagonal blocks of T by substitution (wave 0) | the blocks of T below them by forward
-// substitution on the identity's block columns (waves 0-2) | U = T diag(beta) V (U^T stored
-// from the MFMA layout) and W^T = K^T diag(beta Gam) T^T, whose accumulators are the chain's
-// -W fragments as they stand, stored from registers, split evenly over the eight waves.
-// T shares its LDS array with A, which keeps the workgroup at 51 KiB of LDS and 78 VGPRs:
-// three workgroups per CU.
-template <int DC>
-__global__ void __launch_bounds__(kChunkThreads, 6) v_kernel(const PrefillParams p) {
-    __shared__ __align__(16) float lds[kChunk * kKS + kChunk * kTS];
-    float (*V_s)[kKS] = reinterpret_cast<float (*)[kKS]>(lds);        // v rows
-    float* A_s = lds + kChunk * kKS;                                   // [64][kTS]
-    float* T_s = A_s;                  // T over A: diagonal blocks in place, the others mirrored
-    __shared__ __align__(16) float G_s[kChunk], B_s[kChunk], BG_s[kChunk];
-
-    ChunkGeo g;
-    const Layer& L = p.L;
-    int c, h;
-    v_unit(L, p.NC, blockIdx.x, c, h);
-    if (!chunk_geo(p, c, g)) return;
-    const int src = src_of(L, h);
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int li = lane & 15, lg4 = lane >> 4, c2 = 2 * lane;
-    const size_t ch = (size_t)c * L.h_v + h, cs = (size_t)c * L.h_k + src;
-    const int tb = kConvTok * (w & 3), nt = min(max(g.len - tb, 0), kConvTok);
-
-    v4 kk[3], qk[3];
-    if (w < 4) {
-        uint16_t ra = 0, rb = 0;
-        if (w == 0 && lane < g.len) {
-            const size_t ab = (size_t)(g.t0 + lane) * L.h_v + h;
-            ra = p.a[ab];
-            rb = p.b[ab];
-        }
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-            kk[j] = v4{0.f, 0.f, 0.f, 0.f};
-            qk[j] = kk[j];
-            if (w + 4 * j < 10) {
-                kk[j] = p.ws.raw[raw_at(cs, w, j, 0, lane)];
-                qk[j] = p.ws.raw[raw_at(cs, w, j, 1, lane)];
-            }
-        }
-        if (w == 0) {
-            // Inclusive scan of the log decay over the chunk's tokens, beta, and the decay
-            // factors the chain reads: exp(G_last - G_t), then exp(G_t).
-            const bool ok = lane < g.len;
-            float lgt = ok ? log_gate(L, h, bf16_to_f32(ra)) : 0.0f;
-#pragma unroll
-            for (int off = 1; off < kWave; off <<= 1) {
-                const float o = __shfl_up(lgt, off, kWave);
-                if (lane >= off) lgt += o;
-            }
-            const float bt = ok ? sigmoid_f(bf16_to_f32(rb)) : 0.0f;
-            G_s[lane] = lgt;
-            B_s[lane] = bt;
-            BG_s[lane] = bt * expf(lgt);
-            const float glast = __shfl(lgt, kChunk - 1, kWave);
-            float* E = p.ws.G + ch * 2 * kChunk;
-            E[lane] = expf(glast - lgt);
-            E[kChunk + lane] = expf(lgt);
-        }
-    } else {
-        // v rows of the head, 16 tokens per wave, zero past the chunk end.
-        ConvIn<DC> vin;
-        conv_load<DC>(p, g, g.lo, v_channel(L, h, c2), tb, nt, vin);
+    // v rows of the mapped v heads (group g takes heads g, g + 2, ...), same layout of work,
+    // to the workspace as fp32 rows [64][128], zero past the chunk end.
+    for (int m = grp; m < nmap; m += 2) {
+        const int h = mapped_head(L, src, m);
+        ConvIn<DC> in;
+        conv_load<DC>(p, g, g.lo, v_channel(L, h, c2), tb, nt, in);
         float y0[kConvTok], y1[kConvTok];
-        conv_run<DC>(L, vin, y0, y1);
+        conv_run<DC, SILU>(in, y0, y1);
+        float* V = p.ws.V + ((size_t)c * L.h_v + h) * kChunk * kD + c2;
 #pragma unroll
         for (int t = 0; t < kConvTok; ++t)
-            *reinterpret_cast<float2*>(&V_s[tb + t][c2]) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
+            *reinterpret_cast<float2*>(V + (tb + t) * kD) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
     }
-    lds_barrier();
-    if (w < 4) am_head(kk, qk, G_s, B_s, A_s, p.ws.Mf + ch * kFragM, w, lane);
     lds_barrier();
 
-    // Wave 0 inverts the four unit lower-triangular diagonal blocks of I + A (lane = 16 b +
-    // column c).
-    if (w == 0) {
-        const int b = lane >> 4, cc = lane & 15;
-        const float* Ab = A_s + (16 * b) * kTS + 16 * b;
-        float x[16];
+    // The chain's key planes (row t: 128 bf16, then 16 bytes of padding; hi plane, then lo)
+    // and Q fragments (rows t, k = channel in kperm order), from the swizzled planes: every
+    // thread moves 4 of the 16-byte key chunks and 4 Q fragment chunks.
+    {
+        uint8_t* kg = p.ws.Kp + ((size_t)c * L.h_k + src) * kKSlot;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float acc = r == cc ? 1.0f : 0.0f;
-#pragma unroll
-            for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
-            x[r] = acc;
-            if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // loads hoisted 4 rows ahead at most
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + u * kChunkThreads, pl = e >> 10, t = (e >> 4) & 63, cc = e & 15;
+            *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * cc) =
+                *reinterpret_cast<const u4x*>(Kp + pl * kQKPlane + qk_off(t, 8 * cc));
         }
+        uint16_t* Qg = p.ws.Qf + ((size_t)c * L.h_k + src) * kFragW;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
+        for (int u = 0; u < 2; ++u) {
+            const int e = tid + u * kChunkThreads, ln = e & (kWave - 1), f = e / kWave, m = f >> 2, ks = f & 3;
+            const int row = 16 * m + (ln & 15), k0 = 32 * ks + 4 * (ln >> 4);      // kperm halves
+            const int oa = qk_off(row, k0), ob = qk_off(row, k0 + 16);
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) {
+                const uint2 a = *reinterpret_cast<const uint2*>(Qp + pl * kQKPlane + oa);
+                const uint2 b = *reinterpret_cast<const uint2*>(Qp + pl * kQKPlane + ob);
+                *reinterpret_cast<u4x*>(Qg + frag_at(m, ks, 4, pl, ln)) = u4x{a.x, a.y, b.x, b.y};
+            }
+        }
     }
-    lds_barrier();
-    // T below the diagonal blocks: wave j (0..2) runs column block j by forward substitution
-    // (t_column), split-bf16 products on the 16x16x16 MFMA.
-    if (w == 0) t_column<0>(A_s, T_s, lane);
-    else if (w == 1) t_column<1>(A_s, T_s, lane);
-    else if (w == 2) t_column<2>(A_s, T_s, lane);
-    lds_barrier();
 
-    // K^T fragments of row tiles 2 (w & 3) and 2 (w & 3) + 1 (the A operand of W^T below),
-    // loaded here, so that the U product below hides their latency: held from the first
-    // barrier on, they kept 32 more registers live through the inverse (90 VGPRs, two
-    // workgroups per CU instead of three).
-    const int kw = w & 3;
-    bf8 kt[2][2][2];
-    {
-        const uint16_t* Ktf = p.ws.Ktf + cs * kFragKt;
+    // Raw K K^T and (Q K^T)^T of this wave's triangle blocks (16x16x32 split-bf16 MFMA,
+    // operands straight from the planes: lane (li, lg4) supplies channels 32 ks + 8 lg4 .. +7
+    // of token row li for both operands). The A and B register layouts are mirror images, so
+    // swapping the operands of Q K^T gives its transpose.
+    v4 kk[3], qk[3];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    for (int j = 0; j < 3; ++j) {
+        kk[j] = v4{0.f, 0.f, 0.f, 0.f};
+        qk[j] = kk[j];
+        const int i = gw + 4 * j;
+        if (i >= 10) continue;
+        int br, bc;
+        tri_block(i, br, bc);
+        const int arow = 16 * br + li, brow = 16 * bc + li;
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int pl = 0; pl < 2; ++pl)
-                    kt[t][ks][pl] = *reinterpret_cast<const bf8*>(Ktf + frag_at(2 * kw + t, ks, 2, pl, lane));
+        for (int ks = 0; ks < kD / 32; ++ks) {
+            const int ch = 32 * ks + 8 * lg4, oa = qk_off(arow, ch), ob = qk_off(brow, ch);
+            const bf8 akh = *reinterpret_cast<const bf8*>(Kp + oa);
+            const bf8 akl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + oa);
+            const bf8 aqh = *reinterpret_cast<const bf8*>(Qp + oa);
+            const bf8 aql = *reinterpret_cast<const bf8*>(Qp + kQKPlane + oa);
+            const bf8 bkh = *reinterpret_cast<const bf8*>(Kp + ob);
+            const bf8 bkl = *reinterpret_cast<const bf8*>(Kp + kQKPlane + ob);
+            kk[j] = mfma_bf16(akh, bkh, kk[j]);
+            qk[j] = mfma_bf16(bkh, aqh, qk[j]);
+            kk[j] = mfma_bf16(akh, bkl, kk[j]);
+            qk[j] = mfma_bf16(bkl, aqh, qk[j]);
+            kk[j] = mfma_bf16(akl, bkh, kk[j]);
+            qk[j] = mfma_bf16(bkh, aql, qk[j]);
+        }
     }
-    // U = (T diag beta) V and W = (T diag beta Gam) K on split-bf16 MFMA (16x16x32), every
-    // wave taking a share of both of the same size. The k index (token s) runs in
-    // kperm order, the order of the K^T fragments: lane (li, lg4) of k-step ks holds tokens
-    // 32 ks + 4 lg4 .. +3 (the 16-token block 2 ks) and 32 ks + 16 + 4 lg4 .. +3 (block
-    // 2 ks + 1). T[t][s] = 0 for s > t: tile mt needs the k-steps up to mt / 2, and the blocks
-    // of T above the block diagonal (never written) are read as zeros.
-    // Row tile mt of diag(sc) T^T as an MFMA operand: lane (li, lg4) holds sc_s T[16 mt + li][s]
-    // at the tokens s of k-step ks (zero above the diagonal blocks), split.
-    auto t_frag = [&](const float* sc, int mt, int ks, bf8& h, bf8& l) {
-        const int s0 = 32 * ks + 4 * lg4;
-        const v4 sc0 = *reinterpret_cast<const v4*>(sc + s0), sc1 = *reinterpret_cast<const v4*>(sc + s0 + 16);
-        // T[16 mt + li][s] of blocks J = 2 ks, 2 ks + 1 (mirrored storage; the reads of blocks
-        // above the diagonal land in A and are discarded below).
-        const float* tr = T_s + (32 * ks + li) * kTS + 16 * mt + 4 * lg4;
-        const v4 t0 = *reinterpret_cast<const v4*>(tr), t1 = *reinterpret_cast<const v4*>(tr + 16 * kTS);
-        const bool live0 = 2 * ks <= mt, live1 = 2 * ks + 1 <= mt;
-        float av[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            av[e] = live0 ? t0[e] * sc0[e] : 0.0f;
-            av[e + 4] = live1 ? t1[e] * sc1[e] : 0.0f;
-        }
-        split8(av, h, l);
-    };
-    {
-        // U: T diag(beta) as the A operand, the V columns 16 w .. 16 w + 15 as the B operand;
-        // the accumulator of token tile mt holds U[16 mt + 4 lg4 + r][col], stored as U^T rows.
-        const int col = 16 * w + li;
-        v4 uacc[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) uacc[mt] = v4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int s0 = 32 * ks + 4 * lg4;
-            float bv[8];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                bv[e] = V_s[s0 + e][col];
-                bv[e + 4] = V_s[s0 + 16 + e][col];
-            }
-            bf8 bh, bl;
-            split8(bv, bh, bl);
-#pragma unroll
-            for (int mt = 2 * ks; mt < 4; ++mt) {
-                bf8 ah, al;
-                t_frag(B_s, mt, ks, ah, al);
-                uacc[mt] = mfma_bf16(ah, bh, uacc[mt]);
-                uacc[mt] = mfma_bf16(ah, bl, uacc[mt]);
-                uacc[mt] = mfma_bf16(al, bh, uacc[mt]);
-            }
-        }
-        float* Ut = p.ws.Ut + ch * kD * kChunk;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-            *reinterpret_cast<v4*>(Ut + (size_t)col * kChunk + 16 * mt + 4 * lg4) = uacc[mt];
+    if (gw == 0 && grp < nmap) {
+        const int h = mapped_head(L, src, grp);
+        decay_scan(p, g, h, (size_t)c * L.h_v + h, ra, rb, G_s[grp], B_s[grp], lane);
     }
-    {
-        // W^T = K^T diag(beta Gam) T^T, wave w taking W^T row tiles 2 kw, 2 kw + 1 (k-step kw of
-        // the chain's W fragments) for token tiles 0 and 3 (waves 0-3) or 1 and 2 (waves 4-7),
-        // three (token tile, k-step) pairs each: the K^T fragments
-        // as the A operand and diag(beta Gam) T^T as the B operand, so the accumulator of (row
-        // tile 2 kw + t, token tile mt) holds W[16 mt + li][32 kw + 16 t + 4 lg4 + r], r = 0..3:
-        // entries 4 t + r of lane (li, lg4) of the chain's fragment (mt, kw) of -W, which the
-        // wave then stores whole (negated, split) straight from the accumulators.
-        v4 wacc[2][2];
+    lds_barrier();                                          // the planes' space becomes A/T
+
+    float* A_s = reinterpret_cast<float*>(lds) + grp * (kChunk * kTS);
+    float* T_s = A_s;                  // T over A: diagonal blocks in place, the others mirrored
+    for (int it = 0; 2 * it < nmap; ++it) {
+        const int m = 2 * it + grp;
+        const bool live = m < nmap;
+        const int h = mapped_head(L, src, min(m, nmap - 1));
+        const size_t ch = (size_t)c * L.h_v + h;
+        if (it > 0) {                                       // the next head's decay scan
+            if (live && gw == 0) {
+                const size_t ab = (size_t)(g.t0 + min(lane, g.len - 1)) * L.h_v + h;
+                decay_scan(p, g, h, ch, p.a[ab], p.b[ab], G_s[grp], B_s[grp], lane);
+            }
+            lds_barrier();
+        }
+        if (live) am_head(kk, qk, G_s[grp], B_s[grp], A_s, p.ws.Mf + ch * kFragM, gw, lane);
+        lds_barrier();
+        // The group's first wave inverts the four unit lower-triangular diagonal blocks of
+        // I + A (lane = 16 b + column cc).
+        if (live && gw == 0) {
+            const int b = lane >> 4, cc = lane & 15;
+            const float* Ab = A_s + (16 * b) * kTS + 16 * b;
+            float x[16];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int r = 0; r < 16; ++r) {
+                float acc = r == cc ? 1.0f : 0.0f;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) wacc[t][j] = v4{0.f, 0.f, 0.f, 0.f};
-        const int mts[2] = {w < 4 ? 0 : 1, w < 4 ? 3 : 2};
+                for (int q = 0; q < r; ++q) acc = fmaf(-Ab[r * kTS + q], x[q], acc);
+                x[r] = acc;
+                if ((r & 3) == 3) __builtin_amdgcn_sched_barrier(0);   // loads hoisted 4 rows ahead at most
+            }
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
+            for (int r = 0; r < 16; ++r) T_s[(16 * b + r) * kTS + 16 * b + cc] = x[r];
+        }
+        lds_barrier();
+        // T below the diagonal blocks: wave j (0..2) of the group runs column block j.
+        if (live) {
+            if (gw == 0) t_column<0>(A_s, T_s, lane);
+            else if (gw == 1) t_column<1>(A_s, T_s, lane);
+            else if (gw == 2) t_column<2>(A_s, T_s, lane);
+        }
+        lds_barrier();
+        // T' = T diag(beta) as the chain's A fragments (4 row tiles x 2 k-steps): wave gw
+        // writes fragments gw and gw + 4, (row tile f / 2, k-step f % 2).
+        if (live) {
+            uint16_t* Tf = p.ws.Tf + ch * kFragM;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if (2 * ks > mts[j]) continue;                  // T is zero there (wave-uniform)
-                bf8 bh, bl;
-                t_frag(BG_s, mts[j], ks, bh, bl);
-#pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    wacc[t][j] = mfma_bf16(kt[t][ks][0], bh, wacc[t][j]);
-                    wacc[t][j] = mfma_bf16(kt[t][ks][0], bl, wacc[t][j]);
-                    wacc[t][j] = mfma_bf16(kt[t][ks][1], bh, wacc[t][j]);
-                }
+            for (int u = 0; u < 2; ++u) {
+                const int f = gw + 4 * u, mt = f >> 1, ks = f & 1;
+                bf8 hi, lo;
+                t_frag(T_s, B_s[grp], mt, ks, li, lg4, hi, lo);
+                *reinterpret_cast<bf8*>(Tf + frag_at(mt, ks, 2, 0, lane)) = hi;
+                *reinterpret_cast<bf8*>(Tf + frag_at(mt, ks, 2, 1, lane)) = lo;
             }
         }
-        uint16_t* Wf = p.ws.Wf + ch * kFragW;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float x[8];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                x[r] = -wacc[0][j][r];
-                x[4 + r] = -wacc[1][j][r];
-            }
-            store_frag(Wf, mts[j], kw, 4, lane, x);
-        }
+        if (2 * (it + 1) < nmap) lds_barrier();             // T and beta are read until here
     }
 }
+
 // ---------------------------------------------------------------------------------------
-// chain: one workgroup per (sequence, v head, 16-column state strip), 7 waves
+// chain: one workgroup per (sequence, v head, 16-column state strip), 8 waves
 // ---------------------------------------------------------------------------------------
 // Columns of the state are independent, so a head's chain splits into 8 strips of 16
-// columns, and each strip's workgroup walks its sequence's chunks in order. Roles:
-//   wave 0 (state) carries the strip S (128 x 16) in four-register MFMA accumulators and
-//     per chunk computes
-//       D  = U - W S                                   (64 x 16; W from LDS)
-//       S' = Gam_last S + K^T Dg,  Dg = diag(exp(G_last - G)) D     (K^T from LDS)
-//     The chunk kernel stores W, K^T, Q and M with their k index in accumulator row order
-//     (kperm), so the accumulator tiles of S and D, split to bf16 hi/lo, are the next
-//     product's B operands as they stand: the state path has no LDS round trip and never
-//     waits at a barrier for data. It hands the split S and D of every chunk to the output
-//     waves through a double-buffered LDS slot.
-//   waves 1-4 (output): wave 1 + r computes rows 16 r .. 16 r + 15 of
-//       O = diag(Gam) Q S + M D                        (Q, M from global, one chunk ahead)
-//     from the S and D the state wave handed over.
-//   waves 5, 6 (copy) move the next chunk's W and this chunk's K^T fragments (32 KiB each,
-//     one wave each, so twice the loads are in flight) into LDS with direct global-to-LDS
-//     loads, and wait for them before the barrier.
-// The roles meet at one barrier per chunk. Between barriers c-1 and c the state wave
-// finishes chunk c-1 (K^T from slot (c-1)&1) interleaved with the start of chunk c (W from
-// slot c&1, hand-over slot c&1), the copy waves fill W slot (c+1)&1 and K^T slot c&1, and
-// the output waves compute chunk c-1 from hand-over slot (c-1)&1. The state wave's code
-// path issues no LDS DMA, so the compiler never makes it wait for the copies.
+// columns, and each strip's workgroup walks its sequence's chunks in order. For chunk c_k,
+// with S_k the strip at its start,
+//     W_k     = K_k S_k                                            (64 x 16)
+//     D_k     = T'_k (V_k - diag(Gam_k) W_k)
+//     S_{k+1} = gam_k S_k + K_k^T Dg_k,  Dg_k = diag(E_k) D_k,  gam_k = Gam_k[63]
+//     O_k     = diag(Gam_k) Q_k S_k + M_k D_k
+// run in two phases per chunk, alpha_k and beta_k, each ended by a workgroup barrier:
+//   alpha_k  the state waves (0, 1) each hold 64 rows of S in MFMA accumulators (row tile mt
+//            of wave i: S[64 i + 16 mt + 4 lg4 + r][column li]); for k > 0 they finish
+//            S_k = gam S_{k-1} + K_{k-1}^T Dg_{k-1} on their rows, hand S_k over split and
+//            form their half of W_k (the sum over their 64 channels);
+//   beta_k   the D wave (4) adds the halves and forms D_k, handing over D_k (fp32) for the
+//            outputs and Dg_k (split) with gam_k for the state waves.
+// Products take their k index in accumulator row order (kperm), so an accumulator tile pair,
+// split to bf16 hi/lo, is the next product's B operand as it stands. The D wave reads chunk
+// c_k's V, decay factors and T' from the value slot in alpha_k, and the state waves read the
+// K^T fragments of chunk c_k in beta_k, each while the other side works; the K fragments of
+// W are read as the products need them.
+// The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
+// alpha_{k+1}, with Q, M and Gam loaded from the workspace two chunks ahead. The feed wave (5)
+// copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3 with direct global-to-LDS loads
+// issued in alpha_{k-1} (the slot last held chunk c_{k-2}, read until beta_{k-2}), and in
+// beta_k writes
+// chunk c_{k+1}'s V strip, decay factors and T' fragments into the value slot (read by the D
+// wave in alpha_k) from registers loaded a chunk earlier. Before the first chunk it writes the
+// new rolling conv history of the workgroup's share of the sequence's channels.
+// A last alpha_n finishes S_n (state waves) and O_{n-1} (output waves).
+// Waves w and w + 4 share a SIMD: the state waves' partners (the D wave, the feed wave) work
+// in beta, the state waves in alpha.
 constexpr int kStrip = 16;                              // state columns per chain workgroup
 constexpr int kStrips = kD / kStrip;                    // 8
-constexpr int kChainWaves = 7;
+constexpr int kChainWaves = 8;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
-constexpr int kOpsBytes = 32 * kPlane;                  // W (4 x 4) or K^T (8 x 2) fragments, 2 planes
+constexpr int kKSlots = 3;                              // key slots in a ring
+constexpr int kTSlot = 12 * kPlane;                     // T': its 6 nonzero fragments x 2 planes
+constexpr int kVSlot = 4 * kPlane + 2 * kChunk * 4;     // V (4 row tiles, accumulator layout), E, Gam
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
 constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in fp32
-constexpr int kChainSink = kPlane;                      // target of the L2 warm-up loads
-constexpr int kChainLds = 4 * kOpsBytes + 2 * kHandBytes + kChainSink;   // 156,672 bytes
-constexpr int kWarmAhead = 2;                           // chunks warmed ahead of their copy
-constexpr int kWarmLoadsW = 9;                          // warm-up loads per chunk: W-copy wave
-constexpr int kWarmLoadsK = 10;                         //                          K^T-copy wave
+constexpr int kWBytes = 2 * 4 * kPlane;                 // the two halves of W: 4 row tiles in fp32 each
+constexpr int kDgBytes = 4 * kPlane + 16;               // Dg: 2 k-steps x 2 planes, then gam
+constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlot, kOffH = kOffV + kVSlot;
+constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes;
+constexpr int kChainLds = kOffG + kDgBytes;             // 145,936 bytes
 
-__device__ __forceinline__ bf8 lds_frag(const uint8_t* lds, int off, int lane) {
-    return *reinterpret_cast<const bf8*>(lds + off + lane * 16);
-}
-__device__ __forceinline__ void lds_put(uint8_t* lds, int off, int lane, const bf8& v) {
-    *reinterpret_cast<bf8*>(lds + off + lane * 16) = v;
+typedef __attribute__((address_space(3))) bf8 lds_bf8;
+typedef __attribute__((address_space(3))) v4 lds_v4;
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u2v lds_u2;
+
+// This lane's address in an LDS area at byte offset off (which includes the lane's own part),
+// made opaque to the compiler: reads and writes at base + (a constant below 64 KiB) then use
+// the instruction's immediate offset, where the folded address of an area above 64 KiB
+// would cost an add per access.
+__device__ __forceinline__ lds_u8* lane_at(uint8_t* lds, int off) {
+    lds_u8* b = (lds_u8*)lds + off;
+    __asm__ volatile("" : "+v"(b));
+    return b;
 }
 
 // B operand of one 32-wide k-step from two stacked accumulator tiles (kperm order), split.
@@ -954,76 +829,31 @@ __device__ __forceinline__ void split_tiles(const v4& a, const v4& b, bf8& hi, b
     lo = __builtin_bit_cast(bf8, u4x{l0, l1, l2, l3});
 }
 
-
-__device__ __forceinline__ int chain_w_slot(int q) { return q * kOpsBytes; }
-__device__ __forceinline__ int chain_k_slot(int q) { return (2 + q) * kOpsBytes; }
-__device__ __forceinline__ int chain_h_slot(int q) { return 4 * kOpsBytes + q * kHandBytes; }
-
-// State role: U of chunk c at this lane's rows 16 m + 4 lg4 + i (tokens), column j, the
-// decay factors exp(G_last - G) at the same rows, and Gam_last = exp(G_last).
-__device__ __forceinline__ void chain_load_ug(const PrefillParams& p, int c, int h, int j, int lg4, v4 (&u)[4],
-                                              v4 (&e)[4], float& gam) {
-    const size_t ch = (size_t)c * p.L.h_v + h;
-    const float* Ut = p.ws.Ut + (ch * kD + j) * kChunk + 4 * lg4;
-    const float* E = p.ws.G + ch * 2 * kChunk;
-    gam = E[2 * kChunk - 1];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) e[m] = *reinterpret_cast<const v4*>(E + 16 * m + 4 * lg4);
-#pragma unroll
-    for (int m = 0; m < 4; ++m) u[m] = *reinterpret_cast<const v4*>(Ut + 16 * m);
+// K fragment (token tile mt, channel k-step ks) of a key slot: A operand of K S. Lane
+// (li, lg4) reads row 16 mt + li, channels 32 ks + 4 lg4 .. +3 and 32 ks + 16 + 4 lg4 .. +3,
+// from the lane base kb = slot + li * kPRow + 8 lg4.
+__device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, int ks, bf8& hi, bf8& lo) {
+    const int o = mt * 16 * kPRow + ks * 64;
+    const u2v a = *(const lds_u2*)(kb + o), b = *(const lds_u2*)(kb + o + 32);
+    const u2v c = *(const lds_u2*)(kb + kKPlane + o), d = *(const lds_u2*)(kb + kKPlane + o + 32);
+    hi = __builtin_bit_cast(bf8, u4x{a.x, a.y, b.x, b.y});
+    lo = __builtin_bit_cast(bf8, u4x{c.x, c.y, d.x, d.y});
 }
 
-// Output role: Q and M fragments of row tile r of chunk c, and G at this lane's rows.
-__device__ __forceinline__ void chain_load_qm(const PrefillParams& p, int c, int h, int src, int r, int lane,
-                                              bf8 (&qf)[4][2], bf8 (&mf)[2][2], v4& g) {
-    const size_t ch = (size_t)c * p.L.h_v + h;
-    const uint16_t* Qf = p.ws.Qf + ((size_t)c * p.L.h_k + src) * kFragW;
-    const uint16_t* Mf = p.ws.Mf + ch * kFragM;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int pl = 0; pl < 2; ++pl) qf[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(r, ks, 4, pl, lane));
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int pl = 0; pl < 2; ++pl) mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
-    g = *reinterpret_cast<const v4*>(p.ws.G + ch * 2 * kChunk + kChunk + 16 * r + 4 * (lane >> 4));   // exp(G_t)
+// K^T fragment (channel tile m, token k-step ks) of a key slot: A operand of K^T Dg, by
+// transposing reads (ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
+// j & 3 of the 8-byte reads of lanes (j >> 2) + 4 e, e = 0..3). Lane i of lane group g reads
+// channels 16 m + 4 (i & 3) .. +3 of token 32 ks + 4 g + (i >> 2) (then of the token 16
+// later), so it receives channel 16 m + i at tokens 32 ks + 4 g + e (+ 16): entries e (4 + e)
+// of its kperm fragment chunk. Lane base tb = slot + (4 g + (i >> 2)) * kPRow + 8 (i & 3).
+__device__ __forceinline__ void kt_frag(const lds_u8* tb, int m, int ks, bf8& hi, bf8& lo) {
+    const int o = ks * 32 * kPRow + m * 32;
+    const uint2 a = lds_tr16(tb + o), b = lds_tr16(tb + o + 16 * kPRow);
+    const uint2 c = lds_tr16(tb + kKPlane + o), d = lds_tr16(tb + kKPlane + o + 16 * kPRow);
+    hi = __builtin_bit_cast(bf8, u4x{a.x, a.y, b.x, b.y});
+    lo = __builtin_bit_cast(bf8, u4x{c.x, c.y, d.x, d.y});
 }
 
-// Copy role: the 32 one-KiB fragment planes of W (chunk c, v head h) or K^T (chunk c, q/k
-// head src) into LDS at dst.
-__device__ __forceinline__ void chain_copy(lds_u8* dst, const uint16_t* frags, int lane) {
-    const uint8_t* g = reinterpret_cast<const uint8_t*>(frags) + lane * 16;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, dst + i * kPlane, 16, 0, 0);
-}
-
-// This lane's address in an LDS area at byte offset off, made opaque to the compiler: reads
-// and writes at base + (a constant below 64 KiB) then use the instruction's immediate offset,
-// where the folded address of an area above 64 KiB would cost an add per access.
-__device__ __forceinline__ lds_u8* lane_base(uint8_t* lds, int off, int lane) {
-    lds_u8* b = (lds_u8*)lds + off + lane * 16;
-    __asm__ volatile("" : "+v"(b));
-    return b;
-}
-// W fragments (row tiles m = 0..3, both planes) of k-step ks from the slot at wq (lane base).
-__device__ __forceinline__ void chain_w_frags(const lds_u8* wq, int ks, bf8 (&f)[4][2]) {
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-        const int o = (m * 4 + ks) * 2 * kPlane;
-        f[m][0] = *(const __attribute__((address_space(3))) bf8*)(wq + o);
-        f[m][1] = *(const __attribute__((address_space(3))) bf8*)(wq + o + kPlane);
-    }
-}
-// K^T fragments (row tiles 4 g .. 4 g + 3, both planes) of k-step ks from the slot at kq.
-__device__ __forceinline__ void chain_kt_frags(const lds_u8* kq, int ks, int g, bf8 (&f)[4][2]) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int o = ((4 * g + j) * 2 + ks) * 2 * kPlane;
-        f[j][0] = *(const __attribute__((address_space(3))) bf8*)(kq + o);
-        f[j][1] = *(const __attribute__((address_space(3))) bf8*)(kq + o + kPlane);
-    }
-}
 // acc[j] += A_j B for four row tiles, split products; the products go tile by tile within
 // each of hi hi, hi lo, lo hi, so consecutive MFMAs never share an accumulator.
 __device__ __forceinline__ void mfma4_split(const bf8 (&a)[4][2], const bf8& bh, const bf8& bl, v4* acc) {
@@ -1066,307 +896,389 @@ __device__ __forceinline__ void mfma2_split(const bf8 (&a)[4][2], const bf8& bh,
     for (int t = 0; t < 2; ++t) acc[t] = mfma_bf16(a[t][1], bh, acc[t]);
 }
 
-// State role (wave 0): the strip's whole chunk loop, S (128 x 16) in accumulators.
-// Between barriers c-1 and c (c > c_begin) it finishes chunk c-1,
-//     S <- Gam_{c-1} S + K^T Dg_{c-1}          (K^T from slot (c-1)&1; S arrives scaled)
-// and runs chunk c:
-//     S handed over (split), D = U - W S, D handed over, Dg = E D split, S *= Gam_c.
-// W is stored negated, so the D accumulators start from U. The work is cut into regions
-// of 12 MFMAs, each holding the VALU work (splits, scalings) that can overlap them. Three
-// fragment groups (R0..R2) rotate through the K^T and W fragments, each refilled as soon
-// as its last MFMA has issued.
-__device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t* lds, int lane, int c_begin,
-                                                 int c_end, int h, int j, int lg4, v4 (&S)[8]) {
-    v4 U[4], E[4];
-    float gam;
-    bf8 dh[2], dl[2], sh[4], sl[4];
-    v4 dg2, dg3;                       // Dg row tiles 2, 3, split at the start of part b
-    bf8 R0[4][2], R1[4][2], R2[4][2];
 
-    // Lane bases of the two W, K^T and hand-over slots.
-    lds_u8* const wb[2] = {lane_base(lds, chain_w_slot(0), lane), lane_base(lds, chain_w_slot(1), lane)};
-    lds_u8* const kb[2] = {lane_base(lds, chain_k_slot(0), lane), lane_base(lds, chain_k_slot(1), lane)};
-    lds_u8* const hb[2] = {lane_base(lds, chain_h_slot(0), lane), lane_base(lds, chain_h_slot(1), lane)};
-    typedef __attribute__((address_space(3))) bf8 lds_bf8;
-    typedef __attribute__((address_space(3))) v4 lds_v4;
-    auto put_s = [&](int q, int ks) {
-        *(lds_bf8*)(hb[q] + (2 * ks) * kPlane) = sh[ks];
-        *(lds_bf8*)(hb[q] + (2 * ks + 1) * kPlane) = sl[ks];
-    };
-    // Part b, row tiles 0-3 (K^T k-steps 0, 1 of slot qp in R0, R1); R2 and then R0 take
-    // the row tiles 4-7.
-    auto part_b_lo = [&](int qp) {
-        chain_kt_frags(kb[qp], 0, 0, R0);
-        chain_kt_frags(kb[qp], 1, 0, R1);
-        split_tiles(dg2, dg3, dh[1], dl[1]);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma4_split(R0, dh[0], dl[0], S);
-        __builtin_amdgcn_sched_barrier(0);
-        chain_kt_frags(kb[qp], 0, 1, R2);
-        __builtin_amdgcn_sched_barrier(0);
-        mfma4_split(R1, dh[1], dl[1], S);
-        __builtin_amdgcn_sched_barrier(0);
-        chain_kt_frags(kb[qp], 1, 1, R0);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // Part b, row tiles 4-7; with A, the split and hand-over of S row tiles 0-3 (final
-    // after part_b_lo) and the reads of W k-steps 0, 1 (slot q) into R1, R2.
-    auto part_b_hi = [&](int q, bool A) {
-        mfma4_split(R2, dh[0], dl[0], S + 4);
-        if (A) {
-            split_tiles(S[0], S[1], sh[0], sl[0]);
-            put_s(q, 0);
-            chain_w_frags(wb[q], 0, R1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        mfma4_split(R0, dh[1], dl[1], S + 4);
-        if (A) {
-            split_tiles(S[2], S[3], sh[1], sl[1]);
-            put_s(q, 1);
-            chain_w_frags(wb[q], 1, R2);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // Part a from the W products on: D = U + (-W) S, hand-overs, Dg split, S *= Gam.
-    auto part_a = [&](int q) {
-        // W k-step 0 (R1); S row tiles 4, 5 split; S row tiles 0, 1 scaled; W k-step 2 -> R0.
-        mfma4_split(R1, sh[0], sl[0], U);
-        split_tiles(S[4], S[5], sh[2], sl[2]);
-        put_s(q, 2);
-        S[0] *= gam;
-        S[1] *= gam;
-        chain_w_frags(wb[q], 2, R0);
-        __builtin_amdgcn_sched_barrier(0);
-        // W k-step 1 (R2); S row tiles 6, 7 split; S row tiles 2, 3 scaled; W k-step 3 -> R1.
-        mfma4_split(R2, sh[1], sl[1], U);
-        split_tiles(S[6], S[7], sh[3], sl[3]);
-        put_s(q, 3);
-        S[2] *= gam;
-        S[3] *= gam;
-        chain_w_frags(wb[q], 3, R1);
-        __builtin_amdgcn_sched_barrier(0);
-        // W k-steps 2, 3 of row tiles 0, 1 (final after this); S row tiles 4-7 scaled.
-        mfma2_split(R0, sh[2], sl[2], U);
-        mfma2_split(R1, sh[3], sl[3], U);
-#pragma unroll
-        for (int mt = 4; mt < 8; ++mt) S[mt] *= gam;
-        __builtin_amdgcn_sched_barrier(0);
-        // W k-steps 2, 3 of row tiles 2, 3; D tiles 0, 1 handed over (fp32, the output
-        // waves split it) and Dg tiles 0, 1 split.
-        {
-            bf8 a2[4][2], a3[4][2];
-#pragma unroll
-            for (int pl = 0; pl < 2; ++pl) {
-                a2[0][pl] = R0[2][pl]; a2[1][pl] = R0[3][pl];
-                a3[0][pl] = R1[2][pl]; a3[1][pl] = R1[3][pl];
-            }
-            mfma2_split(a2, sh[2], sl[2], U + 2);
-            mfma2_split(a3, sh[3], sl[3], U + 2);
-        }
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-            *(lds_v4*)(hb[q] + kHandS + m * kPlane) = U[m];
-        split_tiles(E[0] * U[0], E[1] * U[1], dh[0], dl[0]);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int m = 2; m < 4; ++m)
-            *(lds_v4*)(hb[q] + kHandS + m * kPlane) = U[m];
-        dg2 = E[2] * U[2];
-        dg3 = E[3] * U[3];
-        __builtin_amdgcn_sched_barrier(0);
-    };
-
-    chain_load_ug(p, c_begin, h, j, lg4, U, E, gam);
-    lds_barrier();                                            // W of the first chunk in LDS
-    // Chunk c_begin: part a only.
-    split_tiles(S[0], S[1], sh[0], sl[0]);
-    put_s(0, 0);
-    split_tiles(S[2], S[3], sh[1], sl[1]);
-    put_s(0, 1);
-    chain_w_frags(wb[0], 0, R1);
-    chain_w_frags(wb[0], 1, R2);
-    __builtin_amdgcn_sched_barrier(0);
-    part_a(0);
-    for (int c = c_begin + 1; c < c_end; ++c) {
-        chain_load_ug(p, c, h, j, lg4, U, E, gam);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();                                        // barrier c-1
-        const int q = (c - c_begin) & 1;
-        part_b_lo(q ^ 1);
-        part_b_hi(q, true);
-        part_a(q);
-    }
-    lds_barrier();                                            // barrier c_end-1
-    part_b_lo((c_end - 1 - c_begin) & 1);
-    part_b_hi(0, false);
+// A workgroup's sequence: chunk k (0-based) of its n chunks starts at token lo + 64 k; its
+// operands sit at workspace chunk c0 + k.
+struct SeqGeo { int s, lo, hi, n, c0; };
+__device__ __forceinline__ ChunkGeo seq_chunk(const SeqGeo& sg, int k) {
+    ChunkGeo g;
+    g.s = sg.s;
+    g.lo = sg.lo;
+    g.t0 = sg.lo + k * kChunk;
+    g.len = min(kChunk, sg.hi - g.t0);
+    g.pos0 = k * kChunk;
+    return g;
 }
 
-struct ChainOut {
-    bf8 qf[4][2], mf[2][2];
+// State role (waves 0 and 1, half = wave): rows 64 half .. 64 half + 63 of the strip, S[mt]
+// the accumulator of row tile mt (rows 64 half + 16 mt + 4 lg4 + r, column li).
+__device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, int half, v4 (&S)[4]) {
+    const int li = lane & 15, lg4 = lane >> 4;
+    lds_u8 *kb[kKSlots], *tb[kKSlots];
+#pragma unroll
+    for (int q = 0; q < kKSlots; ++q) {
+        kb[q] = lane_at(lds, kOffK + q * kKSlot + li * kPRow + 8 * lg4);
+        tb[q] = lane_at(lds, kOffK + q * kKSlot + (4 * lg4 + (li >> 2)) * kPRow + 8 * (li & 3));
+    }
+    lds_u8* hb = lane_at(lds, kOffH + 4 * half * kPlane + lane * 16);     // S k-steps 2 half, 2 half + 1
+    lds_u8* wb = lane_at(lds, kOffW + 4 * half * kPlane + lane * 16);
+    const lds_u8* gb = lane_at(lds, kOffG + lane * 16);
+    // K: channel k-step 2 half + a, token tile mt; K^T: token k-step ks, channel tile 4 half + j.
+    bf8 KF[2][4][2], KT[2][4][2];
+    auto load_k = [&](int q) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) k_frag(kb[q], mt, 2 * half + a, KF[a][mt][0], KF[a][mt][1]);
+    };
+    auto load_kt = [&](int q) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kt_frag(tb[q], 4 * half + j, ks, KT[ks][j][0], KT[ks][j][1]);
+    };
+    // S_k handed over split (the outputs' B operand) and this wave's half of W_k = K_k S_k.
+    auto hand_and_w = [&]() {
+        bf8 sh[2], sl[2];
+        split_tiles(S[0], S[1], sh[0], sl[0]);
+        split_tiles(S[2], S[3], sh[1], sl[1]);
+        v4 W[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) W[mt] = v4{0.f, 0.f, 0.f, 0.f};
+        mfma4_split(KF[0], sh[0], sl[0], W);
+        mfma4_split(KF[1], sh[1], sl[1], W);
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            *(lds_bf8*)(hb + (2 * a) * kPlane) = sh[a];
+            *(lds_bf8*)(hb + (2 * a + 1) * kPlane) = sl[a];
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) *(lds_v4*)(wb + mt * kPlane) = W[mt];
+    };
+
+    lds_barrier();                                          // alpha_0: chunk c_0's keys in slot 0
+    load_k(0);
+    hand_and_w();
+    int q = 0;                                              // key slot of chunk c_k: k mod 3
+    for (int k = 0; k < n; ++k) {
+        lds_barrier();                                      // beta_k
+        const int q1 = q == kKSlots - 1 ? 0 : q + 1;
+        load_kt(q);                                         // K^T of chunk c_k, for S_{k+1}
+        lds_barrier();                                      // alpha_{k+1}: Dg_k, gam_k handed over
+        bf8 dh[2], dl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            dh[ks] = *(const lds_bf8*)(gb + (2 * ks) * kPlane);
+            dl[ks] = *(const lds_bf8*)(gb + (2 * ks + 1) * kPlane);
+        }
+        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) S[mt] *= gam;
+        mfma4_split(KT[0], dh[0], dl[0], S);
+        mfma4_split(KT[1], dh[1], dl[1], S);
+        if (k + 1 < n) { load_k(q1); hand_and_w(); }
+        q = q1;
+    }
+}
+
+// D role (wave 4): per chunk, D = T' (V - diag(Gam) (W_0 + W_1)) from the state waves' halves of
+// W, with V, the decay factors and T' read from the value slot in the preceding alpha.
+__device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
+    const int lg4 = lane >> 4;
+    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
+    const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
+    const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
+    lds_u8* hb = lane_at(lds, kOffH + kHandS + lane * 16);
+    lds_u8* gb = lane_at(lds, kOffG + lane * 16);
+    for (int k = 0; k < n; ++k) {
+        lds_barrier();                                      // alpha_k: chunk c_k in the value slot
+        v4 V[4], E[4], Gm[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            V[mt] = *(const lds_v4*)(vb + mt * kPlane);
+            E[mt] = *(const lds_v4*)(eb + mt * 64);
+            Gm[mt] = *(const lds_v4*)(eb + 4 * kChunk + mt * 64);
+        }
+        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kPlane +
+                                                                            4 * kChunk + 4 * (kChunk - 1));
+        bf8 F0[4][2], F1[4][2];                             // T' (mt, 0), mt = 0..3; T' (2, 1), (3, 1)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) {
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) F0[mt][pl] = *(const lds_bf8*)(fb + (2 * mt + pl) * kPlane);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) F1[j][pl] = *(const lds_bf8*)(fb + (2 * (4 + j) + pl) * kPlane);
+        }
+        lds_barrier();                                      // beta_k: both halves of W_k handed over
+        v4 X[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            const v4 w0 = *(const lds_v4*)(wb + mt * kPlane), w1 = *(const lds_v4*)(wb + (4 + mt) * kPlane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], V[mt][e]);
+        }
+        bf8 xh[2], xl[2];
+        split_tiles(X[0], X[1], xh[0], xl[0]);
+        split_tiles(X[2], X[3], xh[1], xl[1]);
+        v4 D[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) D[m] = v4{0.f, 0.f, 0.f, 0.f};
+        mfma4_split(F0, xh[0], xl[0], D);                   // tokens 0-31 for every row tile
+        mfma2_split(F1, xh[1], xl[1], D + 2);               // tokens 32-63 for row tiles 2, 3
+        bf8 dh[2], dl[2];
+        split_tiles(E[0] * D[0], E[1] * D[1], dh[0], dl[0]);
+        split_tiles(E[2] * D[2], E[3] * D[3], dh[1], dl[1]);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            *(lds_bf8*)(gb + (2 * ks) * kPlane) = dh[ks];
+            *(lds_bf8*)(gb + (2 * ks + 1) * kPlane) = dl[ks];
+        }
+        if (lane == 0) *(__attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane) = gam;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) *(lds_v4*)(hb + m * kPlane) = D[m];
+    }
+    lds_barrier();                                          // alpha_n
+}
+
+// Output role (waves 2, 3, 6, 7; row tile r): rows 16 r .. 16 r + 15 of every chunk's outputs,
+// O = diag(Gam) Q S + M D, with Q, M and Gam from the workspace, loaded two chunks ahead into
+// two alternating operand sets. In beta_k the wave forms diag(Gam) Q S of chunk c_k, then loads
+// chunk c_{k+2}'s Q and Gam into the set it used; in alpha_{k+1} it adds M D, stores the rows and
+// loads chunk c_{k+2}'s M.
+struct OutQ {
+    bf8 qf[4][2];
     v4 g;                 // exp(G_t) at this lane's rows
 };
-
-// Output role, one chunk: rows 16 r .. 16 r + 15 of O = diag(Gam) Q S + M D from hand-over
-// slot q. Rows at or past len are not stored.
-template <int OUT>
-__device__ __forceinline__ void chain_out_step(const PrefillParams& p, const uint8_t* lds, int q, int lane, int r,
-                                               const ChainOut& x, size_t o_base, int len) {
-    lds_barrier();                                                // the chunk has been handed over
-    bf8 sb[4][2], db[2][2];
+struct OutM {
+    bf8 mf[2][2];
+};
+__device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const SeqGeo& sg, int k, int h, int src,
+                                                 int r, int lane, OutQ& x) {
+    const size_t c = (size_t)(sg.c0 + min(k, sg.n - 1));
+    const uint16_t* Qf = p.ws.Qf + (c * p.L.h_k + src) * kFragW;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) sb[ks][pl] = lds_frag(lds, chain_h_slot(q) + (2 * ks + pl) * kPlane, lane);
-    v4 D[4];
+        for (int pl = 0; pl < 2; ++pl) x.qf[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(r, ks, 4, pl, lane));
+    x.g = *reinterpret_cast<const v4*>(p.ws.G + (c * p.L.h_v + h) * 2 * kChunk + kChunk + 16 * r + 4 * (lane >> 4));
+}
+__device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const SeqGeo& sg, int k, int h, int r,
+                                                 int lane, OutM& x) {
+    const size_t c = (size_t)(sg.c0 + min(k, sg.n - 1));
+    const uint16_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragM;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) D[m] = *reinterpret_cast<const v4*>(lds + chain_h_slot(q) + kHandS + m * kPlane + lane * 16);
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) split_tiles(D[2 * ks], D[2 * ks + 1], db[ks][0], db[ks][1]);
-    v4 o = {0.f, 0.f, 0.f, 0.f};
+        for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
+}
+
+__device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_t* lds, int lane, int r,
+                                                  const SeqGeo& sg, int h, int src, int j0) {
+    const Layer& L = p.L;
+    const int li = lane & 15, lg4 = lane >> 4;
+    OutQ q0, q1;
+    OutM m0, m1;
+    chain_out_load_q(p, sg, 0, h, src, r, lane, q0);
+    chain_out_load_m(p, sg, 0, h, r, lane, m0);
+    chain_out_load_q(p, sg, 1, h, src, r, lane, q1);
+    chain_out_load_m(p, sg, 1, h, r, lane, m1);
+    const lds_u8* hbase = lane_at(lds, kOffH + lane * 16);
+    const size_t row = (size_t)L.h_v * kD;
+    v4 o;
+    auto store = [&](int k) {
+        const ChunkGeo g = seq_chunk(sg, k);
+        const size_t ob = ((size_t)g.t0 * L.h_v + h) * kD + j0 + li;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) o = mfma_split(x.qf[ks][0], x.qf[ks][1], sb[ks][0], sb[ks][1], o);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] *= x.g[i];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) o = mfma_split(x.mf[ks][0], x.mf[ks][1], db[ks][0], db[ks][1], o);
-    const size_t row = (size_t)p.L.h_v * kD;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = 16 * r + 4 * (lane >> 4) + i;
-        if (t < len) {
-            const size_t oo = o_base + (size_t)t * row;
-            if constexpr ((OUT & 1) != 0) p.o[oo] = o[i];
-            if constexpr ((OUT & 2) != 0) p.o_bf16[oo] = f32_to_bf16(o[i]);
+        for (int i = 0; i < 4; ++i) {
+            const int t = 16 * r + 4 * lg4 + i;
+            if (t < g.len) {
+                const size_t oo = ob + (size_t)t * row;
+                if (p.o) p.o[oo] = o[i];
+                if (p.o_bf16) p.o_bf16[oo] = f32_to_bf16(o[i]);
+            }
         }
+    };
+    auto step = [&](int k, OutQ& Q, OutM& M) {
+        lds_barrier();                                      // beta_k: S_k handed over
+        bf8 sb[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) sb[ks][pl] = *(const lds_bf8*)(hbase + (2 * ks + pl) * kPlane);
+        // The three split products in separate accumulators: three short dependency chains.
+        v4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            a0 = mfma_bf16(Q.qf[ks][0], sb[ks][0], a0);
+            a1 = mfma_bf16(Q.qf[ks][0], sb[ks][1], a1);
+            a2 = mfma_bf16(Q.qf[ks][1], sb[ks][0], a2);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * Q.g[i];
+        if (k + 2 < sg.n) chain_out_load_q(p, sg, k + 2, h, src, r, lane, Q);
+        lds_barrier();                                      // alpha_{k+1}: D_k handed over
+        v4 D[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) D[m] = *(const lds_v4*)(hbase + kHandS + m * kPlane);
+        bf8 db[2][2];
+        split_tiles(D[0], D[1], db[0][0], db[0][1]);
+        split_tiles(D[2], D[3], db[1][0], db[1][1]);
+        a0 = o;
+        a1 = v4{0.f, 0.f, 0.f, 0.f};
+        a2 = a1;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            a0 = mfma_bf16(M.mf[ks][0], db[ks][0], a0);
+            a1 = mfma_bf16(M.mf[ks][0], db[ks][1], a1);
+            a2 = mfma_bf16(M.mf[ks][1], db[ks][0], a2);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = a0[i] + a1[i] + a2[i];
+        store(k);
+        if (k + 2 < sg.n) chain_out_load_m(p, sg, k + 2, h, r, lane, M);
+    };
+    lds_barrier();                                          // alpha_0
+    for (int k = 0; k < sg.n; k += 2) {
+        step(k, q0, m0);
+        if (k + 1 < sg.n) step(k + 1, q1, m1);
     }
 }
 
-// Copy role: bring this strip's share of chunk c's operands into L2 ahead of their use (the
-// 8 strips of a head share one XCD and its L2). Direct loads into a sink in LDS, so no
-// register waits for them. The W-copy wave (kWarmLoadsW loads) takes an eighth of W and Q,
-// and the decay factors; the K^T-copy wave (kWarmLoadsK loads) an eighth of K^T and M, and
-// the strip's U rows.
-__device__ __forceinline__ void chain_warm(const PrefillParams& p, lds_u8* sink, int c, int h, int src, int strip,
-                                           int lane, bool w_wave) {
-    const size_t ch = (size_t)c * p.L.h_v + h, cs = (size_t)c * p.L.h_k + src;
-    if (w_wave) {
-        const uint8_t* W = reinterpret_cast<const uint8_t*>(p.ws.Wf + ch * kFragW) + strip * 4 * kPlane + lane * 16;
-        const uint8_t* Q = reinterpret_cast<const uint8_t*>(p.ws.Qf + cs * kFragW) + strip * 4 * kPlane + lane * 16;
-        const uint8_t* G = reinterpret_cast<const uint8_t*>(p.ws.G + ch * 2 * kChunk) + (lane & 31) * 16;
+// Feed role (wave 5). In alpha_{k-1} it starts copying chunk c_{k+1}'s key planes (written by
+// the chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads,
+// and waits for them at the end of alpha_k. In beta_k it writes chunk c_{k+1}'s strip of V (in the D wave's accumulator layout: lane
+// (li, lg4) holds V[16 mt + 4 lg4 + r][j0 + li]), the decay factors (E, then Gam) and T' (its 6
+// nonzero fragments) into the value slot, then loads chunk c_{k+2}'s. Before the first chunk it
+// writes the new rolling conv history of the workgroup's share of the sequence's channels (the
+// h_v * 8 workgroups of a sequence split its C channels into contiguous ranges); nothing else
+// in this kernel touches conv_state.
+__device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
+                                                int h, int strip, int src) {
+    typedef __attribute__((address_space(3))) u4x lds_u4;
+    const Layer& L = p.L;
+    const int li = lane & 15, lg4 = lane >> 4;
+    v4 vv[4], eg;
+    u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
+    auto load = [&](int k) {
+        const size_t chh = (size_t)(sg.c0 + min(k, sg.n - 1)) * L.h_v + h;
+        const float* V = p.ws.V + chh * kChunk * kD + strip * kStrip + li;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __builtin_amdgcn_global_load_lds(W + i * kPlane, sink, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(Q + i * kPlane, sink, 16, 0, 0);
-        }
-        __builtin_amdgcn_global_load_lds(G, sink, 16, 0, 0);
-    } else {
-        const uint8_t* K = reinterpret_cast<const uint8_t*>(p.ws.Ktf + cs * kFragKt) + strip * 4 * kPlane + lane * 16;
-        const uint8_t* M = reinterpret_cast<const uint8_t*>(p.ws.Mf + ch * kFragM) + strip * 2 * kPlane + lane * 16;
-        const uint8_t* U = reinterpret_cast<const uint8_t*>(p.ws.Ut + (ch * kD + strip * kStrip) * kChunk) + lane * 16;
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            __builtin_amdgcn_global_load_lds(K + i * kPlane, sink, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(U + i * kPlane, sink, 16, 0, 0);
+            for (int r = 0; r < 4; ++r) vv[mt][r] = V[(16 * mt + 4 * lg4 + r) * kD];
+        eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
+        const u4x* tsrc = reinterpret_cast<const u4x*>(p.ws.Tf + chh * kFragM) + lane;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const int f = i < 8 ? 2 * (i >> 1) : 2 * (i >> 1) - 3;    // fragment mt * 2 + ks of slot entry i / 2
+            tf[i] = tsrc[(2 * f + (i & 1)) * kWave];
         }
-        __builtin_amdgcn_global_load_lds(M, sink, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(M + kPlane, sink, 16, 0, 0);
+    };
+    auto produce = [&]() {
+        lds_u8* vs = (lds_u8*)lds + kOffV;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) *(lds_v4*)(vs + mt * kPlane + lane * 16) = vv[mt];
+        if (lane < 32) *(lds_v4*)(vs + 4 * kPlane + lane * 16) = eg;
+        lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
+    };
+    auto copy_keys = [&](int k) {
+        const uint8_t* g = p.ws.Kp + ((size_t)(sg.c0 + k) * L.h_k + src) * kKSlot + lane * 16;
+        lds_u8* d = (lds_u8*)lds + kOffK + (k % kKSlots) * kKSlot;
+#pragma unroll
+        for (int i = 0; i < kKSlot / kPlane; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, d + i * kPlane, 16, 0, 0);
+    };
+    // s_waitcnt immediates (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8):
+    // lgkmcnt(0) alone; vmcnt(34) with lgkmcnt(0).
+    constexpr int kWaitLgkm0 = 0xc07f;
+    constexpr int kWaitVm34Lgkm0 = 0x8072;
+    auto wait_barrier = [&]() {
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(0);                      // the copies have landed
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+    };
+
+    {
+        const int G = L.h_v * kStrips, gi = h * kStrips + strip, per = (L.C + G - 1) / G;
+        const int ch_hi = min(L.C, (gi + 1) * per);
+        for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
+    }
+    copy_keys(0);
+    if (sg.n > 1) copy_keys(1);
+    load(0);
+    produce();
+    __builtin_amdgcn_sched_barrier(0);
+    load(1);
+    wait_barrier();                                         // alpha_0
+    for (int k = 0; k < sg.n; ++k) {
+        // Chunk c_{k+2}'s keys go to the slot of chunk c_{k-1}, whose K^T the state waves read in
+        // beta_{k-1}; they land by the end of alpha_{k+1}. Waiting here for all but the 34 copies
+        // just issued leaves chunk c_{k+1}'s keys (issued in alpha_{k-1}) and value operands
+        // (loaded in beta_{k-1}) landed: a wave's loads complete in issue order.
+        __asm__ volatile("" ::: "memory");
+        if (k + 2 < sg.n) {
+            copy_keys(k + 2);
+            static_assert(kKSlot / kPlane == 34, "the wait below counts 34 copies");
+            __builtin_amdgcn_s_waitcnt(kWaitVm34Lgkm0);
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        __builtin_amdgcn_s_barrier();                       // beta_k
+        __asm__ volatile("" ::: "memory");
+        if (k + 1 < sg.n) {
+            produce();
+            __builtin_amdgcn_sched_barrier(0);
+            load(k + 2);
+        }
+        // alpha_{k+1}: the slot writes have completed; the loads stay in flight.
+        __asm__ volatile("" ::: "memory");
+        __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
     }
 }
 
-// s_waitcnt that waits until at most N vector memory operations are outstanding (gfx9
-// encoding: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at their maximum).
-// The field layout is gfx9-family (gfx950 here); another target would need its own encoding.
-#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
-#error "wait_vmcnt encodes gfx950 s_waitcnt fields"
-#endif
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-template <int OUT>
 __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const PrefillParams p) {
     __shared__ __align__(16) uint8_t lds[kChainLds];
 
     const Layer& L = p.L;
     // XCD-aware mapping: the 8 strips of one (sequence, head) pair share an XCD, so its L2
     // serves the pair's chunk operands to all of them.
-    const int lin = blockIdx.x, xcd = lin & 7, k = lin >> 3;
-    const int strip = k & (kStrips - 1);
-    const int pair = (k / kStrips) * 8 + xcd;
+    const int lin = blockIdx.x, xcd = lin & 7, kq = lin >> 3;
+    const int strip = kq & (kStrips - 1);
+    const int pair = (kq / kStrips) * 8 + xcd;
     if (pair >= p.n_seq * L.h_v) return;
     const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
-    int seq_lo, seq_hi;
-    seq_bounds(p, s, seq_lo, seq_hi);
-    const int c_begin = p.single ? 0 : p.ws.chunk_off[s];
-    const int c_end = p.single ? (seq_hi - seq_lo + kChunk - 1) / kChunk : p.ws.chunk_off[s + 1];
-    if (c_begin >= c_end) return;
+    SeqGeo sg;
+    sg.s = s;
+    seq_bounds(p, s, sg.lo, sg.hi);
+    sg.c0 = p.single ? 0 : p.ws.chunk_off[s];
+    const int c_end = p.single ? (sg.hi - sg.lo + kChunk - 1) / kChunk : p.ws.chunk_off[s + 1];
+    sg.n = c_end - sg.c0;
+    if (sg.n <= 0) return;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
     const int j0 = strip * kStrip;
 
-    if (w == 0) {
-        // State strip: rows 16 mt + 4 lg4 + i (k index), column j0 + li (v index); the state
-        // is stored column by column ([d_v][d_k]), so the 4 rows are a float4.
-        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD + (size_t)(j0 + li) * kD + 4 * lg4;
-        v4 S[8];
+    if (w <= 1) {
+        // State rows 64 w + 16 mt + 4 lg4 + i (k index), column j0 + li (v index); the state is
+        // stored column by column ([d_v][d_k]), so the 4 rows are a float4.
+        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD + (size_t)(j0 + li) * kD + 64 * w + 4 * lg4;
+        v4 S[4];
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt) S[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
-        chain_state_role(p, lds, lane, c_begin, c_end, h, j0 + li, lg4, S);
+        for (int mt = 0; mt < 4; ++mt) S[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
+        chain_state_role(lds, lane, sg.n, w, S);
 #pragma unroll
-        for (int mt = 0; mt < 8; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
-    } else if (w <= 4) {
-        const int r = w - 1;
-        ChainOut x;
-        chain_load_qm(p, c_begin, h, src, r, lane, x.qf, x.mf, x.g);
-        lds_barrier();
-        for (int c = c_begin; c < c_end; ++c) {
-            const int t0 = seq_lo + (c - c_begin) * kChunk;
-            chain_out_step<OUT>(p, lds, (c - c_begin) & 1, lane, r, x, ((size_t)t0 * L.h_v + h) * kD + j0 + li,
-                                min(kChunk, seq_hi - t0));
-            __builtin_amdgcn_sched_barrier(0);                    // the reload after the last use
-            chain_load_qm(p, min(c + 1, c_end - 1), h, src, r, lane, x.qf, x.mf, x.g);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
+    } else if (w == 4) {
+        chain_d_role(lds, lane, sg.n);
+    } else if (w == 5) {
+        chain_feed_role(p, lds, lane, sg, h, strip, src);
     } else {
-        const bool w_wave = w == 5;                               // wave 5: W; wave 6: K^T
-        lds_u8* lds3 = (lds_u8*)lds;                              // the copies address LDS directly
-        lds_u8* sink = lds3 + 4 * kOpsBytes + 2 * kHandBytes;
-        auto w_of = [&](int cc) { return p.ws.Wf + ((size_t)cc * L.h_v + h) * kFragW; };
-        auto kt_of = [&](int cc) { return p.ws.Ktf + ((size_t)cc * L.h_k + src) * kFragKt; };
-        // Before the first barrier: W of the first chunk. Between barriers c-1 and c: W of
-        // chunk c+1 (used after barrier c) and K^T of chunk c (used after barrier c); the
-        // slots they replace were last read before barrier c-1.
-        if (w_wave) chain_copy(lds3 + chain_w_slot(0), w_of(c_begin), lane);
-#pragma unroll
-        for (int a = 1; a <= kWarmAhead; ++a)
-            chain_warm(p, sink, min(c_begin + a, c_end - 1), h, src, strip, lane, w_wave);
-        if (!w_wave) {
-            // The new rolling conv history (nothing in this kernel reads conv_state, and the
-            // chunk kernel has read the old history): the sequence's h_v * 8 workgroups split
-            // its C channels into contiguous ranges. Its round trip overlaps the W copy.
-            const int G = L.h_v * kStrips, g = h * kStrips + strip, per = (L.C + G - 1) / G;
-            const int ch_hi = min(L.C, (g + 1) * per);
-            for (int ch = g * per + lane; ch < ch_hi; ch += kWave) commit_history(p, ch, seq_lo, seq_hi - seq_lo, s);
-        }
-        // The copies have landed in LDS; the warm-ups may still be in flight. Bare barriers
-        // in this role: a release fence would also wait for the warm-up loads (LDS DMA counts
-        // as LDS writes).
-        if (w_wave) wait_vmcnt<kWarmAhead * kWarmLoadsW>();
-        __builtin_amdgcn_s_barrier();
-        for (int c = c_begin; c < c_end; ++c) {
-            const int q = (c - c_begin) & 1;
-            if (w_wave) {
-                if (c + 1 < c_end) chain_copy(lds3 + chain_w_slot(q ^ 1), w_of(c + 1), lane);
-            } else {
-                chain_copy(lds3 + chain_k_slot(q), kt_of(c), lane);
-            }
-            chain_warm(p, sink, min(c + 1 + kWarmAhead, c_end - 1), h, src, strip, lane, w_wave);
-            if (w_wave) wait_vmcnt<kWarmLoadsW>(); else wait_vmcnt<kWarmLoadsK>();   // this trip's copies done
-            __builtin_amdgcn_s_barrier();                         // barrier c
-        }
-        __builtin_amdgcn_s_waitcnt(0);
+        chain_output_role(p, lds, lane, w < 4 ? w - 2 : w - 4, sg, h, src, j0);
     }
 }
 
@@ -1400,6 +1312,18 @@ extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int
     const size_t base = ix_gdn_prefill_workspace_size(cfg, n_seq, total_T);
     if (!base) return 0;
     return base + (((size_t)total_T * cfg->h_v * ixg::kD * sizeof(float) + 255) & ~(size_t)255);
+}
+
+// The chunk kernel, then the chain. The conv activation is a template parameter of the chunk
+// kernel: inlined into every unrolled conv output, a runtime choice would carry the
+// activation's code in the kernels that do not use it.
+template <int DC>
+static void launch_prefill(const ixg::PrefillParams& p, dim3 tgrid, dim3 cgrid, dim3 cblock, bool silu,
+                           hipStream_t s) {
+    using namespace ixg;
+    if (silu) hipLaunchKernelGGL((tri_kernel<DC, true>), tgrid, dim3(kChunkThreads), 0, s, p);
+    else hipLaunchKernelGGL((tri_kernel<DC, false>), tgrid, dim3(kChunkThreads), 0, s, p);
+    hipLaunchKernelGGL(chain_kernel, cgrid, cblock, 0, s, p);
 }
 
 static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
@@ -1437,28 +1361,14 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const dim3 qgrid((unsigned)NC, (unsigned)cfg->h_k), vgrid((unsigned)(NC * cfg->h_v));
-    switch (cfg->d_conv) {
-        case 2:
-            hipLaunchKernelGGL(qk_kernel<2>, qgrid, dim3(kChunkThreads), 0, s, p);
-            hipLaunchKernelGGL(v_kernel<2>, vgrid, dim3(kChunkThreads), 0, s, p);
-            break;
-        case 3:
-            hipLaunchKernelGGL(qk_kernel<3>, qgrid, dim3(kChunkThreads), 0, s, p);
-            hipLaunchKernelGGL(v_kernel<3>, vgrid, dim3(kChunkThreads), 0, s, p);
-            break;
-        default:
-            hipLaunchKernelGGL(qk_kernel<4>, qgrid, dim3(kChunkThreads), 0, s, p);
-            hipLaunchKernelGGL(v_kernel<4>, vgrid, dim3(kChunkThreads), 0, s, p);
-            break;
-    }
+    const dim3 tgrid((unsigned)NC, (unsigned)cfg->h_k);
     const long long groups = (pairs + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
-    switch ((p.o ? 1 : 0) | (p.o_bf16 ? 2 : 0)) {
-        case 0: hipLaunchKernelGGL(chain_kernel<0>, cgrid, cblock, 0, s, p); break;
-        case 1: hipLaunchKernelGGL(chain_kernel<1>, cgrid, cblock, 0, s, p); break;
-        case 2: hipLaunchKernelGGL(chain_kernel<2>, cgrid, cblock, 0, s, p); break;
-        default: hipLaunchKernelGGL(chain_kernel<3>, cgrid, cblock, 0, s, p); break;
+    const bool silu = cfg->conv_act == IX_GDN_ACT_SILU;
+    switch (cfg->d_conv) {
+        case 2: launch_prefill<2>(p, tgrid, cgrid, cblock, silu, s); break;
+        case 3: launch_prefill<3>(p, tgrid, cgrid, cblock, silu, s); break;
+        default: launch_prefill<4>(p, tgrid, cgrid, cblock, silu, s); break;
     }
     if (gate)
         hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o,
