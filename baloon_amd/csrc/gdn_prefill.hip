@@ -60,9 +60,8 @@ struct Ws {
                          // inclusive cumulative log decay G (padded rows repeat the last)
     uint8_t* Kp;         // [NC][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
     uint16_t* Qf;        // [NC][h_k] Q (64 x 128) as split-bf16 A fragments
-    float* V;            // [NC][h_v][64][128] conv outputs of the v channels (zero past the chunk end)
 };
-constexpr int kWsSections = 9;
+constexpr int kWsSections = 8;
 constexpr int kPRow = 2 * 128 + 16;                     // key plane row: 128 bf16, 16 bytes of padding
 constexpr int kKPlane = 64 * kPRow;                     // one plane (hi or lo) of 64 keys
 constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 34,816 bytes
@@ -76,7 +75,6 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSec
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
         sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk * kChunk,
         sizeof(float) * NC * c->h_v * 2 * kChunk, (size_t)kKSlot * NC * c->h_k, sizeof(uint16_t) * NC * c->h_k * 4 * 4 * 2 * 512,
-        sizeof(float) * NC * c->h_v * kChunk * 128,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -93,7 +91,6 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.G = reinterpret_cast<float*>(base + off[5]);
     w.Kp = reinterpret_cast<uint8_t*>(base + off[6]);
     w.Qf = reinterpret_cast<uint16_t*>(base + off[7]);
-    w.V = reinterpret_cast<float*>(base + off[8]);
     return w;
 }
 
@@ -619,19 +616,6 @@ __global__ void __launch_bounds__(kChunkThreads) tri_kernel(const PrefillParams 
             *reinterpret_cast<uint32_t*>(dst + kQKPlane + o) = lo;
         }
     }
-    // v rows of the mapped v heads (group g takes heads g, g + 2, ...), same layout of work,
-    // to the workspace as fp32 rows [64][128], zero past the chunk end.
-    for (int m = grp; m < nmap; m += 2) {
-        const int h = mapped_head(L, src, m);
-        ConvIn<DC> in;
-        conv_load<DC>(p, g, g.lo, v_channel(L, h, c2), tb, nt, in);
-        float y0[kConvTok], y1[kConvTok];
-        conv_run<DC, SILU>(in, y0, y1);
-        float* V = p.ws.V + ((size_t)c * L.h_v + h) * kChunk * kD + c2;
-#pragma unroll
-        for (int t = 0; t < kConvTok; ++t)
-            *reinterpret_cast<float2*>(V + (tb + t) * kD) = t < nt ? float2{y0[t], y1[t]} : float2{0.0f, 0.0f};
-    }
     lds_barrier();
 
     // The chain's key planes (row t: 128 bf16, then 16 bytes of padding; hi plane, then lo)
@@ -794,14 +778,16 @@ constexpr int kChainWaves = 8;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
 constexpr int kKSlots = 3;                              // key slots in a ring
 constexpr int kTSlot = 12 * kPlane;                     // T': its 6 nonzero fragments x 2 planes
-constexpr int kVSlot = 4 * kPlane + 2 * kChunk * 4;     // V (4 row tiles, accumulator layout), E, Gam
+constexpr int kVSlot = 2 * kChunk * 4;                  // decay factors E, then Gam
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
 constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in fp32
 constexpr int kWBytes = 2 * 4 * kPlane;                 // the two halves of W: 4 row tiles in fp32 each
 constexpr int kDgBytes = 4 * kPlane + 16;               // Dg: 2 k-steps x 2 planes, then gam
 constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlot, kOffH = kOffV + kVSlot;
-constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes;
-constexpr int kChainLds = kOffG + kDgBytes;             // 145,936 bytes
+constexpr int kXRows = 72;                              // the D wave's x staging: rows -3 .. 68 of a chunk
+constexpr int kXBytes = kXRows * kStrip * 2;            // 16 bf16 channels per row
+constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
+constexpr int kChainLds = kOffX + kXBytes;              // 144,144 bytes
 
 typedef __attribute__((address_space(3))) bf8 lds_bf8;
 typedef __attribute__((address_space(3))) v4 lds_v4;
@@ -981,27 +967,101 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     }
 }
 
+// The D wave's v columns. Chunk c_k's x rows -3 .. 68 (relative to its first token) for the
+// strip's 16 v channels, one channel pair per lane: lane l loads pair l & 7 of rows
+// 8 i + (l >> 3) - 3, i = 0..8, as one word. Rows before the sequence start come from the old
+// conv history, rows past its end repeat its last token (their V rows are zeroed).
+struct XStage { uint32_t w[9]; };
+template <int DC>
+__device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo& sg, int k, int h, int strip,
+                                           int lane, XStage& xs) {
+    const Layer& L = p.L;
+    const int ch = v_channel(L, h, strip * kStrip + 2 * (lane & 7));
+    const int pos0 = k * kChunk, last = sg.hi - sg.lo - 1;
+    const uint16_t* hist = p.conv_state + ((size_t)sg.s * L.C + ch) * (DC - 1) + (DC - 1);
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+        const int pos = pos0 + 8 * i + (lane >> 3) - 3;   // >= 0 for i > 0
+        if (i == 0 && pos < 0) {
+            const int hp = max(pos, -(DC - 1));             // rows before -(DC-1) feed no output
+            xs.w[i] = (uint32_t)hist[hp] | ((uint32_t)hist[hp + (DC - 1)] << 16);
+        } else {
+            xs.w[i] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(sg.lo + min(pos, last)) * L.C + ch);
+        }
+    }
+}
+// The conv of the staged rows, in the D wave's accumulator layout: lane (li, lg4) gets
+// V[16 mt + 4 lg4 + e][channel li], e = 0..3, zero for rows at or past len. The rows pass
+// through LDS (row r + 3 at 32 bytes per row), which this wave alone uses. Same accumulation
+// order as the fused kernels' conv.
+template <int DC, bool SILU>
+__device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int lane, const float (&w)[DC], int len,
+                                           v4 (&V)[4]) {
+    typedef __attribute__((address_space(3))) uint32_t lds_u32;
+    typedef __attribute__((address_space(3))) uint16_t lds_u16;
+    lds_u8* xst = (lds_u8*)lds + kOffX;
+    // The words go in as 32-bit and come back as 16-bit values: the fences keep the compiler
+    // from reordering the two (the wave's own LDS accesses then complete in program order).
+    __asm__ volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 9; ++i) *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) = xs.w[i];
+    __asm__ volatile("" ::: "memory");
+    const int li = lane & 15, lg4 = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+        const int t0 = 16 * mt + 4 * lg4;
+        float xv[DC + 3];
+#pragma unroll
+        for (int j = 0; j < DC + 3; ++j)
+            xv[j] = __uint_as_float((uint32_t) * (const lds_u16*)(xst + (t0 - (DC - 1) + j + 3) * 32 + 2 * li) << 16);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < DC; ++i) acc = fmaf(xv[e + i], w[i], acc);
+            if constexpr (SILU) acc = acc * sigmoid_f(acc);
+            V[mt][e] = t0 + e < len ? acc : 0.0f;
+        }
+    }
+    __asm__ volatile("" ::: "memory");
+}
+
 // D role (wave 4): per chunk, D = T' (V - diag(Gam) (W_0 + W_1)) from the state waves' halves of
-// W, with V, the decay factors and T' read from the value slot in the preceding alpha.
-__device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
-    const int lg4 = lane >> 4;
-    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
-    const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
+// W, with the decay factors and T' read from the value slot in the preceding alpha. The wave
+// builds the strip's v columns itself, a chunk ahead: chunk c_0's before alpha_0 (when it also
+// reads their old conv history, which the feed wave replaces only after that barrier), chunk
+// c_{k+1}'s in alpha_k, from x rows loaded a chunk earlier.
+template <int DC, bool SILU>
+__device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
+                                             int h, int strip) {
+    const Layer& L = p.L;
+    const int lg4 = lane >> 4, n = sg.n;
+    const lds_u8* eb = lane_at(lds, kOffV + 16 * lg4);
     const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
     lds_u8* hb = lane_at(lds, kOffH + kHandS + lane * 16);
     lds_u8* gb = lane_at(lds, kOffG + lane * 16);
+    float cw[DC];                                           // conv weights of the lane's channel
+    {
+        const uint16_t* wp = L.conv_w + (size_t)v_channel(L, h, strip * kStrip + (lane & 15)) * DC;
+#pragma unroll
+        for (int i = 0; i < DC; ++i) cw[i] = bf16_to_f32(wp[i]);
+    }
+    XStage xs;
+    v4 Vc[4], Vn[4];
+    stage_load<DC>(p, sg, 0, h, strip, lane, xs);
+    stage_conv<DC, SILU>(lds, xs, lane, cw, seq_chunk(sg, 0).len, Vc);
+    if (n > 1) stage_load<DC>(p, sg, 1, h, strip, lane, xs);
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // alpha_k: chunk c_k in the value slot
-        v4 V[4], E[4], Gm[4];
+        v4 E[4], Gm[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
-            V[mt] = *(const lds_v4*)(vb + mt * kPlane);
             E[mt] = *(const lds_v4*)(eb + mt * 64);
             Gm[mt] = *(const lds_v4*)(eb + 4 * kChunk + mt * 64);
         }
-        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kPlane +
-                                                                            4 * kChunk + 4 * (kChunk - 1));
+        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kChunk +
+                                                                            4 * (kChunk - 1));
         bf8 F0[4][2], F1[4][2];                             // T' (mt, 0), mt = 0..3; T' (2, 1), (3, 1)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) {
@@ -1010,13 +1070,17 @@ __device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) F1[j][pl] = *(const lds_bf8*)(fb + (2 * (4 + j) + pl) * kPlane);
         }
+        if (k + 1 < n) {
+            stage_conv<DC, SILU>(lds, xs, lane, cw, seq_chunk(sg, k + 1).len, Vn);
+            if (k + 2 < n) stage_load<DC>(p, sg, k + 2, h, strip, lane, xs);
+        }
         lds_barrier();                                      // beta_k: both halves of W_k handed over
         v4 X[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const v4 w0 = *(const lds_v4*)(wb + mt * kPlane), w1 = *(const lds_v4*)(wb + (4 + mt) * kPlane);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], V[mt][e]);
+            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], Vc[mt][e]);
         }
         bf8 xh[2], xl[2];
         split_tiles(X[0], X[1], xh[0], xl[0]);
@@ -1037,6 +1101,8 @@ __device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
         if (lane == 0) *(__attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane) = gam;
 #pragma unroll
         for (int m = 0; m < 4; ++m) *(lds_v4*)(hb + m * kPlane) = D[m];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) Vc[m] = Vn[m];
     }
     lds_barrier();                                          // alpha_n
 }
@@ -1147,26 +1213,21 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 
 // Feed role (wave 5). In alpha_{k-1} it starts copying chunk c_{k+1}'s key planes (written by
 // the chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads,
-// and waits for them at the end of alpha_k. In beta_k it writes chunk c_{k+1}'s strip of V (in the D wave's accumulator layout: lane
-// (li, lg4) holds V[16 mt + 4 lg4 + r][j0 + li]), the decay factors (E, then Gam) and T' (its 6
-// nonzero fragments) into the value slot, then loads chunk c_{k+2}'s. Before the first chunk it
-// writes the new rolling conv history of the workgroup's share of the sequence's channels (the
-// h_v * 8 workgroups of a sequence split its C channels into contiguous ranges); nothing else
-// in this kernel touches conv_state.
+// and waits for them at the end of alpha_k. In beta_k it writes chunk c_{k+1}'s decay factors
+// (E, then Gam) and T' (its 6 nonzero fragments) into the value slot, then loads chunk
+// c_{k+2}'s. It also writes the new rolling conv history of the workgroup's channels: before
+// alpha_0 its share of the sequence's q/k channels (the h_v * 8 workgroups of a sequence split
+// them into contiguous ranges; the chunk kernel has read their old history), in alpha_0 the
+// strip's 16 v channels (whose old history the D wave read before alpha_0). Nothing else in
+// this kernel writes conv_state.
 __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
                                                 int h, int strip, int src) {
     typedef __attribute__((address_space(3))) u4x lds_u4;
     const Layer& L = p.L;
-    const int li = lane & 15, lg4 = lane >> 4;
-    v4 vv[4], eg;
+    v4 eg;
     u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
     auto load = [&](int k) {
         const size_t chh = (size_t)(sg.c0 + min(k, sg.n - 1)) * L.h_v + h;
-        const float* V = p.ws.V + chh * kChunk * kD + strip * kStrip + li;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) vv[mt][r] = V[(16 * mt + 4 * lg4 + r) * kD];
         eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
         const u4x* tsrc = reinterpret_cast<const u4x*>(p.ws.Tf + chh * kFragM) + lane;
 #pragma unroll
@@ -1176,10 +1237,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         }
     };
     auto produce = [&]() {
-        lds_u8* vs = (lds_u8*)lds + kOffV;
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) *(lds_v4*)(vs + mt * kPlane + lane * 16) = vv[mt];
-        if (lane < 32) *(lds_v4*)(vs + 4 * kPlane + lane * 16) = eg;
+        if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + lane * 16) = eg;
         lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
 #pragma unroll
         for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
@@ -1202,8 +1260,8 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     };
 
     {
-        const int G = L.h_v * kStrips, gi = h * kStrips + strip, per = (L.C + G - 1) / G;
-        const int ch_hi = min(L.C, (gi + 1) * per);
+        const int G = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + G - 1) / G;
+        const int ch_hi = min(cqk, (gi + 1) * per);
         for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
     }
     copy_keys(0);
@@ -1213,11 +1271,13 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     __builtin_amdgcn_sched_barrier(0);
     load(1);
     wait_barrier();                                         // alpha_0
+    if (lane < kStrip) commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
     for (int k = 0; k < sg.n; ++k) {
         // Chunk c_{k+2}'s keys go to the slot of chunk c_{k-1}, whose K^T the state waves read in
         // beta_{k-1}; they land by the end of alpha_{k+1}. Waiting here for all but the 34 copies
-        // just issued leaves chunk c_{k+1}'s keys (issued in alpha_{k-1}) and value operands
-        // (loaded in beta_{k-1}) landed: a wave's loads complete in issue order.
+        // just issued leaves chunk c_{k+1}'s keys (issued in alpha_{k-1}), its value operands
+        // (loaded in beta_{k-1}) and the history writes of alpha_0 complete: a wave's vector
+        // memory operations complete in issue order.
         __asm__ volatile("" ::: "memory");
         if (k + 2 < sg.n) {
             copy_keys(k + 2);
@@ -1241,6 +1301,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     }
 }
 
+template <int DC, bool SILU>
 __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const PrefillParams p) {
     __shared__ __align__(16) uint8_t lds[kChainLds];
 
@@ -1274,7 +1335,7 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
     } else if (w == 4) {
-        chain_d_role(lds, lane, sg.n);
+        chain_d_role<DC, SILU>(p, lds, lane, sg, h, strip);
     } else if (w == 5) {
         chain_feed_role(p, lds, lane, sg, h, strip, src);
     } else {
@@ -1321,9 +1382,13 @@ template <int DC>
 static void launch_prefill(const ixg::PrefillParams& p, dim3 tgrid, dim3 cgrid, dim3 cblock, bool silu,
                            hipStream_t s) {
     using namespace ixg;
-    if (silu) hipLaunchKernelGGL((tri_kernel<DC, true>), tgrid, dim3(kChunkThreads), 0, s, p);
-    else hipLaunchKernelGGL((tri_kernel<DC, false>), tgrid, dim3(kChunkThreads), 0, s, p);
-    hipLaunchKernelGGL(chain_kernel, cgrid, cblock, 0, s, p);
+    if (silu) {
+        hipLaunchKernelGGL((tri_kernel<DC, true>), tgrid, dim3(kChunkThreads), 0, s, p);
+        hipLaunchKernelGGL((chain_kernel<DC, true>), cgrid, cblock, 0, s, p);
+    } else {
+        hipLaunchKernelGGL((tri_kernel<DC, false>), tgrid, dim3(kChunkThreads), 0, s, p);
+        hipLaunchKernelGGL((chain_kernel<DC, false>), cgrid, cblock, 0, s, p);
+    }
 }
 
 static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
