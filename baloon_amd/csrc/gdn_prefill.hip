@@ -562,7 +562,7 @@ __device__ __forceinline__ void decay_scan(const PrefillParams& p, const ChunkGe
 // Every barrier orders LDS only, so no wave waits for its own global stores.
 // ---------------------------------------------------------------------------------------
 template <int DC, bool SILU>
-__global__ void __launch_bounds__(kChunkThreads) tri_kernel(const PrefillParams p) {
+__global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per_eu(4))) tri_kernel(const PrefillParams p) {
     __shared__ __align__(16) uint8_t lds[4 * kQKPlane];   // k hi, k lo, q hi, q lo; then A/T of two heads
     __shared__ __align__(16) float G_s[2][kChunk], B_s[2][kChunk];
     uint8_t* Kp = lds;
@@ -618,16 +618,20 @@ __global__ void __launch_bounds__(kChunkThreads) tri_kernel(const PrefillParams 
     }
     lds_barrier();
 
-    // The chain's key planes (row t: 128 bf16, then 16 bytes of padding; hi plane, then lo)
-    // and Q fragments (rows t, k = channel in kperm order), from the swizzled planes: every
-    // thread moves 4 of the 16-byte key chunks and 4 Q fragment chunks.
+    // The chain's key planes (row t: 128 bf16 with each 32-channel block in kperm order, then
+    // 16 bytes of padding; hi plane, then lo) and Q fragments (rows t, k = channel in kperm
+    // order), from the swizzled planes: every thread moves 4 of the 16-byte key chunks and 4 Q
+    // fragment chunks. Key chunk j of a row holds channels 32 (j / 4) + 4 (j % 4) .. +3, then
+    // the 4 channels 16 later.
     {
         uint8_t* kg = p.ws.Kp + ((size_t)c * L.h_k + src) * kKSlot;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = tid + u * kChunkThreads, pl = e >> 10, t = (e >> 4) & 63, cc = e & 15;
-            *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * cc) =
-                *reinterpret_cast<const u4x*>(Kp + pl * kQKPlane + qk_off(t, 8 * cc));
+            const int c0 = 32 * (cc >> 2) + 4 * (cc & 3);
+            const uint2 a = *reinterpret_cast<const uint2*>(Kp + pl * kQKPlane + qk_off(t, c0));
+            const uint2 b = *reinterpret_cast<const uint2*>(Kp + pl * kQKPlane + qk_off(t, c0 + 16));
+            *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * cc) = u4x{a.x, a.y, b.x, b.y};
         }
         uint16_t* Qg = p.ws.Qf + ((size_t)c * L.h_k + src) * kFragW;
 #pragma unroll
@@ -758,41 +762,37 @@ __global__ void __launch_bounds__(kChunkThreads) tri_kernel(const PrefillParams 
 //            outputs and Dg_k (split) with gam_k for the state waves.
 // Products take their k index in accumulator row order (kperm), so an accumulator tile pair,
 // split to bf16 hi/lo, is the next product's B operand as it stands. The D wave reads chunk
-// c_k's V, decay factors and T' from the value slot in alpha_k, and the state waves read the
-// K^T fragments of chunk c_k in beta_k, each while the other side works; the K fragments of
-// W are read as the products need them.
+// c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
 // The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
-// alpha_{k+1}, with Q, M and Gam loaded from the workspace two chunks ahead. The feed wave (5)
-// copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3 with direct global-to-LDS loads
-// issued in alpha_{k-1} (the slot last held chunk c_{k-2}, read until beta_{k-2}), and in
-// beta_k writes
-// chunk c_{k+1}'s V strip, decay factors and T' fragments into the value slot (read by the D
-// wave in alpha_k) from registers loaded a chunk earlier. Before the first chunk it writes the
-// new rolling conv history of the workgroup's share of the sequence's channels.
+// alpha_{k+1}, with Q, M and Gam loaded from the workspace two chunks ahead; in beta_k each
+// also builds row tile r of chunk c_{k+1}'s V (the conv of the strip's v channels) into the
+// value slot. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
+// with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
+// until alpha_{k-1}), and in beta_k writes chunk c_{k+1}'s decay factors and T' fragments into
+// the value slot from registers loaded in alpha_k; it also writes the new rolling conv history
+// of the workgroup's channels.
 // A last alpha_n finishes S_n (state waves) and O_{n-1} (output waves).
-// Waves w and w + 4 share a SIMD: the state waves' partners (the D wave, the feed wave) work
-// in beta, the state waves in alpha.
+// Waves w and w + 4 share a SIMD: the state waves' partners (the D wave, the feed wave) only
+// read and copy in alpha, where the state waves work.
 constexpr int kStrip = 16;                              // state columns per chain workgroup
 constexpr int kStrips = kD / kStrip;                    // 8
 constexpr int kChainWaves = 8;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
 constexpr int kKSlots = 3;                              // key slots in a ring
 constexpr int kTSlot = 12 * kPlane;                     // T': its 6 nonzero fragments x 2 planes
-constexpr int kVSlot = 2 * kChunk * 4;                  // decay factors E, then Gam
+constexpr int kVSlot = 4 * kPlane + 2 * kChunk * 4;     // V (4 row tiles, accumulator layout), E, Gam
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
 constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in fp32
 constexpr int kWBytes = 2 * 4 * kPlane;                 // the two halves of W: 4 row tiles in fp32 each
 constexpr int kDgBytes = 4 * kPlane + 16;               // Dg: 2 k-steps x 2 planes, then gam
 constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlot, kOffH = kOffV + kVSlot;
-constexpr int kXRows = 72;                              // the D wave's x staging: rows -3 .. 68 of a chunk
-constexpr int kXBytes = kXRows * kStrip * 2;            // 16 bf16 channels per row
+constexpr int kXRows = 24;                              // an output wave's x staging: rows 16 r - 3 .. 16 r + 20
+constexpr int kXBytes = 4 * kXRows * kStrip * 2;        // 16 bf16 channels per row, 4 output waves
 constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
-constexpr int kChainLds = kOffX + kXBytes;              // 144,144 bytes
+constexpr int kChainLds = kOffX + kXBytes;              // 149,008 bytes
 
 typedef __attribute__((address_space(3))) bf8 lds_bf8;
 typedef __attribute__((address_space(3))) v4 lds_v4;
-typedef uint32_t u2v __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) u2v lds_u2;
 
 // This lane's address in an LDS area at byte offset off (which includes the lane's own part),
 // made opaque to the compiler: reads and writes at base + (a constant below 64 KiB) then use
@@ -815,15 +815,16 @@ __device__ __forceinline__ void split_tiles(const v4& a, const v4& b, bf8& hi, b
     lo = __builtin_bit_cast(bf8, u4x{l0, l1, l2, l3});
 }
 
+// Key slots hold each 32-channel block of a key row in kperm order: channels 4 a .. 4 a + 3,
+// then 16 + 4 a .. 16 + 4 a + 3, for a = 0..3, i.e. channel 32 b + 16 h + 4 a + e sits at
+// position 32 b + 8 a + 4 h + e.
 // K fragment (token tile mt, channel k-step ks) of a key slot: A operand of K S. Lane
-// (li, lg4) reads row 16 mt + li, channels 32 ks + 4 lg4 .. +3 and 32 ks + 16 + 4 lg4 .. +3,
-// from the lane base kb = slot + li * kPRow + 8 lg4.
+// (li, lg4) reads row 16 mt + li, channels 32 ks + 4 lg4 .. +3 and 32 ks + 16 + 4 lg4 .. +3:
+// 16 contiguous bytes per plane from the lane base kb = slot + li * kPRow + 16 lg4.
 __device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, int ks, bf8& hi, bf8& lo) {
     const int o = mt * 16 * kPRow + ks * 64;
-    const u2v a = *(const lds_u2*)(kb + o), b = *(const lds_u2*)(kb + o + 32);
-    const u2v c = *(const lds_u2*)(kb + kKPlane + o), d = *(const lds_u2*)(kb + kKPlane + o + 32);
-    hi = __builtin_bit_cast(bf8, u4x{a.x, a.y, b.x, b.y});
-    lo = __builtin_bit_cast(bf8, u4x{c.x, c.y, d.x, d.y});
+    hi = *(const lds_bf8*)(kb + o);
+    lo = *(const lds_bf8*)(kb + kKPlane + o);
 }
 
 // K^T fragment (channel tile m, token k-step ks) of a key slot: A operand of K^T Dg, by
@@ -831,9 +832,10 @@ __device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, int ks, bf8& hi
 // j & 3 of the 8-byte reads of lanes (j >> 2) + 4 e, e = 0..3). Lane i of lane group g reads
 // channels 16 m + 4 (i & 3) .. +3 of token 32 ks + 4 g + (i >> 2) (then of the token 16
 // later), so it receives channel 16 m + i at tokens 32 ks + 4 g + e (+ 16): entries e (4 + e)
-// of its kperm fragment chunk. Lane base tb = slot + (4 g + (i >> 2)) * kPRow + 8 (i & 3).
+// of its kperm fragment chunk. Those 4 channels sit at position 32 (m / 2) + 8 (i & 3) +
+// 4 (m & 1); lane base tb = slot + (4 g + (i >> 2)) * kPRow + 16 (i & 3).
 __device__ __forceinline__ void kt_frag(const lds_u8* tb, int m, int ks, bf8& hi, bf8& lo) {
-    const int o = ks * 32 * kPRow + m * 32;
+    const int o = ks * 32 * kPRow + (m >> 1) * 64 + (m & 1) * 8;
     const uint2 a = lds_tr16(tb + o), b = lds_tr16(tb + o + 16 * kPRow);
     const uint2 c = lds_tr16(tb + kKPlane + o), d = lds_tr16(tb + kKPlane + o + 16 * kPRow);
     hi = __builtin_bit_cast(bf8, u4x{a.x, a.y, b.x, b.y});
@@ -903,8 +905,8 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     lds_u8 *kb[kKSlots], *tb[kKSlots];
 #pragma unroll
     for (int q = 0; q < kKSlots; ++q) {
-        kb[q] = lane_at(lds, kOffK + q * kKSlot + li * kPRow + 8 * lg4);
-        tb[q] = lane_at(lds, kOffK + q * kKSlot + (4 * lg4 + (li >> 2)) * kPRow + 8 * (li & 3));
+        kb[q] = lane_at(lds, kOffK + q * kKSlot + li * kPRow + 16 * lg4);
+        tb[q] = lane_at(lds, kOffK + q * kKSlot + (4 * lg4 + (li >> 2)) * kPRow + 16 * (li & 3));
     }
     lds_u8* hb = lane_at(lds, kOffH + 4 * half * kPlane + lane * 16);     // S k-steps 2 half, 2 half + 1
     lds_u8* wb = lane_at(lds, kOffW + 4 * half * kPlane + lane * 16);
@@ -949,8 +951,8 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // beta_k
         const int q1 = q == kKSlots - 1 ? 0 : q + 1;
-        load_kt(q);                                         // K^T of chunk c_k, for S_{k+1}
         lds_barrier();                                      // alpha_{k+1}: Dg_k, gam_k handed over
+        load_kt(q);                                         // K^T of chunk c_k, for S_{k+1}
         bf8 dh[2], dl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -967,21 +969,22 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     }
 }
 
-// The D wave's v columns. Chunk c_k's x rows -3 .. 68 (relative to its first token) for the
-// strip's 16 v channels, one channel pair per lane: lane l loads pair l & 7 of rows
-// 8 i + (l >> 3) - 3, i = 0..8, as one word. Rows before the sequence start come from the old
-// conv history, rows past its end repeat its last token (their V rows are zeroed).
-struct XStage { uint32_t w[9]; };
+// The strip's v columns, built by the output waves: wave r builds row tile r of V. x rows
+// 16 r - 3 + 8 i + (l >> 3), i = 0..2, of a chunk (relative to its first token) for the strip's
+// 16 v channels, one channel pair per lane: lane l loads pair l & 7 as one word. Rows before the
+// sequence start come from the old conv history, rows past its end repeat its last token
+// (their V rows are zeroed).
+struct XStage { uint32_t w[3]; };
 template <int DC>
-__device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo& sg, int k, int h, int strip,
+__device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo& sg, int k, int h, int strip, int r,
                                            int lane, XStage& xs) {
     const Layer& L = p.L;
     const int ch = v_channel(L, h, strip * kStrip + 2 * (lane & 7));
-    const int pos0 = k * kChunk, last = sg.hi - sg.lo - 1;
+    const int pos0 = k * kChunk + 16 * r - 3, last = sg.hi - sg.lo - 1;
     const uint16_t* hist = p.conv_state + ((size_t)sg.s * L.C + ch) * (DC - 1) + (DC - 1);
 #pragma unroll
-    for (int i = 0; i < 9; ++i) {
-        const int pos = pos0 + 8 * i + (lane >> 3) - 3;   // >= 0 for i > 0
+    for (int i = 0; i < 3; ++i) {
+        const int pos = pos0 + 8 * i + (lane >> 3);        // >= 0 for i > 0
         if (i == 0 && pos < 0) {
             const int hp = max(pos, -(DC - 1));             // rows before -(DC-1) feed no output
             xs.w[i] = (uint32_t)hist[hp] | ((uint32_t)hist[hp + (DC - 1)] << 16);
@@ -990,78 +993,61 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo&
         }
     }
 }
-// The conv of the staged rows, in the D wave's accumulator layout: lane (li, lg4) gets
-// V[16 mt + 4 lg4 + e][channel li], e = 0..3, zero for rows at or past len. The rows pass
-// through LDS (row r + 3 at 32 bytes per row), which this wave alone uses. Same accumulation
-// order as the fused kernels' conv.
+// The conv of the staged rows into row tile r of the value slot, in the D wave's accumulator
+// layout: lane (li, lg4) holds V[16 r + 4 lg4 + e][channel li], e = 0..3, zero for rows at or
+// past len. The rows pass through the wave's own LDS staging area (row 16 r - 3 + i at 32 i
+// bytes). Same accumulation order as the fused kernels' conv.
 template <int DC, bool SILU>
-__device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int lane, const float (&w)[DC], int len,
-                                           v4 (&V)[4]) {
+__device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int r, int lane, const float (&w)[DC],
+                                           int len) {
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) uint16_t lds_u16;
-    lds_u8* xst = (lds_u8*)lds + kOffX;
+    lds_u8* xst = (lds_u8*)lds + kOffX + r * kXRows * 32;
     // The words go in as 32-bit and come back as 16-bit values: the fences keep the compiler
     // from reordering the two (the wave's own LDS accesses then complete in program order).
     __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 9; ++i) *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) = xs.w[i];
+    for (int i = 0; i < 3; ++i) *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) = xs.w[i];
     __asm__ volatile("" ::: "memory");
-    const int li = lane & 15, lg4 = lane >> 4;
+    const int li = lane & 15, lg4 = lane >> 4, t0 = 16 * r + 4 * lg4;
+    float xv[DC + 3];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-        const int t0 = 16 * mt + 4 * lg4;
-        float xv[DC + 3];
+    for (int j = 0; j < DC + 3; ++j)
+        xv[j] = __uint_as_float((uint32_t) * (const lds_u16*)(xst + (4 * lg4 - (DC - 1) + j + 3) * 32 + 2 * li) << 16);
+    v4 V;
 #pragma unroll
-        for (int j = 0; j < DC + 3; ++j)
-            xv[j] = __uint_as_float((uint32_t) * (const lds_u16*)(xst + (t0 - (DC - 1) + j + 3) * 32 + 2 * li) << 16);
+    for (int e = 0; e < 4; ++e) {
+        float acc = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int i = 0; i < DC; ++i) acc = fmaf(xv[e + i], w[i], acc);
-            if constexpr (SILU) acc = acc * sigmoid_f(acc);
-            V[mt][e] = t0 + e < len ? acc : 0.0f;
-        }
+        for (int i = 0; i < DC; ++i) acc = fmaf(xv[e + i], w[i], acc);
+        if constexpr (SILU) acc = acc * sigmoid_f(acc);
+        V[e] = t0 + e < len ? acc : 0.0f;
     }
+    *(lds_v4*)((lds_u8*)lds + kOffV + r * kPlane + lane * 16) = V;
     __asm__ volatile("" ::: "memory");
 }
 
 // D role (wave 4): per chunk, D = T' (V - diag(Gam) (W_0 + W_1)) from the state waves' halves of
-// W, with the decay factors and T' read from the value slot in the preceding alpha. The wave
-// builds the strip's v columns itself, a chunk ahead: chunk c_0's before alpha_0 (when it also
-// reads their old conv history, which the feed wave replaces only after that barrier), chunk
-// c_{k+1}'s in alpha_k, from x rows loaded a chunk earlier.
-template <int DC, bool SILU>
-__device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
-                                             int h, int strip) {
-    const Layer& L = p.L;
-    const int lg4 = lane >> 4, n = sg.n;
-    const lds_u8* eb = lane_at(lds, kOffV + 16 * lg4);
+// W, with V, the decay factors and T' read from the value slot in the preceding alpha.
+__device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
+    const int lg4 = lane >> 4;
+    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
     const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
     lds_u8* hb = lane_at(lds, kOffH + kHandS + lane * 16);
     lds_u8* gb = lane_at(lds, kOffG + lane * 16);
-    float cw[DC];                                           // conv weights of the lane's channel
-    {
-        const uint16_t* wp = L.conv_w + (size_t)v_channel(L, h, strip * kStrip + (lane & 15)) * DC;
-#pragma unroll
-        for (int i = 0; i < DC; ++i) cw[i] = bf16_to_f32(wp[i]);
-    }
-    XStage xs;
-    v4 Vc[4], Vn[4];
-    stage_load<DC>(p, sg, 0, h, strip, lane, xs);
-    stage_conv<DC, SILU>(lds, xs, lane, cw, seq_chunk(sg, 0).len, Vc);
-    if (n > 1) stage_load<DC>(p, sg, 1, h, strip, lane, xs);
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // alpha_k: chunk c_k in the value slot
-        v4 E[4], Gm[4];
+        v4 V[4], E[4], Gm[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
+            V[mt] = *(const lds_v4*)(vb + mt * kPlane);
             E[mt] = *(const lds_v4*)(eb + mt * 64);
             Gm[mt] = *(const lds_v4*)(eb + 4 * kChunk + mt * 64);
         }
-        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kChunk +
-                                                                            4 * (kChunk - 1));
+        const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kPlane +
+                                                                            4 * kChunk + 4 * (kChunk - 1));
         bf8 F0[4][2], F1[4][2];                             // T' (mt, 0), mt = 0..3; T' (2, 1), (3, 1)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) {
@@ -1070,17 +1056,13 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
 #pragma unroll
             for (int j = 0; j < 2; ++j) F1[j][pl] = *(const lds_bf8*)(fb + (2 * (4 + j) + pl) * kPlane);
         }
-        if (k + 1 < n) {
-            stage_conv<DC, SILU>(lds, xs, lane, cw, seq_chunk(sg, k + 1).len, Vn);
-            if (k + 2 < n) stage_load<DC>(p, sg, k + 2, h, strip, lane, xs);
-        }
         lds_barrier();                                      // beta_k: both halves of W_k handed over
         v4 X[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             const v4 w0 = *(const lds_v4*)(wb + mt * kPlane), w1 = *(const lds_v4*)(wb + (4 + mt) * kPlane);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], Vc[mt][e]);
+            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], V[mt][e]);
         }
         bf8 xh[2], xl[2];
         split_tiles(X[0], X[1], xh[0], xl[0]);
@@ -1101,17 +1083,17 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
         if (lane == 0) *(__attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane) = gam;
 #pragma unroll
         for (int m = 0; m < 4; ++m) *(lds_v4*)(hb + m * kPlane) = D[m];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) Vc[m] = Vn[m];
     }
     lds_barrier();                                          // alpha_n
 }
 
 // Output role (waves 2, 3, 6, 7; row tile r): rows 16 r .. 16 r + 15 of every chunk's outputs,
 // O = diag(Gam) Q S + M D, with Q, M and Gam from the workspace, loaded two chunks ahead into
-// two alternating operand sets. In beta_k the wave forms diag(Gam) Q S of chunk c_k, then loads
-// chunk c_{k+2}'s Q and Gam into the set it used; in alpha_{k+1} it adds M D, stores the rows and
-// loads chunk c_{k+2}'s M.
+// two alternating operand sets. In beta_k the wave forms diag(Gam) Q S of chunk c_k, builds row
+// tile r of chunk c_{k+1}'s V, then loads chunk c_{k+2}'s Q and Gam into the set it used and its
+// x rows; in alpha_{k+1} it adds M D, stores the rows and loads chunk c_{k+2}'s M. Row tile r of
+// chunk c_0's V is built before alpha_0, when the wave also reads the old conv history (wave 0's
+// first rows), which the feed wave replaces only after that barrier.
 struct OutQ {
     bf8 qf[4][2];
     v4 g;                 // exp(G_t) at this lane's rows
@@ -1139,10 +1121,21 @@ __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const S
         for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
 }
 
+template <int DC, bool SILU>
 __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_t* lds, int lane, int r,
-                                                  const SeqGeo& sg, int h, int src, int j0) {
+                                                  const SeqGeo& sg, int h, int src, int strip) {
     const Layer& L = p.L;
-    const int li = lane & 15, lg4 = lane >> 4;
+    const int li = lane & 15, lg4 = lane >> 4, j0 = strip * kStrip;
+    float cw[DC];                                           // conv weights of the lane's v channel
+    {
+        const uint16_t* wp = L.conv_w + (size_t)v_channel(L, h, j0 + li) * DC;
+#pragma unroll
+        for (int i = 0; i < DC; ++i) cw[i] = bf16_to_f32(wp[i]);
+    }
+    XStage xs;
+    stage_load<DC>(p, sg, 0, h, strip, r, lane, xs);
+    stage_conv<DC, SILU>(lds, xs, r, lane, cw, seq_chunk(sg, 0).len);
+    if (sg.n > 1) stage_load<DC>(p, sg, 1, h, strip, r, lane, xs);
     OutQ q0, q1;
     OutM m0, m1;
     chain_out_load_q(p, sg, 0, h, src, r, lane, q0);
@@ -1182,6 +1175,10 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * Q.g[i];
+        if (k + 1 < sg.n) {                                 // row tile r of chunk c_{k+1}'s V
+            stage_conv<DC, SILU>(lds, xs, r, lane, cw, seq_chunk(sg, k + 1).len);
+            if (k + 2 < sg.n) stage_load<DC>(p, sg, k + 2, h, strip, r, lane, xs);
+        }
         if (k + 2 < sg.n) chain_out_load_q(p, sg, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
         v4 D[4];
@@ -1211,14 +1208,13 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     }
 }
 
-// Feed role (wave 5). In alpha_{k-1} it starts copying chunk c_{k+1}'s key planes (written by
-// the chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads,
-// and waits for them at the end of alpha_k. In beta_k it writes chunk c_{k+1}'s decay factors
-// (E, then Gam) and T' (its 6 nonzero fragments) into the value slot, then loads chunk
-// c_{k+2}'s. It also writes the new rolling conv history of the workgroup's channels: before
+// Feed role (wave 5). In alpha_k it starts copying chunk c_{k+1}'s key planes (written by the
+// chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads and
+// loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and T''s 6
+// nonzero fragments) into the value slot and waits for the copies before the barrier. It also writes the new rolling conv history of the workgroup's channels: before
 // alpha_0 its share of the sequence's q/k channels (the h_v * 8 workgroups of a sequence split
 // them into contiguous ranges; the chunk kernel has read their old history), in alpha_0 the
-// strip's 16 v channels (whose old history the D wave read before alpha_0). Nothing else in
+// strip's 16 v channels (whose old history the output waves read before alpha_0). Nothing else in
 // this kernel writes conv_state.
 __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
                                                 int h, int strip, int src) {
@@ -1237,7 +1233,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         }
     };
     auto produce = [&]() {
-        if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + lane * 16) = eg;
+        if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + 4 * kPlane + lane * 16) = eg;
         lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
 #pragma unroll
         for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
@@ -1248,10 +1244,9 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
 #pragma unroll
         for (int i = 0; i < kKSlot / kPlane; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, d + i * kPlane, 16, 0, 0);
     };
-    // s_waitcnt immediates (gfx9 layout: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8):
-    // lgkmcnt(0) alone; vmcnt(34) with lgkmcnt(0).
+    // s_waitcnt lgkmcnt(0) alone (gfx9 layout: vmcnt bits 3:0 and 15:14 and expcnt 6:4 at their
+    // maxima, lgkmcnt 11:8 zero).
     constexpr int kWaitLgkm0 = 0xc07f;
-    constexpr int kWaitVm34Lgkm0 = 0x8072;
     auto wait_barrier = [&]() {
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(0);                      // the copies have landed
@@ -1265,39 +1260,24 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
     }
     copy_keys(0);
-    if (sg.n > 1) copy_keys(1);
     load(0);
     produce();
-    __builtin_amdgcn_sched_barrier(0);
-    load(1);
     wait_barrier();                                         // alpha_0
     if (lane < kStrip) commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
     for (int k = 0; k < sg.n; ++k) {
-        // Chunk c_{k+2}'s keys go to the slot of chunk c_{k-1}, whose K^T the state waves read in
-        // beta_{k-1}; they land by the end of alpha_{k+1}. Waiting here for all but the 34 copies
-        // just issued leaves chunk c_{k+1}'s keys (issued in alpha_{k-1}), its value operands
-        // (loaded in beta_{k-1}) and the history writes of alpha_0 complete: a wave's vector
-        // memory operations complete in issue order.
-        __asm__ volatile("" ::: "memory");
-        if (k + 2 < sg.n) {
-            copy_keys(k + 2);
-            static_assert(kKSlot / kPlane == 34, "the wait below counts 34 copies");
-            __builtin_amdgcn_s_waitcnt(kWaitVm34Lgkm0);
-        } else {
-            __builtin_amdgcn_s_waitcnt(0);
-        }
-        __builtin_amdgcn_s_barrier();                       // beta_k
-        __asm__ volatile("" ::: "memory");
+        // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
+        // in alpha_{k-1}; they are read from alpha_{k+1} on.
         if (k + 1 < sg.n) {
-            produce();
-            __builtin_amdgcn_sched_barrier(0);
-            load(k + 2);
+            copy_keys(k + 1);
+            load(k + 1);
         }
-        // alpha_{k+1}: the slot writes have completed; the loads stay in flight.
+        // beta_k: nothing this wave wrote to LDS is pending; the copies and loads stay in flight.
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
+        if (k + 1 < sg.n) produce();                        // waits for the loads, and so the copies
+        wait_barrier();                                     // alpha_{k+1}: the copies have landed
     }
 }
 
@@ -1335,11 +1315,11 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
     } else if (w == 4) {
-        chain_d_role<DC, SILU>(p, lds, lane, sg, h, strip);
+        chain_d_role(lds, lane, sg.n);
     } else if (w == 5) {
         chain_feed_role(p, lds, lane, sg, h, strip, src);
     } else {
-        chain_output_role(p, lds, lane, w < 4 ? w - 2 : w - 4, sg, h, src, j0);
+        chain_output_role<DC, SILU>(p, lds, lane, w < 4 ? w - 2 : w - 4, sg, h, src, strip);
     }
 }
 
