@@ -32,6 +32,7 @@ EXPORTS = (
     "ix_gdn_step", "ix_gdn_conv_step", "ix_gdn_l2_norm", "ix_gdn_beta_gate", "ix_gdn_out_norm",
     "ix_gdn_channels", "ix_gdn_decode_workspace_size", "ix_gdn_decode", "ix_gdn_prefill_workspace_size",
     "ix_gdn_prefill", "ix_gdn_decode_gated", "ix_gdn_prefill_gated_workspace_size", "ix_gdn_prefill_gated",
+    "ix_gdn_prefill_window_workspace_size",
     "ix_gdn_window_record_size", "ix_gdn_decode_window", "ix_gdn_decode_window_mfma", "ix_gdn_commit_window",
     "ix_bf16_gemv", "ix_bf16_gemv_pair", "ix_bf16_gemv_split", "ix_mmvq_q8_0", "ix_gdn_in_proj_width", "ix_gdn_in_proj",
     "ix_gdn_version", "ix_gdn_decode_noalloc", "ix_q8_1_quantize", "ix_gdn_commit_window_layers",
@@ -99,6 +100,7 @@ def lib() -> ctypes.CDLL:
         "ix_gdn_prefill": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
         "ix_gdn_decode_gated": ([P, I, P, P, P, P, P, P, P, P, P, P, P, P, P], I),
         "ix_gdn_prefill_gated_workspace_size": ([P, I, I], Z),
+        "ix_gdn_prefill_window_workspace_size": ([P, I, I, I, I], Z),
         "ix_gdn_prefill_gated": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P, P, Z, P], I),
         "ix_gdn_window_record_size": ([P, I, I], Z),
         "ix_gdn_decode_window": ([P, I, I, P, P, P, P, P, P, P, P, P, P, P, P], I),
@@ -225,6 +227,13 @@ def ix_gdn_decode_gated(cfg: Cfg, B, x, conv_state, conv_w, a, b, A_log, dt_bias
 
 def ix_gdn_prefill_gated_workspace_size(cfg: Cfg, n_seq: int, total_T: int) -> int:
     return lib().ix_gdn_prefill_gated_workspace_size(ctypes.byref(cfg), n_seq, total_T)
+
+
+def ix_gdn_prefill_window_workspace_size(cfg: Cfg, n_seq: int, total_T: int, window_chunks: int,
+                                         gated: bool = False) -> int:
+    """Workspace bytes for the (gated) prefill run in windows of window_chunks 64-token chunks."""
+    return lib().ix_gdn_prefill_window_workspace_size(ctypes.byref(cfg), n_seq, total_T, window_chunks,
+                                                      1 if gated else 0)
 
 
 def ix_gdn_prefill_gated(cfg: Cfg, n_seq, total_T, cu_seqlens, x, conv_state, conv_w, a, b, A_log, dt_bias, state,

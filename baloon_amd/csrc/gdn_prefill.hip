@@ -50,16 +50,18 @@ constexpr int kPlanThreads = 1024;
 // ---------------------------------------------------------------------------------------
 // Workspace layout (host and device agree through this struct)
 // ---------------------------------------------------------------------------------------
+// The chunk tables cover every chunk; the chunk operands cover one window of W chunks (the
+// kernels run window by window, W chosen to fit the caller's workspace).
 struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
-    uint16_t* Tf;        // [NC][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
-    uint16_t* Mf;        // [NC][h_v] M (64 x 64) as split-bf16 A fragments
-    float* G;            // [NC][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
+    uint16_t* Tf;        // [W][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
+    uint16_t* Mf;        // [W][h_v] M (64 x 64) as split-bf16 A fragments
+    float* G;            // [W][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
                          // inclusive cumulative log decay G (padded rows repeat the last)
-    uint8_t* Kp;         // [NC][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
-    uint16_t* Qf;        // [NC][h_k] Q (64 x 128) as split-bf16 A fragments
+    uint8_t* Kp;         // [W][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
+    uint16_t* Qf;        // [W][h_k] Q (64 x 128) as split-bf16 A fragments
 };
 constexpr int kWsSections = 8;
 constexpr int kPRow = 2 * 128 + 16;                     // key plane row: 128 bf16, 16 bytes of padding
@@ -68,13 +70,18 @@ constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 34,816 b
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Byte offsets of every workspace section for (n_seq, T); returns the total size.
-inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t off[kWsSections]) {
-    const size_t NC = (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq;
+// Chunks of (n_seq, T) at most: each sequence adds at most one partial chunk.
+inline size_t max_chunks(int n_seq, int T) { return (size_t)(T + kChunk - 1) / kChunk + (size_t)n_seq; }
+
+// Byte offsets of every workspace section for (n_seq, T) in windows of W chunks; returns the
+// total size.
+inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t W, size_t off[kWsSections]) {
+    const size_t NC = max_chunks(n_seq, T);
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
-        sizeof(float) * NC * c->h_v * kChunk * kChunk, sizeof(float) * NC * c->h_v * kChunk * kChunk,
-        sizeof(float) * NC * c->h_v * 2 * kChunk, (size_t)kKSlot * NC * c->h_k, sizeof(uint16_t) * NC * c->h_k * 4 * 4 * 2 * 512,
+        sizeof(float) * W * c->h_v * kChunk * kChunk, sizeof(float) * W * c->h_v * kChunk * kChunk,
+        sizeof(float) * W * c->h_v * 2 * kChunk, (size_t)kKSlot * W * c->h_k,
+        sizeof(uint16_t) * W * c->h_k * 4 * 4 * 2 * 512,
     };
     size_t pos = 0;
     for (int i = 0; i < kWsSections; ++i) { off[i] = pos; pos += align256(sz[i]); }
@@ -103,10 +110,12 @@ struct PrefillParams {
     const uint16_t* a;          // [T][h_v]
     const uint16_t* b;          // [T][h_v]
     float* state;               // [n_seq][h_v][d_v][d_k]
-    float* o;                   // [T][h_v][128] or null
+    float* o;                   // [T][h_v][128], the window's rows (o_win), or null
     uint16_t* o_bf16;           // [T][h_v][128] or null
     int n_seq, T, NC;
     int single;                 // n_seq == 1: no plan pass; the geometry comes from cu[0], cu[1]
+    int cb, W;                  // the window: chunks cb .. cb + W - 1
+    int o_win;                  // o holds the window's tokens only (row 0 = its first token)
 };
 
 // Clamped bounds [lo, hi) of sequence s: the plan's seq_lo (running maximum of the offsets,
@@ -217,6 +226,25 @@ __device__ __forceinline__ bool chunk_geo(const PrefillParams& p, int c, ChunkGe
     g.len = min(kChunk, r.w - g.t0);
     g.pos0 = g.t0 - g.lo;
     return true;
+}
+
+// Tokens [t0, t1) of the window's chunks (consecutive chunks cover consecutive tokens); t0 = t1
+// for a window past the last chunk.
+__device__ __forceinline__ void window_tokens(const PrefillParams& p, int& t0, int& t1) {
+    ChunkGeo a, b;
+    t0 = t1 = 0;
+    if (!chunk_geo(p, p.cb, a)) return;
+    int nc;
+    if (p.single) {
+        int lo, hi;
+        seq_bounds(p, 0, lo, hi);
+        nc = (hi - lo + kChunk - 1) / kChunk;
+    } else {
+        nc = p.ws.chunk_off[p.n_seq];
+    }
+    chunk_geo(p, min(p.cb + p.W, nc) - 1, b);               // chunk cb exists, so this one does
+    t0 = a.t0;
+    t1 = b.t0 + b.len;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -569,7 +597,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
     uint8_t* Qp = lds + 2 * kQKPlane;
 
     ChunkGeo g;
-    const int c = blockIdx.x;
+    const int c = p.cb + blockIdx.x, lc = blockIdx.x;       // chunk, and its place in the window
     if (!chunk_geo(p, c, g)) return;
     const Layer& L = p.L;
     const int src = blockIdx.y;
@@ -624,7 +652,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
     // fragment chunks. Key chunk j of a row holds channels 32 (j / 4) + 4 (j % 4) .. +3, then
     // the 4 channels 16 later.
     {
-        uint8_t* kg = p.ws.Kp + ((size_t)c * L.h_k + src) * kKSlot;
+        uint8_t* kg = p.ws.Kp + ((size_t)lc * L.h_k + src) * kKSlot;
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int e = tid + u * kChunkThreads, pl = e >> 10, t = (e >> 4) & 63, cc = e & 15;
@@ -633,7 +661,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
             const uint2 b = *reinterpret_cast<const uint2*>(Kp + pl * kQKPlane + qk_off(t, c0 + 16));
             *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * cc) = u4x{a.x, a.y, b.x, b.y};
         }
-        uint16_t* Qg = p.ws.Qf + ((size_t)c * L.h_k + src) * kFragW;
+        uint16_t* Qg = p.ws.Qf + ((size_t)lc * L.h_k + src) * kFragW;
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int e = tid + u * kChunkThreads, ln = e & (kWave - 1), f = e / kWave, m = f >> 2, ks = f & 3;
@@ -681,7 +709,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
     }
     if (gw == 0 && grp < nmap) {
         const int h = mapped_head(L, src, grp);
-        decay_scan(p, g, h, (size_t)c * L.h_v + h, ra, rb, G_s[grp], B_s[grp], lane);
+        decay_scan(p, g, h, (size_t)lc * L.h_v + h, ra, rb, G_s[grp], B_s[grp], lane);
     }
     lds_barrier();                                          // the planes' space becomes A/T
 
@@ -691,7 +719,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
         const int m = 2 * it + grp;
         const bool live = m < nmap;
         const int h = mapped_head(L, src, min(m, nmap - 1));
-        const size_t ch = (size_t)c * L.h_v + h;
+        const size_t ch = (size_t)lc * L.h_v + h;
         if (it > 0) {                                       // the next head's decay scan
             if (live && gw == 0) {
                 const size_t ab = (size_t)(g.t0 + min(lane, g.len - 1)) * L.h_v + h;
@@ -885,16 +913,17 @@ __device__ __forceinline__ void mfma2_split(const bf8 (&a)[4][2], const bf8& bh,
 }
 
 
-// A workgroup's sequence: chunk k (0-based) of its n chunks starts at token lo + 64 k; its
-// operands sit at workspace chunk c0 + k.
-struct SeqGeo { int s, lo, hi, n, c0; };
+// A workgroup's share of its sequence in the window: n chunks, the first being chunk k0 of the
+// sequence (tokens lo + 64 k0 on); chunk k (0-based) of the n has its operands at window slot
+// wk + k. last: the window holds the sequence's last chunk.
+struct SeqGeo { int s, lo, hi, n, k0, wk, last; };
 __device__ __forceinline__ ChunkGeo seq_chunk(const SeqGeo& sg, int k) {
     ChunkGeo g;
     g.s = sg.s;
     g.lo = sg.lo;
-    g.t0 = sg.lo + k * kChunk;
+    g.pos0 = (sg.k0 + k) * kChunk;
+    g.t0 = sg.lo + g.pos0;
     g.len = min(kChunk, sg.hi - g.t0);
-    g.pos0 = k * kChunk;
     return g;
 }
 
@@ -980,7 +1009,7 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo&
                                            int lane, XStage& xs) {
     const Layer& L = p.L;
     const int ch = v_channel(L, h, strip * kStrip + 2 * (lane & 7));
-    const int pos0 = k * kChunk + 16 * r - 3, last = sg.hi - sg.lo - 1;
+    const int pos0 = (sg.k0 + k) * kChunk + 16 * r - 3, last = sg.hi - sg.lo - 1;
     const uint16_t* hist = p.conv_state + ((size_t)sg.s * L.C + ch) * (DC - 1) + (DC - 1);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
@@ -1103,7 +1132,7 @@ struct OutM {
 };
 __device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const SeqGeo& sg, int k, int h, int src,
                                                  int r, int lane, OutQ& x) {
-    const size_t c = (size_t)(sg.c0 + min(k, sg.n - 1));
+    const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
     const uint16_t* Qf = p.ws.Qf + (c * p.L.h_k + src) * kFragW;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -1113,7 +1142,7 @@ __device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const S
 }
 __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const SeqGeo& sg, int k, int h, int r,
                                                  int lane, OutM& x) {
-    const size_t c = (size_t)(sg.c0 + min(k, sg.n - 1));
+    const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
     const uint16_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragM;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -1145,16 +1174,19 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     const lds_u8* hbase = lane_at(lds, kOffH + lane * 16);
     const size_t row = (size_t)L.h_v * kD;
     v4 o;
+    // A window buffer for o starts at the window's first token.
+    int tw0 = 0, tw1;
+    if (p.o_win) window_tokens(p, tw0, tw1);
     auto store = [&](int k) {
         const ChunkGeo g = seq_chunk(sg, k);
         const size_t ob = ((size_t)g.t0 * L.h_v + h) * kD + j0 + li;
+        const size_t obw = ((size_t)(g.t0 - tw0) * L.h_v + h) * kD + j0 + li;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * r + 4 * lg4 + i;
             if (t < g.len) {
-                const size_t oo = ob + (size_t)t * row;
-                if (p.o) p.o[oo] = o[i];
-                if (p.o_bf16) p.o_bf16[oo] = f32_to_bf16(o[i]);
+                if (p.o) p.o[obw + (size_t)t * row] = o[i];
+                if (p.o_bf16) p.o_bf16[ob + (size_t)t * row] = f32_to_bf16(o[i]);
             }
         }
     };
@@ -1223,7 +1255,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     v4 eg;
     u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
     auto load = [&](int k) {
-        const size_t chh = (size_t)(sg.c0 + min(k, sg.n - 1)) * L.h_v + h;
+        const size_t chh = (size_t)(sg.wk + min(k, sg.n - 1)) * L.h_v + h;
         eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
         const u4x* tsrc = reinterpret_cast<const u4x*>(p.ws.Tf + chh * kFragM) + lane;
 #pragma unroll
@@ -1239,7 +1271,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
     };
     auto copy_keys = [&](int k) {
-        const uint8_t* g = p.ws.Kp + ((size_t)(sg.c0 + k) * L.h_k + src) * kKSlot + lane * 16;
+        const uint8_t* g = p.ws.Kp + ((size_t)(sg.wk + k) * L.h_k + src) * kKSlot + lane * 16;
         lds_u8* d = (lds_u8*)lds + kOffK + (k % kKSlots) * kKSlot;
 #pragma unroll
         for (int i = 0; i < kKSlot / kPlane; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, d + i * kPlane, 16, 0, 0);
@@ -1257,13 +1289,15 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     {
         const int G = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + G - 1) / G;
         const int ch_hi = min(cqk, (gi + 1) * per);
-        for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
+        if (sg.last)
+            for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
     }
     copy_keys(0);
     load(0);
     produce();
     wait_barrier();                                         // alpha_0
-    if (lane < kStrip) commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
+    if (sg.last && lane < kStrip)
+        commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
     for (int k = 0; k < sg.n; ++k) {
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
         // in alpha_{k-1}; they are read from alpha_{k+1} on.
@@ -1296,10 +1330,15 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     SeqGeo sg;
     sg.s = s;
     seq_bounds(p, s, sg.lo, sg.hi);
-    sg.c0 = p.single ? 0 : p.ws.chunk_off[s];
+    // the sequence's chunks c0 .. c_end - 1, clipped to the window
+    const int c0 = p.single ? 0 : p.ws.chunk_off[s];
     const int c_end = p.single ? (sg.hi - sg.lo + kChunk - 1) / kChunk : p.ws.chunk_off[s + 1];
-    sg.n = c_end - sg.c0;
+    const int lo_c = max(c0, p.cb), hi_c = min(c_end, p.cb + p.W);
+    sg.n = hi_c - lo_c;
     if (sg.n <= 0) return;
+    sg.k0 = lo_c - c0;
+    sg.wk = lo_c - p.cb;
+    sg.last = hi_c == c_end;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
     const int j0 = strip * kStrip;
@@ -1335,6 +1374,18 @@ __global__ void __launch_bounds__(256) out_gate_kernel(const float* __restrict__
     out_gate_head(g, row, o[row + lane], o[row + lane + kWave], lane);
 }
 
+// The same norm over one window's rows, for the gated prefill without a caller o: the chain
+// wrote the window's fp32 outputs to p.o, row 0 being the window's first token.
+__global__ void __launch_bounds__(256) out_gate_window_kernel(const PrefillParams p, const OutGate g) {
+    int t0, t1;
+    window_tokens(p, t0, t1);
+    const long long r = (long long)blockIdx.x * 4 + threadIdx.x / kWave;       // row in the window
+    if (r >= (long long)(t1 - t0) * p.L.h_v) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const size_t row = (size_t)r * kD;
+    out_gate_head(g, (size_t)t0 * p.L.h_v * kD + row, p.o[row + lane], p.o[row + lane + kWave], lane);
+}
+
 }  // namespace
 }  // namespace ixg
 
@@ -1342,21 +1393,34 @@ extern "C" hipError_t ix_gdn_check_cfg_(const ix_gdn_cfg* c);
 
 extern "C" hipError_t ix_gdn_check_gate_(const ix_gdn_out_gate* g);
 
+// Workspace bytes for windows of W chunks; with gwin, plus the window's fp32 outputs (the gated
+// prefill's norm input when the caller passes no o).
+static size_t prefill_ws_bytes(const ix_gdn_cfg* cfg, int n_seq, int T, size_t W, bool gwin) {
+    size_t off[ixg::kWsSections];
+    size_t b = ixg::ws_layout(cfg, n_seq, T, W, off);
+    if (gwin) b += ixg::align256(W * ixg::kChunk * cfg->h_v * ixg::kD * sizeof(float));
+    return b;
+}
+
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    size_t off[ixg::kWsSections];
-    return ixg::ws_layout(cfg, n_seq, total_T, off);
+    return prefill_ws_bytes(cfg, n_seq, total_T, ixg::max_chunks(n_seq, total_T), false);
 }
 
-// The gated prefill's workspace: the prefill's, then [total_T][h_v][d_v] fp32 outputs.
 extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
-    const size_t base = ix_gdn_prefill_workspace_size(cfg, n_seq, total_T);
-    if (!base) return 0;
-    return base + (((size_t)total_T * cfg->h_v * ixg::kD * sizeof(float) + 255) & ~(size_t)255);
+    if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
+    return prefill_ws_bytes(cfg, n_seq, total_T, ixg::max_chunks(n_seq, total_T), true);
 }
 
-// The chunk kernel, then the chain. The conv activation is a template parameter of the chunk
-// kernel: inlined into every unrolled conv output, a runtime choice would carry the
+extern "C" size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T,
+                                                       int window_chunks, int gated) {
+    if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0 || window_chunks < 1) return 0;
+    const size_t W = std::min((size_t)window_chunks, ixg::max_chunks(n_seq, total_T));
+    return prefill_ws_bytes(cfg, n_seq, total_T, W, gated != 0);
+}
+
+// One window: the chunk kernel, then the chain. The conv activation and width are template
+// parameters: inlined into every unrolled conv output, a runtime choice would carry the
 // activation's code in the kernels that do not use it.
 template <int DC>
 static void launch_prefill(const ixg::PrefillParams& p, dim3 tgrid, dim3 cgrid, dim3 cblock, bool silu,
@@ -1386,11 +1450,19 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (!x || !a || !b || !workspace) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(workspace) & 255) return hipErrorInvalidValue;
     if (reinterpret_cast<uintptr_t>(state) & 15) return hipErrorInvalidValue;      // float4 state accesses
+    // The window: as many chunks as the workspace holds (all of them with the full size).
+    const bool gwin = gate && !o;
+    const size_t NCmax = max_chunks(n_seq, total_T);
+    if (workspace_bytes < prefill_ws_bytes(cfg, n_seq, total_T, 1, gwin)) return hipErrorInvalidValue;
+    size_t W = 1, W_hi = NCmax;
+    while (W < W_hi) {
+        const size_t mid = (W + W_hi + 1) / 2;
+        if (prefill_ws_bytes(cfg, n_seq, total_T, mid, gwin) <= workspace_bytes) W = mid;
+        else W_hi = mid - 1;
+    }
     size_t off[kWsSections];
-    const size_t need = ws_layout(cfg, n_seq, total_T, off);
-    if (workspace_bytes < (gate ? ix_gdn_prefill_gated_workspace_size(cfg, n_seq, total_T) : need))
-        return hipErrorInvalidValue;
-    const long long NC = (total_T + kChunk - 1) / kChunk + (long long)n_seq;
+    const size_t need = ws_layout(cfg, n_seq, total_T, W, off);
+    const long long NC = (long long)NCmax;
     const long long pairs = (long long)n_seq * cfg->h_v;
     if (NC * cfg->h_v > 0x7fffffffLL || ((pairs + 7) / 8) * 8 * kStrips > 0x7fffffffLL) return hipErrorInvalidValue;
     const long long rows = (long long)total_T * cfg->h_v;
@@ -1403,21 +1475,31 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     p.state = state; p.o = o; p.o_bf16 = o_bf16;
     p.n_seq = n_seq; p.T = total_T; p.NC = (int)NC;
     p.single = n_seq == 1;
-    if (gate && !o) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
+    p.o_win = gwin;
+    if (gwin) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const dim3 tgrid((unsigned)NC, (unsigned)cfg->h_k);
     const long long groups = (pairs + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
     const bool silu = cfg->conv_act == IX_GDN_ACT_SILU;
-    switch (cfg->d_conv) {
-        case 2: launch_prefill<2>(p, tgrid, cgrid, cblock, silu, s); break;
-        case 3: launch_prefill<3>(p, tgrid, cgrid, cblock, silu, s); break;
-        default: launch_prefill<4>(p, tgrid, cgrid, cblock, silu, s); break;
+    const OutGate og = make_out_gate(gate);
+    // Windows run in stream order: each chain resumes from the state and conv history the
+    // previous one left; a window past the last chunk finds nothing to do.
+    for (size_t cb = 0; cb < NCmax; cb += W) {
+        p.cb = (int)cb;
+        p.W = (int)std::min(W, NCmax - cb);
+        const dim3 tgrid((unsigned)p.W, (unsigned)cfg->h_k);
+        switch (cfg->d_conv) {
+            case 2: launch_prefill<2>(p, tgrid, cgrid, cblock, silu, s); break;
+            case 3: launch_prefill<3>(p, tgrid, cgrid, cblock, silu, s); break;
+            default: launch_prefill<4>(p, tgrid, cgrid, cblock, silu, s); break;
+        }
+        if (gwin)
+            hipLaunchKernelGGL(out_gate_window_kernel, dim3((unsigned)(((long long)p.W * kChunk * cfg->h_v + 3) / 4)),
+                               dim3(256), 0, s, p, og);
     }
-    if (gate)
-        hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o,
-                           make_out_gate(gate), rows);
+    if (gate && !gwin)
+        hipLaunchKernelGGL(out_gate_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, p.o, og, rows);
     return hipGetLastError();
 }
 

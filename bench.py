@@ -635,12 +635,35 @@ def prefill_leg(O, T=4096, iters=10):
     sec = timed(stream, lambda i: run(warm + i), iters) / iters
     tflops = PREFILL_FLOP_PER_TOKEN * T / sec / 1e12
     check = O.gate_prefill(D, T, to_host(css[-1]), state_host(sts[-1]), to_host(o))
-    del ws
+    # The same call with a workspace of 16-chunk windows (1024 tokens): bounded memory, same
+    # results bit for bit.
+    wchunks = 16
+    wneed = bx.ix_gdn_prefill_window_workspace_size(cfg, 1, T, wchunks)
+    wws = torch.empty(wneed, dtype=torch.uint8, device="cuda")
+    full_st, full_cs = sts[-1].clone(), css[-1].clone()
+    for st_, cs_ in zip(sts, css):
+        st_.zero_()
+        cs_.zero_()
+    ow = torch.empty_like(o)
+
+    def run_w(i):
+        return bx.ix_gdn_prefill(cfg, 1, T, cu, x, css[i], w, a, b, A_log, dt, sts[i], None, ow, wws, wneed, stream)
+
+    for i in range(warm):
+        bx.check("ix_gdn_prefill", run_w(i))
+    wsec = timed(stream, lambda i: run_w(warm + i), iters) / iters
+    same = bool(torch.equal(ow, o)) and bool(torch.equal(sts[-1], full_st)) and bool(torch.equal(css[-1], full_cs))
+    if not same:
+        raise SystemExit("prefill: the windowed run differs from the one-window run")
+    del ws, wws
     torch.cuda.empty_cache()
     return dict(T=T, tokens_per_s=round(T / sec, 1), us_per_call=round(sec * 1e6, 1),
                 mfma=dict(bound="mfma", achieved=round(tflops, 2), peak=MFMA_BF16_PEAK_TFLOPS, unit="TFLOP/s",
                           frac=round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)),
-                workspace_mib=round(need / 2 ** 20, 1), check=check)
+                workspace_mib=round(need / 2 ** 20, 1),
+                windowed=dict(window_tokens=wchunks * 64, us_per_call=round(wsec * 1e6, 1),
+                              workspace_mib=round(wneed / 2 ** 20, 1), bit_identical=same),
+                check=check)
 
 
 def prefill_varlen_leg(O, iters=5):

@@ -160,8 +160,18 @@ hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, 
                                uint16_t* o_bf16, const ix_gdn_out_gate* gate, void* workspace,
                                hipStream_t s IX_GDN_DEFAULT_STREAM);
 
-/* Bytes of device workspace ix_gdn_prefill needs for n_seq sequences and total_T tokens. */
+/* Bytes of device workspace for ix_gdn_prefill over n_seq sequences and total_T tokens in one
+ * window (the fastest; about 2 MiB per 64-token chunk at the Qwen3-Next head layout). */
 size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
+
+/* Bytes of device workspace for ix_gdn_prefill (gated = 0) or ix_gdn_prefill_gated (gated = 1)
+ * in windows of window_chunks 64-token chunks: the chunk tables (16 bytes per chunk) plus the
+ * chunk operands of one window. Any workspace of at least the size for window_chunks = 1 works;
+ * the prefill then runs in windows of as many chunks as the workspace holds, one after the
+ * other, with results identical to the one-window run. 0 for invalid arguments. Addition; no
+ * reference counterpart (for callers that bound device memory independently of total_T). */
+size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T, int window_chunks,
+                                            int gated);
 
 /* Chunked (WY-form, chunk 64) prefill of n_seq packed sequences, the same math as
  * total_T applications of ix_gdn_decode:
@@ -170,7 +180,9 @@ size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total
  *   conv_state [n_seq][C][d_conv-1] bf16 in/out; state [n_seq][h_v][d_v][d_k] fp32 in/out
  *   (16-byte aligned)
  *   o [total_T][h_v][d_v] fp32 or NULL; o_bf16 likewise
- *   workspace: device memory of ix_gdn_prefill_workspace_size() bytes, 256-byte aligned. */
+ *   workspace: 256-byte aligned device memory of at least
+ *   ix_gdn_prefill_window_workspace_size(cfg, n_seq, total_T, 1, 0) bytes (windows of one
+ *   chunk); ix_gdn_prefill_workspace_size() bytes run the whole batch as one window. */
 hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
                           const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
                           const uint16_t* b, const float* A_log, const float* dt_bias, float* state, float* o,
@@ -183,7 +195,8 @@ size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int
 
 /* ix_gdn_prefill followed by the gated output norm of every (token, v head) row:
  * gate->z, gate->y, gate->y_bf16 are [total_T][h_v][d_v]; workspace_bytes must be at least
- * ix_gdn_prefill_gated_workspace_size(). */
+ * ix_gdn_prefill_window_workspace_size(cfg, n_seq, total_T, 1, 1) (one window:
+ * ix_gdn_prefill_gated_workspace_size()). */
 hipError_t ix_gdn_prefill_gated(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
                                 const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
                                 const uint16_t* a, const uint16_t* b, const float* A_log, const float* dt_bias,

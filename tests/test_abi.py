@@ -124,12 +124,20 @@ def test_prefill_validation_without_launch():
     assert bx.ix_gdn_prefill_workspace_size(cfg, 2, -1) == 0
     assert bx.ix_gdn_prefill_workspace_size(bx.make_cfg(d_k=64), 2, 100) == 0
     assert bx.ix_gdn_prefill_workspace_size(cfg, 2, 200) > need       # grows with tokens
+    small = bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 1)   # windows of one chunk
+    assert 0 < small < need and small % 256 == 0
+    assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 10 ** 6) == need
+    assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 0) == 0
+    assert bx.ix_gdn_prefill_window_workspace_size(cfg, 0, 100, 1) == 0
+    assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 1, gated=True) > small
+    # the window operands do not grow with tokens; only the chunk tables do (16 bytes a chunk)
+    assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 64 * 1000, 1) - small <= 1000 * 16 + 512
     p = ctypes.c_void_p(1 << 20)
 
     def call(n_seq, T, ws, nbytes, c=cfg):
         return L.ix_gdn_prefill(ctypes.byref(c), n_seq, T, p, p, p, p, p, p, p, p, p, NULL, NULL, ws, nbytes, NULL)
 
-    assert call(2, 100, p, need - 1) == INVALID                      # workspace too small
+    assert call(2, 100, p, small - 1) == INVALID                     # below one chunk's window
     assert call(2, 100, ctypes.c_void_p((1 << 20) + 64), need) == INVALID   # not 256-byte aligned
     assert call(2, 100, NULL, need) == INVALID                       # no workspace
     assert call(0, 100, p, need) == INVALID
@@ -178,7 +186,8 @@ def test_gated_validation_without_launch():
                                       nbytes, NULL)
 
     assert pre(None, gneed) == INVALID
-    assert pre(ok, gneed - 1) == INVALID                   # needs room for the norm's fp32 input
+    gsmall = bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 1, gated=True)
+    assert pre(ok, gsmall - 1) == INVALID                  # needs room for one window's fp32 norm input
     assert pre(bx.OutGate(1 << 20, 1 << 20, 1e-6, None, None), gneed) == INVALID
 
 

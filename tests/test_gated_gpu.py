@@ -154,3 +154,21 @@ def test_prefill_gated_matches_out_norm():
     _, _, ro = oracle.prefill(cfg, cu, tok["x"], st["conv_state"], p["w"], tok["a"], tok["b"], p["A_log"],
                               p["dt_bias"], st["state"], nthreads=NT)
     assert oracle.rel_err(y, oracle.gated_out(ro, g["z"], g["nrm"], EPS)) <= TOL_Y_E2E
+    # Without o, a workspace of a few chunks' windows (the norm's fp32 input held one window at
+    # a time) gives the same y and states bit for bit.
+    for window in (1, 2):
+        wneed = bx.ix_gdn_prefill_window_workspace_size(cfg, n, T, window, gated=True)
+        assert 0 < wneed < need
+        wws = torch.empty(wneed, dtype=torch.uint8, device="cuda")
+        d_cs, d_st = dev(st["conv_state"]), state_to_dev(st["state"])
+        y_w = torch.full((T, cfg.h_v, cfg.d_v), float("nan"), dtype=torch.float32, device="cuda")
+        yb_w = torch.zeros(T, cfg.h_v, cfg.d_v, dtype=torch.bfloat16, device="cuda")
+        rc = bx.ix_gdn_prefill_gated(cfg, n, T, d_cu, dev(tok["x"]), d_cs, d_w, dev(tok["a"]), dev(tok["b"]), d_A,
+                                     d_dt, d_st, o=None, gate=bx.out_gate(d_z, d_n, EPS, y_w, yb_w), workspace=wws,
+                                     workspace_bytes=wneed)
+        assert rc == 0
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(y_w), y_no, err_msg=f"window {window}")
+        np.testing.assert_array_equal(host(yb_w), yb_no)
+        np.testing.assert_array_equal(host(d_st), s_no)
+        np.testing.assert_array_equal(host(d_cs), cs_no)
