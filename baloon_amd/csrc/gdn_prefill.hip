@@ -1242,12 +1242,13 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 
 // Feed role (wave 5). In alpha_k it starts copying chunk c_{k+1}'s key planes (written by the
 // chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads and
-// loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and T''s 6
-// nonzero fragments) into the value slot and waits for the copies before the barrier. It also writes the new rolling conv history of the workgroup's channels: before
-// alpha_0 its share of the sequence's q/k channels (the h_v * 8 workgroups of a sequence split
-// them into contiguous ranges; the chunk kernel has read their old history), in alpha_0 the
-// strip's 16 v channels (whose old history the output waves read before alpha_0). Nothing else in
-// this kernel writes conv_state.
+// loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and the 6
+// nonzero fragments of T') into the value slot and waits for the copies before the barrier.
+// In the window that holds the sequence's last chunk it also writes the new rolling conv
+// history of the workgroup's channels: before alpha_0 its share of the sequence's q/k channels
+// (the h_v * 8 workgroups of a sequence split them into contiguous ranges; the chunk kernel has
+// read their old history), in alpha_0 the strip's 16 v channels (whose old history the output
+// waves read before the first window's alpha_0). Nothing else in this kernel writes conv_state.
 __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
                                                 int h, int strip, int src) {
     typedef __attribute__((address_space(3))) u4x lds_u4;
