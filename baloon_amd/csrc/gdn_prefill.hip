@@ -56,6 +56,8 @@ struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
+    int32_t* seq_rank;   // [n_seq + 1] non-empty sequences before s (seq_rank[n_seq] = all of them)
+    int32_t* seq_list;   // [n_seq] the non-empty sequences in order
     uint16_t* Tf;        // [W][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
     uint16_t* Mf;        // [W][h_v] M (64 x 64) as split-bf16 A fragments
     float* G;            // [W][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
@@ -63,7 +65,7 @@ struct Ws {
     uint8_t* Kp;         // [W][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
     uint16_t* Qf;        // [W][h_k] Q (64 x 128) as split-bf16 A fragments
 };
-constexpr int kWsSections = 8;
+constexpr int kWsSections = 10;
 constexpr int kPRow = 2 * 128 + 16;                     // key plane row: 128 bf16, 16 bytes of padding
 constexpr int kKPlane = 64 * kPRow;                     // one plane (hi or lo) of 64 keys
 constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 34,816 bytes
@@ -79,7 +81,7 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t W, size_t 
     const size_t NC = max_chunks(n_seq, T);
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
-        sizeof(float) * W * c->h_v * kChunk * kChunk, sizeof(float) * W * c->h_v * kChunk * kChunk,
+        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * n_seq, sizeof(float) * W * c->h_v * kChunk * kChunk, sizeof(float) * W * c->h_v * kChunk * kChunk,
         sizeof(float) * W * c->h_v * 2 * kChunk, (size_t)kKSlot * W * c->h_k,
         sizeof(uint16_t) * W * c->h_k * 4 * 4 * 2 * 512,
     };
@@ -93,11 +95,13 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.seq_lo = reinterpret_cast<int32_t*>(base + off[0]);
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
     w.chunk_rec = reinterpret_cast<int4*>(base + off[2]);
-    w.Tf = reinterpret_cast<uint16_t*>(base + off[3]);
-    w.Mf = reinterpret_cast<uint16_t*>(base + off[4]);
-    w.G = reinterpret_cast<float*>(base + off[5]);
-    w.Kp = reinterpret_cast<uint8_t*>(base + off[6]);
-    w.Qf = reinterpret_cast<uint16_t*>(base + off[7]);
+    w.seq_rank = reinterpret_cast<int32_t*>(base + off[3]);
+    w.seq_list = reinterpret_cast<int32_t*>(base + off[4]);
+    w.Tf = reinterpret_cast<uint16_t*>(base + off[5]);
+    w.Mf = reinterpret_cast<uint16_t*>(base + off[6]);
+    w.G = reinterpret_cast<float*>(base + off[7]);
+    w.Kp = reinterpret_cast<uint8_t*>(base + off[8]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
     return w;
 }
 
@@ -187,8 +191,21 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const PrefillParams 
         run = carry;
         __syncthreads();
     }
-    // the chunk table: chunk c belongs to the last sequence s with chunk_off[s] <= c
     const int nc = run;
+    // seq_rank = exclusive prefix count of the non-empty sequences, seq_list their indices
+    run = 0;
+    for (int base = 0; base <= n; base += kPlanThreads) {
+        const int s = base + tid;
+        const int ne = s < n && p.ws.chunk_off[s + 1] > p.ws.chunk_off[s] ? 1 : 0;
+        const int inc = block_inclusive_scan<false>(ne, wave_tot) + run;
+        if (s <= n) p.ws.seq_rank[s] = inc - ne;
+        if (ne) p.ws.seq_list[inc - 1] = s;
+        if (tid == kPlanThreads - 1) carry = inc;
+        __syncthreads();
+        run = carry;
+        __syncthreads();
+    }
+    // the chunk table: chunk c belongs to the last sequence s with chunk_off[s] <= c
     for (int c = tid; c < nc; c += kPlanThreads) {
         int lo = 0, hi = n - 1;
         while (lo < hi) {
@@ -1323,11 +1340,20 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     const Layer& L = p.L;
     // XCD-aware mapping: the 8 strips of one (sequence, head) pair share an XCD, so its L2
     // serves the pair's chunk operands to all of them.
+    // Slot j of a window takes the j-th non-empty sequence from the one of the window's first
+    // chunk on: a window of W chunks touches at most W sequences.
     const int lin = blockIdx.x, xcd = lin & 7, kq = lin >> 3;
     const int strip = kq & (kStrips - 1);
     const int pair = (kq / kStrips) * 8 + xcd;
-    if (pair >= p.n_seq * L.h_v) return;
-    const int s = pair / L.h_v, h = pair % L.h_v, src = src_of(L, h);
+    if (pair >= min(p.n_seq, p.W) * L.h_v) return;
+    const int h = pair % L.h_v, src = src_of(L, h);
+    int s = 0;
+    if (!p.single) {
+        if (p.cb >= p.ws.chunk_off[p.n_seq]) return;        // past the last chunk
+        const int r = p.ws.seq_rank[p.ws.chunk_rec[p.cb].x] + pair / L.h_v;
+        if (r >= p.ws.seq_rank[p.n_seq]) return;
+        s = p.ws.seq_list[r];                                // its chunks may start past the window
+    }
     SeqGeo sg;
     sg.s = s;
     seq_bounds(p, s, sg.lo, sg.hi);
@@ -1480,7 +1506,8 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     if (gwin) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
     if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    const long long groups = (pairs + 7) / 8;
+    // chain workgroups: (sequence slot, v head, strip), at most min(n_seq, W) slots per window
+    const long long groups = ((long long)std::min((size_t)n_seq, W) * cfg->h_v + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
     const bool silu = cfg->conv_act == IX_GDN_ACT_SILU;
     const OutGate og = make_out_gate(gate);

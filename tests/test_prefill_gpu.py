@@ -241,6 +241,25 @@ def test_windows_match_one_window(cu, window):
         np.testing.assert_array_equal(a, b)
 
 
+def test_windows_with_many_sequences():
+    # 600 short sequences, a third of them empty, in windows of two chunks: each window's chain
+    # takes at most two sequence slots, found through the plan's list of non-empty sequences.
+    cfg = bx.make_cfg(h_k=2, h_v=4)
+    rng = np.random.default_rng(inputs.seed_for(4) + 9)
+    lens = rng.integers(1, 100, 600)
+    lens[rng.random(600) < 0.3] = 0
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    n, T = 600, int(cu[-1])
+    seed = inputs.seed_for(4) + 10
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, T)
+    st = inputs.initial_states(cfg, seed, n)
+    full = gpu_prefill(cfg, cu, tok, p, st)
+    win = gpu_prefill(cfg, cu, tok, p, st, window=2)
+    for a, b in zip(full, win):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_state_only_and_repeatable():
     cfg = bx.make_cfg()
     seed = inputs.seed_for(3) + 5
