@@ -1261,11 +1261,11 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 // chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads and
 // loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and the 6
 // nonzero fragments of T') into the value slot and waits for the copies before the barrier.
-// In the window that holds the sequence's last chunk it also writes the new rolling conv
-// history of the workgroup's channels: before alpha_0 its share of the sequence's q/k channels
+// In the window that holds the sequence's last chunk it also writes, in alpha_0, the new
+// rolling conv history of the workgroup's channels: its share of the sequence's q/k channels
 // (the h_v * 8 workgroups of a sequence split them into contiguous ranges; the chunk kernel has
-// read their old history), in alpha_0 the strip's 16 v channels (whose old history the output
-// waves read before the first window's alpha_0). Nothing else in this kernel writes conv_state.
+// read their old history) and the strip's 16 v channels (whose old history the output waves
+// read before the first window's alpha_0). Nothing else in this kernel writes conv_state.
 __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
                                                 int h, int strip, int src) {
     typedef __attribute__((address_space(3))) u4x lds_u4;
@@ -1304,18 +1304,16 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         __asm__ volatile("" ::: "memory");
     };
 
-    {
-        const int G = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + G - 1) / G;
-        const int ch_hi = min(cqk, (gi + 1) * per);
-        if (sg.last)
-            for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
-    }
     copy_keys(0);
     load(0);
     produce();
     wait_barrier();                                         // alpha_0
-    if (sg.last && lane < kStrip)
-        commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
+    if (sg.last) {
+        const int G = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + G - 1) / G;
+        const int ch_hi = min(cqk, (gi + 1) * per);
+        for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
+        if (lane < kStrip) commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
+    }
     for (int k = 0; k < sg.n; ++k) {
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
         // in alpha_{k-1}; they are read from alpha_{k+1} on.
@@ -1429,14 +1427,20 @@ static size_t prefill_ws_bytes(const ix_gdn_cfg* cfg, int n_seq, int T, size_t W
     return b;
 }
 
+// The default workspace: windows of at most kDefaultWindow chunks (8,192 tokens). The chunk
+// kernel and the chain never overlap, so a long batch in such windows takes about as long as in
+// one window, and the workspace stops growing with total_T (only the chunk tables do, 16 bytes
+// per chunk).
+constexpr size_t kDefaultWindow = 128;
+
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, ixg::max_chunks(n_seq, total_T), false);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kDefaultWindow), false);
 }
 
 extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, ixg::max_chunks(n_seq, total_T), true);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kDefaultWindow), true);
 }
 
 extern "C" size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T,

@@ -160,8 +160,10 @@ hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, 
                                uint16_t* o_bf16, const ix_gdn_out_gate* gate, void* workspace,
                                hipStream_t s IX_GDN_DEFAULT_STREAM);
 
-/* Bytes of device workspace for ix_gdn_prefill over n_seq sequences and total_T tokens in one
- * window (the fastest; about 2 MiB per 64-token chunk at the Qwen3-Next head layout). */
+/* Bytes of device workspace for ix_gdn_prefill over n_seq sequences and total_T tokens in
+ * windows of at most 128 chunks of 64 tokens (about 2 MiB per chunk at the Qwen3-Next head
+ * layout: 270 MiB at most, plus 16 bytes per chunk of tables). A batch of up to 8,192 tokens
+ * runs as one window; longer ones take about as long in windows as in one. */
 size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
 
 /* Bytes of device workspace for ix_gdn_prefill (gated = 0) or ix_gdn_prefill_gated (gated = 1)
@@ -182,21 +184,23 @@ size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, in
  *   o [total_T][h_v][d_v] fp32 or NULL; o_bf16 likewise
  *   workspace: 256-byte aligned device memory of at least
  *   ix_gdn_prefill_window_workspace_size(cfg, n_seq, total_T, 1, 0) bytes (windows of one
- *   chunk); ix_gdn_prefill_workspace_size() bytes run the whole batch as one window. */
+ *   chunk); the prefill uses windows of as many chunks as the workspace holds, e.g.
+ *   ix_gdn_prefill_workspace_size() bytes. */
 hipError_t ix_gdn_prefill(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
                           const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w, const uint16_t* a,
                           const uint16_t* b, const float* A_log, const float* dt_bias, float* state, float* o,
                           uint16_t* o_bf16, void* workspace, size_t workspace_bytes,
                           hipStream_t s IX_GDN_DEFAULT_STREAM);
 
-/* Bytes of device workspace ix_gdn_prefill_gated needs (the prefill's, plus room for the
- * fp32 outputs the norm reads when the caller passes no o). */
+/* Bytes of device workspace ix_gdn_prefill_gated needs in the default windows (the
+ * prefill's, plus room for one window's fp32 outputs, which the norm reads when the caller
+ * passes no o). */
 size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
 
 /* ix_gdn_prefill followed by the gated output norm of every (token, v head) row:
  * gate->z, gate->y, gate->y_bf16 are [total_T][h_v][d_v]; workspace_bytes must be at least
- * ix_gdn_prefill_window_workspace_size(cfg, n_seq, total_T, 1, 1) (one window:
- * ix_gdn_prefill_gated_workspace_size()). */
+ * ix_gdn_prefill_window_workspace_size(cfg, n_seq, total_T, 1, 1) (windows of one chunk;
+ * ix_gdn_prefill_gated_workspace_size() gives the default windows). */
 hipError_t ix_gdn_prefill_gated(const ix_gdn_cfg* cfg, int n_seq, int total_T, const int32_t* cu_seqlens,
                                 const uint16_t* x, uint16_t* conv_state, const uint16_t* conv_w,
                                 const uint16_t* a, const uint16_t* b, const float* A_log, const float* dt_bias,
