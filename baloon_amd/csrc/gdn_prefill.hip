@@ -1161,10 +1161,12 @@ __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const S
                                                  int lane, OutM& x) {
     const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
     const uint16_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragM;
+    // Row tiles 0 and 1 end before token 32, so their k-step 1 of M (tokens 32..63) is zero.
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
+        if (ks == 0 || r >= 2)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
+            for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
 }
 
 template <int DC, bool SILU>
@@ -1230,20 +1232,24 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         }
         if (k + 2 < sg.n) chain_out_load_q(p, sg, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
-        v4 D[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) D[m] = *(const lds_v4*)(hbase + kHandS + m * kPlane);
+        // M D: tokens 0-31 for every row tile, tokens 32-63 for row tiles 2 and 3 only.
         bf8 db[2][2];
-        split_tiles(D[0], D[1], db[0][0], db[0][1]);
-        split_tiles(D[2], D[3], db[1][0], db[1][1]);
+        {
+            const v4 d0 = *(const lds_v4*)(hbase + kHandS), d1 = *(const lds_v4*)(hbase + kHandS + kPlane);
+            split_tiles(d0, d1, db[0][0], db[0][1]);
+        }
         a0 = o;
         a1 = v4{0.f, 0.f, 0.f, 0.f};
         a2 = a1;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            a0 = mfma_bf16(M.mf[ks][0], db[ks][0], a0);
-            a1 = mfma_bf16(M.mf[ks][0], db[ks][1], a1);
-            a2 = mfma_bf16(M.mf[ks][1], db[ks][0], a2);
+        a0 = mfma_bf16(M.mf[0][0], db[0][0], a0);
+        a1 = mfma_bf16(M.mf[0][0], db[0][1], a1);
+        a2 = mfma_bf16(M.mf[0][1], db[0][0], a2);
+        if (r >= 2) {
+            const v4 d2 = *(const lds_v4*)(hbase + kHandS + 2 * kPlane), d3 = *(const lds_v4*)(hbase + kHandS + 3 * kPlane);
+            split_tiles(d2, d3, db[1][0], db[1][1]);
+            a0 = mfma_bf16(M.mf[1][0], db[1][0], a0);
+            a1 = mfma_bf16(M.mf[1][0], db[1][1], a1);
+            a2 = mfma_bf16(M.mf[1][1], db[1][0], a2);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = a0[i] + a1[i] + a2[i];
