@@ -1,4 +1,4 @@
-// gdn_prefill.hip -- chunked WY-form GDN prefill for gfx950 (ix_gdn_prefill).
+// gdn_prefill.hip -- chunked GDN prefill for gfx950 (ix_gdn_prefill).
 //
 // The same math as applying the fused decode token by token (conv, L2 norms, gates, head
 // map, delta rule; the reference's step is src/ix_gdn.cu:25-56), regrouped into chunks of
@@ -18,24 +18,21 @@
 // forming W.) Only differences G_t - G_s with t >= s are exponentiated, so no intermediate
 // overflows however strong the decay (Gam_t itself may underflow to 0, its correct value).
 //
-// Kernels, in stream order:
-//   plan_kernel    clamps cu_seqlens to a non-decreasing sequence in [0, total_T] and builds
-//                  the chunk table (sequence and first token of each chunk); not launched
-//                  for a single sequence, whose geometry the kernels derive from cu[0], cu[1]
-//   tri_kernel     per (chunk, q/k head): conv (history from conv_state at sequence starts,
-//                  which it also copies to the workspace) and L2 norms of q and k, the K K^T
-//                  and Q K^T lower block triangles once for all the v heads mapped to the q/k
-//                  head, then per v head the decay scan and beta, A and M, T = (I + A)^-1
-//                  (diagonal blocks by substitution, the rest by block forward substitution),
-//                  and T' = T diag(beta): written as split-bf16 MFMA fragments with M and the
-//                  decay factors -- 32.5 KiB per (chunk, v head), the chain's whole operand set
-//   chain_kernel   per (sequence, v head, 16-column state strip): walks the chunks in order.
-//                  One wave carries the strip in MFMA accumulators; one rebuilds the chunk's
-//                  normalised keys from x into LDS (the state wave reads them as K for K S and,
-//                  with transposing reads, as K^T for K^T Dg); one builds the strip's v columns
-//                  and copies T' into LDS; four compute the outputs, each rebuilding its 16 q
-//                  rows from x in registers. Before the first chunk the v wave writes the new
-//                  rolling conv history of the pair's share of channels.
+// Kernels, in stream order, per window of chunks (the workspace holds one window's chunk
+// operands; windows run one after the other, with identical results for any window size):
+//   plan_kernel    (once, n_seq > 1 only) clamps cu_seqlens to a non-decreasing sequence in
+//                  [0, total_T], builds the chunk table and lists the non-empty sequences;
+//                  a single sequence's geometry comes from cu[0], cu[1] directly
+//   tri_kernel     per (chunk, q/k head): conv and L2 norms of the chunk's q and k rows, the
+//                  K K^T and Q K^T lower block triangles once for all the v heads mapped to the
+//                  q/k head, then per v head the decay scan and beta, A and M, T = (I + A)^-1
+//                  (diagonal blocks by substitution, the rest by block forward substitution)
+//                  and T' = T diag(beta); it writes the chain's operands in their final
+//                  layouts: key planes, Q, M and T' as split-bf16 MFMA fragments, decay factors
+//   chain_kernel   per (sequence, v head, 16-column state strip): walks the window's chunks of
+//                  its sequence in order, two phases per chunk (roles below), and writes the
+//                  outputs, the state and, with the sequence's last chunk, the new conv history
+//   out_gate_*     (ix_gdn_prefill_gated) the gated RMS output norm of every (token, head) row
 // Every dense product runs on split-bf16 MFMA (three bf16 products per fp32 product, ~2^-16
 // relative error); only the 16 x 16 diagonal blocks of T are inverted in fp32 arithmetic.
 // The chunked result stays within ~1e-5 (state) of the token-by-token recurrence in double.
@@ -593,7 +590,8 @@ __device__ __forceinline__ void decay_scan(const PrefillParams& p, const ChunkGe
 }
 
 // ---------------------------------------------------------------------------------------
-// tri_kernel: grid (NC, h_k), 512 threads; workgroup = (chunk, q/k head).
+// tri_kernel: grid (window chunks, h_k), 512 threads at most 128 VGPRs (two workgroups per
+// CU); workgroup = (chunk, q/k head).
 //   1. q rows (waves 0-3) and k rows (waves 4-7): conv and L2 norm into split-bf16 planes.
 //   2. Each group of four waves (waves 0-3, waves 4-7) forms the raw K K^T and (Q K^T)^T
 //      blocks of the lower block triangle in its registers (both groups the same blocks), and
@@ -602,8 +600,8 @@ __device__ __forceinline__ void decay_scan(const PrefillParams& p, const ChunkGe
 //      and M to its fragments, the diagonal blocks of T = (I + A)^-1 by substitution (the
 //      group's first wave), the blocks below them by block forward substitution (three
 //      waves), then T' = T diag(beta) as fragments (two per wave).
-// At a sequence's first chunk the workgroup also copies the old conv history of its q/k
-// channels and of its v heads' channels to the workspace, where the chain reads it.
+// At a sequence's first chunk the conv reads the old q/k history from conv_state; the chain,
+// which runs after this kernel, writes the new history.
 // Every barrier orders LDS only, so no wave waits for its own global stores.
 // ---------------------------------------------------------------------------------------
 template <int DC, bool SILU>
