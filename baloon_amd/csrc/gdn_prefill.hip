@@ -799,8 +799,9 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 // run in two phases per chunk, alpha_k and beta_k, each ended by a workgroup barrier:
 //   alpha_k  the state waves (0, 1) each hold 64 rows of S in MFMA accumulators (row tile mt
 //            of wave i: S[64 i + 16 mt + 4 lg4 + r][column li]); for k > 0 they finish
-//            S_k = gam S_{k-1} + K_{k-1}^T Dg_{k-1} on their rows, hand S_k over split and
-//            form their half of W_k (the sum over their 64 channels);
+//            S_k = gam S_{k-1} + K_{k-1}^T Dg_{k-1} on their rows (K^T read in beta_{k-1}),
+//            hand S_k over split and form their half of W_k (the sum over their 64 channels,
+//            K read as the products need it);
 //   beta_k   the D wave (4) adds the halves and forms D_k, handing over D_k (fp32) for the
 //            outputs and Dg_k (split) with gam_k for the state waves.
 // Products take their k index in accumulator row order (kperm), so an accumulator tile pair,
@@ -811,7 +812,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 // also builds row tile r of chunk c_{k+1}'s V (the conv of the strip's v channels) into the
 // value slot. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
 // with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
-// until alpha_{k-1}), and in beta_k writes chunk c_{k+1}'s decay factors and T' fragments into
+// until beta_{k-2}), and in beta_k writes chunk c_{k+1}'s decay factors and T' fragments into
 // the value slot from registers loaded in alpha_k; it also writes the new rolling conv history
 // of the workgroup's channels.
 // A last alpha_n finishes S_n (state waves) and O_{n-1} (output waves).
@@ -995,8 +996,12 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // beta_k
         const int q1 = q == kKSlots - 1 ? 0 : q + 1;
+        // K^T of chunk c_k, for S_{k+1}, read in beta after a pause of about 768 cycles: issued
+        // at once, its 32 reads would queue the D wave's W reads behind them; not issued
+        // until alpha, their latency would open the next phase.
+        __builtin_amdgcn_s_sleep(12);
+        load_kt(q);
         lds_barrier();                                      // alpha_{k+1}: Dg_k, gam_k handed over
-        load_kt(q);                                         // K^T of chunk c_k, for S_{k+1}
         bf8 dh[2], dl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -1320,7 +1325,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     }
     for (int k = 0; k < sg.n; ++k) {
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
-        // in alpha_{k-1}; they are read from alpha_{k+1} on.
+        // in beta_{k-2}; they are read from alpha_{k+1} on.
         if (k + 1 < sg.n) {
             copy_keys(k + 1);
             load(k + 1);
