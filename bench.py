@@ -114,13 +114,35 @@ def bf16_f32(bits) -> np.ndarray:
     return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+_HEAT = {}
+
+
+def heat(ms=40.0):
+    """Brings the GPU to its loaded clocks: about `ms` of in-place streaming over a scratch
+    buffer that nothing measured or checked reads. Started from idle, the first tens of
+    milliseconds of a workload run up to ~8% slower while the clocks rise (the same decode
+    launches took 46.9 us in their first 12 ms and 45.3 us after), so every timed region below
+    is measured at the clocks a continuously loaded GPU runs at."""
+    import torch
+    if "buf" not in _HEAT:
+        _HEAT["buf"] = torch.ones(64 << 20, dtype=torch.float32, device="cuda")      # 256 MiB
+    buf = _HEAT["buf"]
+    end = time.perf_counter() + ms / 1e3
+    while time.perf_counter() < end:
+        for _ in range(8):
+            buf.mul_(1.0)
+        torch.cuda.synchronize()
+
+
 def timed(stream, fn, n):
-    """n calls of fn(i) between HIP events recorded on `stream`; every status checked after."""
+    """n calls of fn(i) between HIP events recorded on `stream`, right after heat(); every
+    status checked after."""
     import torch
 
     import baloon_amd as bx
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    heat()
     e0.record(stream)
     rcs = [fn(i) for i in range(n)]
     e1.record(stream)
@@ -593,6 +615,7 @@ def latency_leg(O, iters=200, graph_steps=32, graph_replays=20):
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
+    heat()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(graph_replays):
@@ -761,6 +784,7 @@ def hbm_ceiling(nbuf=4, mib=128, iters=20):
     for b in bufs:
         b.mul_(1.0)
     torch.cuda.synchronize()
+    heat()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(iters):
