@@ -527,8 +527,8 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
         }
     }
     // Blocks 0 and 1 of every wave: fragment (br, bc / 2) of the first. Block 2 of waves 0 and
-    // 1 (a diagonal block, right neighbour zero); waves 2 and 3 write the zero fragments of
-    // block rows 0 and 1 at k-step 1.
+    // 1 (a diagonal block, right neighbour zero). The fragments of block rows 0 and 1 at
+    // k-step 1 are zero and not stored: the chain never reads them.
     int br, bc;
     tri_block(w, br, bc);
     float x[8];
@@ -537,13 +537,10 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
     store_frag(Mf, br, bc >> 1, 2, lane, x);
     if (w < 2) {
         tri_block(w + 8, br, bc);
-    } else {
-        br = w - 2;
-        bc = 2;
-    }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { x[r] = mv[2][r]; x[4 + r] = 0.0f; }
-    store_frag(Mf, br, bc >> 1, 2, lane, x);
+        for (int r = 0; r < 4; ++r) { x[r] = mv[2][r]; x[4 + r] = 0.0f; }
+        store_frag(Mf, br, bc >> 1, 2, lane, x);
+    }
 }
 
 // Row tile mt, k-step ks of T' = T diag(sc) as a split-bf16 A fragment: lane (li, lg4) holds
@@ -770,12 +767,14 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
         }
         lds_barrier();
         // T' = T diag(beta) as the chain's A fragments (4 row tiles x 2 k-steps): wave gw
-        // writes fragments gw and gw + 4, (row tile f / 2, k-step f % 2).
+        // writes fragments gw and gw + 4, (row tile f / 2, k-step f % 2), except the zero ones
+        // above the diagonal blocks (row tiles 0 and 1 at k-step 1), which the chain never reads.
         if (live) {
             uint16_t* Tf = p.ws.Tf + ch * kFragM;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int f = gw + 4 * u, mt = f >> 1, ks = f & 1;
+                if (ks == 1 && mt < 2) continue;
                 bf8 hi, lo;
                 t_frag(T_s, B_s[grp], mt, ks, li, lg4, hi, lo);
                 *reinterpret_cast<bf8*>(Tf + frag_at(mt, ks, 2, 0, lane)) = hi;

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 # kernel carries a few (its SGPR working set is the chunk geometry and many workspace base
 # addresses); it is bounded here at its current count so that a regression fails. Every other
 # kernel must have none.
-SGPR_SPILL_BOUND = {"chain_kernel": 16, "tri_kernel": 24}
+SGPR_SPILL_BOUND = {"chain_kernel": 16, "tri_kernel": 32}
 
 
 def resource_lines():
