@@ -63,9 +63,13 @@ struct Ws {
     uint16_t* Qf;        // [W][h_k] Q (64 x 128) as split-bf16 A fragments
 };
 constexpr int kWsSections = 10;
-constexpr int kPRow = 2 * 128 + 16;                     // key plane row: 128 bf16, 16 bytes of padding
+constexpr int kPRow = 2 * 128;                          // key plane row: 128 bf16 as 16 chunks of 16 bytes
 constexpr int kKPlane = 64 * kPRow;                     // one plane (hi or lo) of 64 keys
-constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 34,816 bytes
+constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 32 KiB
+// Chunk j of key row t is stored at chunk j ^ kswz(t) of its row: the two 2-bit halves of
+// t mod 16 swapped, so that the chain's 16-byte fragment reads (16 rows, one chunk column) and
+// its transposing 8-byte reads (4 rows x 4 chunk columns per lane group) hit 16 distinct chunks.
+__host__ __device__ constexpr int kswz(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
@@ -658,8 +662,8 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
     }
     lds_barrier();
 
-    // The chain's key planes (row t: 128 bf16 with each 32-channel block in kperm order, then
-    // 16 bytes of padding; hi plane, then lo) and Q fragments (rows t, k = channel in kperm
+    // The chain's key planes (row t: 128 bf16 with each 32-channel block in kperm order, its
+    // 16-byte chunks swizzled by kswz(t); hi plane, then lo) and Q fragments (rows t, k = channel in kperm
     // order), from the swizzled planes: every thread moves 4 of the 16-byte key chunks and 4 Q
     // fragment chunks. Key chunk j of a row holds channels 32 (j / 4) + 4 (j % 4) .. +3, then
     // the 4 channels 16 later.
@@ -671,7 +675,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
             const int c0 = 32 * (cc >> 2) + 4 * (cc & 3);
             const uint2 a = *reinterpret_cast<const uint2*>(Kp + pl * kQKPlane + qk_off(t, c0));
             const uint2 b = *reinterpret_cast<const uint2*>(Kp + pl * kQKPlane + qk_off(t, c0 + 16));
-            *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * cc) = u4x{a.x, a.y, b.x, b.y};
+            *reinterpret_cast<u4x*>(kg + pl * kKPlane + t * kPRow + 16 * (cc ^ kswz(t))) = u4x{a.x, a.y, b.x, b.y};
         }
         uint16_t* Qg = p.ws.Qf + ((size_t)lc * L.h_k + src) * kFragW;
 #pragma unroll
@@ -832,7 +836,7 @@ constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlo
 constexpr int kXRows = 24;                              // an output wave's x staging: rows 16 r - 3 .. 16 r + 20
 constexpr int kXBytes = 4 * kXRows * kStrip * 2;        // 16 bf16 channels per row, 4 output waves
 constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
-constexpr int kChainLds = kOffX + kXBytes;              // 149,008 bytes
+constexpr int kChainLds = kOffX + kXBytes;              // 142,864 bytes
 
 typedef __attribute__((address_space(3))) bf8 lds_bf8;
 typedef __attribute__((address_space(3))) v4 lds_v4;
@@ -863,9 +867,13 @@ __device__ __forceinline__ void split_tiles(const v4& a, const v4& b, bf8& hi, b
 // position 32 b + 8 a + 4 h + e.
 // K fragment (token tile mt, channel k-step ks) of a key slot: A operand of K S. Lane
 // (li, lg4) reads row 16 mt + li, channels 32 ks + 4 lg4 .. +3 and 32 ks + 16 + 4 lg4 .. +3:
-// 16 contiguous bytes per plane from the lane base kb = slot + li * kPRow + 16 lg4.
-__device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, int ks, bf8& hi, bf8& lo) {
-    const int o = mt * 16 * kPRow + ks * 64;
+// the 16 bytes of chunk 4 ks + lg4, stored at chunk (4 ks + lg4) ^ kswz(li) of the row.
+__device__ __forceinline__ int k_lane(int li, int lg4, int ks) {
+    return li * kPRow + 16 * ((4 * ks + lg4) ^ kswz(li));
+}
+// kb: the slot plus k_lane(li, lg4, ks).
+__device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, bf8& hi, bf8& lo) {
+    const int o = mt * 16 * kPRow;
     hi = *(const lds_bf8*)(kb + o);
     lo = *(const lds_bf8*)(kb + kKPlane + o);
 }
@@ -873,12 +881,17 @@ __device__ __forceinline__ void k_frag(const lds_u8* kb, int mt, int ks, bf8& hi
 // K^T fragment (channel tile m, token k-step ks) of a key slot: A operand of K^T Dg, by
 // transposing reads (ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
 // j & 3 of the 8-byte reads of lanes (j >> 2) + 4 e, e = 0..3). Lane i of lane group g reads
-// channels 16 m + 4 (i & 3) .. +3 of token 32 ks + 4 g + (i >> 2) (then of the token 16
+// channels 16 m + 4 (i & 3) .. +3 of token t = 32 ks + 4 g + (i >> 2) (then of the token 16
 // later), so it receives channel 16 m + i at tokens 32 ks + 4 g + e (+ 16): entries e (4 + e)
-// of its kperm fragment chunk. Those 4 channels sit at position 32 (m / 2) + 8 (i & 3) +
-// 4 (m & 1); lane base tb = slot + (4 g + (i >> 2)) * kPRow + 16 (i & 3).
-__device__ __forceinline__ void kt_frag(const lds_u8* tb, int m, int ks, bf8& hi, bf8& lo) {
-    const int o = ks * 32 * kPRow + (m >> 1) * 64 + (m & 1) * 8;
+// of its kperm fragment chunk. Those 4 channels are half m & 1 of chunk 4 (m / 2) + (i & 3),
+// stored at chunk (4 (m / 2) + (i & 3)) ^ kswz(t) of the row (kswz(t) depends on i and g only).
+__device__ __forceinline__ int kt_lane(int i, int g, int mh) {
+    const int t = 4 * g + (i >> 2);
+    return t * kPRow + 16 * ((4 * mh + (i & 3)) ^ kswz(t));
+}
+// tb: the slot plus kt_lane(i, g, m / 2); half = m & 1.
+__device__ __forceinline__ void kt_frag(const lds_u8* tb, int half, int ks, bf8& hi, bf8& lo) {
+    const int o = ks * 32 * kPRow + half * 8;
     const uint2 a = lds_tr16(tb + o), b = lds_tr16(tb + o + 16 * kPRow);
     const uint2 c = lds_tr16(tb + kKPlane + o), d = lds_tr16(tb + kKPlane + o + 16 * kPRow);
     hi = __builtin_bit_cast(bf8, u4x{a.x, a.y, b.x, b.y});
@@ -946,11 +959,12 @@ __device__ __forceinline__ ChunkGeo seq_chunk(const SeqGeo& sg, int k) {
 // the accumulator of row tile mt (rows 64 half + 16 mt + 4 lg4 + r, column li).
 __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, int half, v4 (&S)[4]) {
     const int li = lane & 15, lg4 = lane >> 4;
-    lds_u8 *kb[kKSlots], *tb[kKSlots];
+    // Lane offsets in a key slot: K of k-steps 2 half + a, K^T of channel tiles 4 half + 2 a + j.
+    int koff[2], toff[2];
 #pragma unroll
-    for (int q = 0; q < kKSlots; ++q) {
-        kb[q] = lane_at(lds, kOffK + q * kKSlot + li * kPRow + 16 * lg4);
-        tb[q] = lane_at(lds, kOffK + q * kKSlot + (4 * lg4 + (li >> 2)) * kPRow + 16 * (li & 3));
+    for (int a = 0; a < 2; ++a) {
+        koff[a] = k_lane(li, lg4, 2 * half + a);
+        toff[a] = kt_lane(li, lg4, 2 * half + a);
     }
     lds_u8* hb = lane_at(lds, kOffH + 4 * half * kPlane + lane * 16);     // S k-steps 2 half, 2 half + 1
     lds_u8* wb = lane_at(lds, kOffW + 4 * half * kPlane + lane * 16);
@@ -958,16 +972,18 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
     // K: channel k-step 2 half + a, token tile mt; K^T: token k-step ks, channel tile 4 half + j.
     bf8 KF[2][4][2], KT[2][4][2];
     auto load_k = [&](int q) {
+        const lds_u8* slot = (lds_u8*)lds + kOffK + q * kKSlot;
 #pragma unroll
         for (int a = 0; a < 2; ++a)
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) k_frag(kb[q], mt, 2 * half + a, KF[a][mt][0], KF[a][mt][1]);
+            for (int mt = 0; mt < 4; ++mt) k_frag(slot + koff[a], mt, KF[a][mt][0], KF[a][mt][1]);
     };
     auto load_kt = [&](int q) {
+        const lds_u8* slot = (lds_u8*)lds + kOffK + q * kKSlot;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) kt_frag(tb[q], 4 * half + j, ks, KT[ks][j][0], KT[ks][j][1]);
+            for (int j = 0; j < 4; ++j) kt_frag(slot + toff[j >> 1], j & 1, ks, KT[ks][j][0], KT[ks][j][1]);
     };
     // S_k handed over split (the outputs' B operand) and this wave's half of W_k = K_k S_k.
     auto hand_and_w = [&]() {
