@@ -55,14 +55,17 @@ struct Ws {
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
     int32_t* seq_rank;   // [n_seq + 1] non-empty sequences before s (seq_rank[n_seq] = all of them)
     int32_t* seq_list;   // [n_seq] the non-empty sequences in order
-    uint16_t* Tf;        // [W][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
-    uint16_t* Mf;        // [W][h_v] M (64 x 64) as split-bf16 A fragments
+    uint8_t* Tf;         // [W][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
+                         // (the nonzero ones, kTriFragBytes per head)
+    uint8_t* Mf;         // [W][h_v] M (64 x 64) as split-bf16 A fragments (kFragMBytes per head)
     float* G;            // [W][h_v][2][64] decay factors exp(G_last - G_t), then exp(G_t), of the
                          // inclusive cumulative log decay G (padded rows repeat the last)
     uint8_t* Kp;         // [W][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
     uint16_t* Qf;        // [W][h_k] Q (64 x 128) as split-bf16 A fragments
 };
 constexpr int kWsSections = 10;
+constexpr int kTriFragBytes = 10 * 1024;                // T' of one (chunk, v head)
+constexpr int kFragMBytes = 16 * 1024;                  // M of one (chunk, v head)
 constexpr int kPRow = 2 * 128;                          // key plane row: 128 bf16 as 16 chunks of 16 bytes
 constexpr int kKPlane = 64 * kPRow;                     // one plane (hi or lo) of 64 keys
 constexpr int kKSlot = 2 * kKPlane;                     // hi, then lo: 32 KiB
@@ -82,7 +85,7 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t W, size_t 
     const size_t NC = max_chunks(n_seq, T);
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
-        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * n_seq, sizeof(float) * W * c->h_v * kChunk * kChunk, sizeof(float) * W * c->h_v * kChunk * kChunk,
+        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * n_seq, (size_t)kTriFragBytes * W * c->h_v, (size_t)kFragMBytes * W * c->h_v,
         sizeof(float) * W * c->h_v * 2 * kChunk, (size_t)kKSlot * W * c->h_k,
         sizeof(uint16_t) * W * c->h_k * 4 * 4 * 2 * 512,
     };
@@ -98,8 +101,8 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.chunk_rec = reinterpret_cast<int4*>(base + off[2]);
     w.seq_rank = reinterpret_cast<int32_t*>(base + off[3]);
     w.seq_list = reinterpret_cast<int32_t*>(base + off[4]);
-    w.Tf = reinterpret_cast<uint16_t*>(base + off[5]);
-    w.Mf = reinterpret_cast<uint16_t*>(base + off[6]);
+    w.Tf = reinterpret_cast<uint8_t*>(base + off[5]);
+    w.Mf = reinterpret_cast<uint8_t*>(base + off[6]);
     w.G = reinterpret_cast<float*>(base + off[7]);
     w.Kp = reinterpret_cast<uint8_t*>(base + off[8]);
     w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
@@ -393,15 +396,41 @@ __device__ __forceinline__ size_t frag_at(int m, int ks, int nks, int plane, int
     return ((((size_t)m * nks + ks) * 2 + plane) * kWave + lane) * 8;       // in bf16 elements
 }
 
-__device__ __forceinline__ void store_frag(uint16_t* base, int m, int ks, int nks, int lane, const float (&x)[8]) {
-    bf8 hi, lo;
-    split8(x, hi, lo);
-    *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 0, lane)) = hi;
-    *reinterpret_cast<bf8*>(base + frag_at(m, ks, nks, 1, lane)) = lo;
+__device__ __forceinline__ void store_frag(uint8_t* base, int m, int ks, int nks, int lane, const bf8& hi, const bf8& lo) {
+    *reinterpret_cast<bf8*>(base + 2 * frag_at(m, ks, nks, 0, lane)) = hi;
+    *reinterpret_cast<bf8*>(base + 2 * frag_at(m, ks, nks, 1, lane)) = lo;
+}
+
+// T' (64 x 64, lower triangular, split) stores its 6 nonzero fragments back to back, (0, 0),
+// (1, 0), (2, 0), (2, 1), (3, 0), (3, 1); (0, 0) and (2, 1) pair a diagonal block with a zero
+// block, so only entries 0..3 of each lane are stored (8 bytes a lane, 512 a plane). Byte offset
+// of a lane's part of one plane:
+__host__ __device__ constexpr bool tri_half(int m, int ks) { return (m == 0 && ks == 0) || (m == 2 && ks == 1); }
+__device__ __forceinline__ int tri_frag_at(int m, int ks, int plane, int lane) {
+    const int off = m == 0 ? 0 : m == 1 ? 1024 : m == 2 ? (ks ? 5120 : 3072) : (ks ? 8192 : 6144);
+    return off + (tri_half(m, ks) ? plane * 512 + lane * 8 : plane * 1024 + lane * 16);
+}
+__device__ __forceinline__ void store_tri_frag(uint8_t* base, int m, int ks, int lane, const bf8& hi, const bf8& lo) {
+    if (tri_half(m, ks)) {
+        const u4x h = __builtin_bit_cast(u4x, hi), l = __builtin_bit_cast(u4x, lo);
+        *reinterpret_cast<uint2*>(base + tri_frag_at(m, ks, 0, lane)) = uint2{h.x, h.y};
+        *reinterpret_cast<uint2*>(base + tri_frag_at(m, ks, 1, lane)) = uint2{l.x, l.y};
+    } else {
+        *reinterpret_cast<bf8*>(base + tri_frag_at(m, ks, 0, lane)) = hi;
+        *reinterpret_cast<bf8*>(base + tri_frag_at(m, ks, 1, lane)) = lo;
+    }
+}
+// The whole fragment plane (zeros in a half fragment's entries 4..7); m and ks are compile-time
+// constants where it is used.
+__device__ __forceinline__ u4x load_tri_frag(const uint8_t* base, int m, int ks, int plane, int lane) {
+    if (tri_half(m, ks)) {
+        const uint2 v = *reinterpret_cast<const uint2*>(base + tri_frag_at(m, ks, plane, lane));
+        return u4x{v.x, v.y, 0u, 0u};
+    }
+    return *reinterpret_cast<const u4x*>(base + tri_frag_at(m, ks, plane, lane));
 }
 
 // Fragment sizes in bf16 elements: (rows/16) x (k/32) fragments x 2 planes x 512.
-constexpr size_t kFragM = 4 * 2 * 2 * 512;     // 64 x 64 (T', M)
 constexpr size_t kFragW = 4 * 4 * 2 * 512;     // 64 x 128 (Q)
 
 // ---------------------------------------------------------------------------------------
@@ -497,7 +526,7 @@ __device__ __forceinline__ void t_column(const float* A_s, float* T_s, int lane)
 // Branch-free; the decay uses the hardware exp (relative error <= 4e-6 down to the fp32
 // underflow of exp(G_t - G_s)).
 __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], const float* G, const float* Bt,
-                                        float* A_s, uint16_t* Mf, int w, int lane) {
+                                        float* A_s, uint8_t* Mf, int w, int lane) {
     const int li = lane & 15, lg4 = lane >> 4;
     float mv[3][4];
 #pragma unroll
@@ -536,14 +565,17 @@ __device__ __forceinline__ void am_head(const v4 (&kk)[3], const v4 (&qk)[3], co
     int br, bc;
     tri_block(w, br, bc);
     float x[8];
+    bf8 hi, lo;
 #pragma unroll
     for (int r = 0; r < 4; ++r) { x[r] = mv[0][r]; x[4 + r] = mv[1][r]; }
-    store_frag(Mf, br, bc >> 1, 2, lane, x);
+    split8(x, hi, lo);
+    store_frag(Mf, br, bc >> 1, 2, lane, hi, lo);
     if (w < 2) {
         tri_block(w + 8, br, bc);
 #pragma unroll
         for (int r = 0; r < 4; ++r) { x[r] = mv[2][r]; x[4 + r] = 0.0f; }
-        store_frag(Mf, br, bc >> 1, 2, lane, x);
+        split8(x, hi, lo);
+        store_frag(Mf, br, bc >> 1, 2, lane, hi, lo);
     }
 }
 
@@ -743,7 +775,7 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
             }
             lds_barrier();
         }
-        if (live) am_head(kk, qk, G_s[grp], B_s[grp], A_s, p.ws.Mf + ch * kFragM, gw, lane);
+        if (live) am_head(kk, qk, G_s[grp], B_s[grp], A_s, p.ws.Mf + ch * kFragMBytes, gw, lane);
         lds_barrier();
         // The group's first wave inverts the four unit lower-triangular diagonal blocks of
         // I + A (lane = 16 b + column cc).
@@ -774,15 +806,14 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
         // writes fragments gw and gw + 4, (row tile f / 2, k-step f % 2), except the zero ones
         // above the diagonal blocks (row tiles 0 and 1 at k-step 1), which the chain never reads.
         if (live) {
-            uint16_t* Tf = p.ws.Tf + ch * kFragM;
+            uint8_t* Tf = p.ws.Tf + ch * kTriFragBytes;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int f = gw + 4 * u, mt = f >> 1, ks = f & 1;
                 if (ks == 1 && mt < 2) continue;
                 bf8 hi, lo;
                 t_frag(T_s, B_s[grp], mt, ks, li, lg4, hi, lo);
-                *reinterpret_cast<bf8*>(Tf + frag_at(mt, ks, 2, 0, lane)) = hi;
-                *reinterpret_cast<bf8*>(Tf + frag_at(mt, ks, 2, 1, lane)) = lo;
+                store_tri_frag(Tf, mt, ks, lane, hi, lo);
             }
         }
         if (2 * (it + 1) < nmap) lds_barrier();             // T and beta are read until here
@@ -1178,13 +1209,13 @@ __device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const S
 __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const SeqGeo& sg, int k, int h, int r,
                                                  int lane, OutM& x) {
     const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
-    const uint16_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragM;
+    const uint8_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragMBytes;
     // Row tiles 0 and 1 end before token 32, so their k-step 1 of M (tokens 32..63) is zero.
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
         if (ks == 0 || r >= 2)
 #pragma unroll
-            for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + frag_at(r, ks, 2, pl, lane));
+            for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + 2 * frag_at(r, ks, 2, pl, lane));
 }
 
 template <int DC, bool SILU>
@@ -1299,11 +1330,11 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     auto load = [&](int k) {
         const size_t chh = (size_t)(sg.wk + min(k, sg.n - 1)) * L.h_v + h;
         eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
-        const u4x* tsrc = reinterpret_cast<const u4x*>(p.ws.Tf + chh * kFragM) + lane;
+        const uint8_t* tsrc = p.ws.Tf + chh * kTriFragBytes;
 #pragma unroll
         for (int i = 0; i < 12; ++i) {
-            const int f = i < 8 ? 2 * (i >> 1) : 2 * (i >> 1) - 3;    // fragment mt * 2 + ks of slot entry i / 2
-            tf[i] = tsrc[(2 * f + (i & 1)) * kWave];
+            const int e = i >> 1, mt = e < 4 ? e : e - 2, ks = e < 4 ? 0 : 1;    // slot entry e, plane i & 1
+            tf[i] = load_tri_frag(tsrc, mt, ks, i & 1, lane);
         }
     };
     auto produce = [&]() {
@@ -1407,7 +1438,9 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     } else if (w == 5) {
         chain_feed_role(p, lds, lane, sg, h, strip, src);
     } else {
-        chain_output_role<DC, SILU>(p, lds, lane, w < 4 ? w - 2 : w - 4, sg, h, src, strip);
+        // Row tiles 0, 1 on waves 2, 3 and 3, 2 on waves 6, 7: each SIMD's pair runs 3 of M D's
+        // 6 k-steps (2-4% faster than tiles 2, 3 on waves 6, 7).
+        chain_output_role<DC, SILU>(p, lds, lane, w < 4 ? w - 2 : 9 - w, sg, h, src, strip);
     }
 }
 
