@@ -53,8 +53,6 @@ struct Ws {
     int32_t* seq_lo;     // [n_seq + 1] clamped token offsets
     int32_t* chunk_off;  // [n_seq + 1] first chunk of each sequence; chunk_off[n_seq] = #chunks
     int4* chunk_rec;     // [NC] {sequence, first token, sequence start, sequence end}
-    int32_t* seq_rank;   // [n_seq + 1] non-empty sequences before s (seq_rank[n_seq] = all of them)
-    int32_t* seq_list;   // [n_seq] the non-empty sequences in order
     uint8_t* Tf;         // [W][h_v] T' = (I + A)^-1 diag(beta) (64 x 64) as split-bf16 A fragments
                          // (the nonzero ones, kTriFragBytes per head)
     uint8_t* Mf;         // [W][h_v] M (64 x 64) as split-bf16 A fragments (kFragMBytes per head)
@@ -63,7 +61,7 @@ struct Ws {
     uint8_t* Kp;         // [W][h_k] normalised keys as split-bf16 planes in the chain's LDS layout
     uint16_t* Qf;        // [W][h_k] Q (64 x 128) as split-bf16 A fragments
 };
-constexpr int kWsSections = 10;
+constexpr int kWsSections = 8;
 constexpr int kTriFragBytes = 10 * 1024;                // T' of one (chunk, v head)
 constexpr int kFragMBytes = 16 * 1024;                  // M of one (chunk, v head)
 constexpr int kPRow = 2 * 128;                          // key plane row: 128 bf16 as 16 chunks of 16 bytes
@@ -85,8 +83,7 @@ inline size_t ws_layout(const ix_gdn_cfg* c, int n_seq, int T, size_t W, size_t 
     const size_t NC = max_chunks(n_seq, T);
     const size_t sz[kWsSections] = {
         sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * (n_seq + 1), sizeof(int4) * NC,
-        sizeof(int32_t) * (n_seq + 1), sizeof(int32_t) * n_seq, (size_t)kTriFragBytes * W * c->h_v, (size_t)kFragMBytes * W * c->h_v,
-        sizeof(float) * W * c->h_v * 2 * kChunk, (size_t)kKSlot * W * c->h_k,
+        (size_t)kTriFragBytes * W * c->h_v, (size_t)kFragMBytes * W * c->h_v, sizeof(float) * W * c->h_v * 2 * kChunk, (size_t)kKSlot * W * c->h_k,
         sizeof(uint16_t) * W * c->h_k * 4 * 4 * 2 * 512,
     };
     size_t pos = 0;
@@ -99,13 +96,11 @@ inline Ws ws_bind(char* base, const size_t off[kWsSections]) {
     w.seq_lo = reinterpret_cast<int32_t*>(base + off[0]);
     w.chunk_off = reinterpret_cast<int32_t*>(base + off[1]);
     w.chunk_rec = reinterpret_cast<int4*>(base + off[2]);
-    w.seq_rank = reinterpret_cast<int32_t*>(base + off[3]);
-    w.seq_list = reinterpret_cast<int32_t*>(base + off[4]);
-    w.Tf = reinterpret_cast<uint8_t*>(base + off[5]);
-    w.Mf = reinterpret_cast<uint8_t*>(base + off[6]);
-    w.G = reinterpret_cast<float*>(base + off[7]);
-    w.Kp = reinterpret_cast<uint8_t*>(base + off[8]);
-    w.Qf = reinterpret_cast<uint16_t*>(base + off[9]);
+    w.Tf = reinterpret_cast<uint8_t*>(base + off[3]);
+    w.Mf = reinterpret_cast<uint8_t*>(base + off[4]);
+    w.G = reinterpret_cast<float*>(base + off[5]);
+    w.Kp = reinterpret_cast<uint8_t*>(base + off[6]);
+    w.Qf = reinterpret_cast<uint16_t*>(base + off[7]);
     return w;
 }
 
@@ -123,6 +118,7 @@ struct PrefillParams {
     int n_seq, T, NC;
     int single;                 // n_seq == 1: no plan pass; the geometry comes from cu[0], cu[1]
     int cb, W;                  // the window: chunks cb .. cb + W - 1
+    int G;                      // chain workgroups per (v head, strip) in a window (1 for n_seq == 1)
     int o_win;                  // o holds the window's tokens only (row 0 = its first token)
 };
 
@@ -196,19 +192,6 @@ __global__ void __launch_bounds__(kPlanThreads) plan_kernel(const PrefillParams 
         __syncthreads();
     }
     const int nc = run;
-    // seq_rank = exclusive prefix count of the non-empty sequences, seq_list their indices
-    run = 0;
-    for (int base = 0; base <= n; base += kPlanThreads) {
-        const int s = base + tid;
-        const int ne = s < n && p.ws.chunk_off[s + 1] > p.ws.chunk_off[s] ? 1 : 0;
-        const int inc = block_inclusive_scan<false>(ne, wave_tot) + run;
-        if (s <= n) p.ws.seq_rank[s] = inc - ne;
-        if (ne) p.ws.seq_list[inc - 1] = s;
-        if (tid == kPlanThreads - 1) carry = inc;
-        __syncthreads();
-        run = carry;
-        __syncthreads();
-    }
     // the chunk table: chunk c belongs to the last sequence s with chunk_off[s] <= c
     for (int c = tid; c < nc; c += kPlanThreads) {
         int lo = 0, hi = n - 1;
@@ -354,27 +337,34 @@ __device__ __forceinline__ void conv_run(ConvIn<DC> in, float (&y0)[kConvTok], f
 
 // ---------------------------------------------------------------------------------------
 // commit: the rolling conv history of channel ch after sequence s, tokens lo .. lo+len-1
-// (len > 0); run by the chain kernel, whose other reads of the old history go to the
-// workspace copy the chunk kernel made
+// (len > 0); run by the chain kernel after every read of the old history
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ void commit_history(const PrefillParams& p, int ch, int lo, int len, int s) {
+// The new history's dc-1 values, loaded (hist_fetch), then stored (hist_put) once they have
+// arrived, so that a wave can issue other loads in between.
+struct HistNew { uint16_t v[3]; };
+__device__ __forceinline__ HistNew hist_fetch(const PrefillParams& p, int ch, int lo, int len, int s) {
     const Layer& L = p.L;
-    uint16_t* st = p.conv_state + ((size_t)s * L.C + ch) * (L.dc - 1);
+    const uint16_t* st = p.conv_state + ((size_t)s * L.C + ch) * (L.dc - 1);
     // extended history [old (dc-1 values) | the sequence's inputs]; the new history is its
     // last dc-1 entries, i.e. entries len .. len+dc-2. An entry below dc-1 is old history.
     const uint16_t o0 = st[0], o1 = L.dc > 2 ? st[1] : (uint16_t)0, o2 = L.dc > 3 ? st[2] : (uint16_t)0;
     // Entries j >= dc-1 are not stored; their token index is clamped into the sequence, so
     // that no load reaches past its last token.
-    uint16_t nw[3];
+    HistNew h;
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
         const int ext = len + j;                               // index into the extended history
         const int pos = ext - (L.dc - 1);                      // token position when >= 0
-        nw[j] = pos >= 0 ? p.x[(size_t)(lo + min(pos, len - 1)) * L.C + ch] : (ext == 0 ? o0 : ext == 1 ? o1 : o2);
+        h.v[j] = pos >= 0 ? p.x[(size_t)(lo + min(pos, len - 1)) * L.C + ch] : (ext == 0 ? o0 : ext == 1 ? o1 : o2);
     }
-    st[0] = nw[0];
-    if (L.dc > 2) st[1] = nw[1];
-    if (L.dc > 3) st[2] = nw[2];
+    return h;
+}
+__device__ __forceinline__ void hist_put(const PrefillParams& p, int ch, int s, const HistNew& h) {
+    const Layer& L = p.L;
+    uint16_t* st = p.conv_state + ((size_t)s * L.C + ch) * (L.dc - 1);
+    st[0] = h.v[0];
+    if (L.dc > 2) st[1] = h.v[1];
+    if (L.dc > 3) st[2] = h.v[2];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -975,21 +965,62 @@ __device__ __forceinline__ void mfma2_split(const bf8 (&a)[4][2], const bf8& bh,
 // A workgroup's share of its sequence in the window: n chunks, the first being chunk k0 of the
 // sequence (tokens lo + 64 k0 on); chunk k (0-based) of the n has its operands at window slot
 // wk + k. last: the window holds the sequence's last chunk.
-struct SeqGeo { int s, lo, hi, n, k0, wk, last; };
-__device__ __forceinline__ ChunkGeo seq_chunk(const SeqGeo& sg, int k) {
-    ChunkGeo g;
-    g.s = sg.s;
-    g.lo = sg.lo;
-    g.pos0 = (sg.k0 + k) * kChunk;
-    g.t0 = sg.lo + g.pos0;
-    g.len = min(kChunk, sg.hi - g.t0);
-    return g;
+// A chain workgroup's run: the window's chunks a .. a + n - 1, consecutive chunks of one or more
+// consecutive sequences; wk = a - cb, the first one's place in the window; lo, hi: the bounds
+// of the only sequence when n_seq == 1.
+struct ChainRun { int a, n, wk, lo, hi; };
+// Chunk c of a run: its sequence s, first token t0 and the sequence's bounds [lo, hi).
+struct RunChunk {
+    int s, t0, lo, hi;
+    __device__ int len() const { return min(kChunk, hi - t0); }
+    __device__ bool starts() const { return t0 == lo; }               // the sequence's first chunk
+    __device__ bool ends() const { return t0 + kChunk >= hi; }        // its last
+};
+__device__ __forceinline__ RunChunk run_chunk(const PrefillParams& p, const ChainRun& run, int c) {
+    RunChunk r;
+    if (p.single) {
+        r.s = 0;
+        r.lo = run.lo;
+        r.hi = run.hi;
+        r.t0 = run.lo + c * kChunk;
+    } else {
+        const int4 v = p.ws.chunk_rec[c];
+        r.s = v.x;
+        r.t0 = v.y;
+        r.lo = v.z;
+        r.hi = v.w;
+    }
+    return r;
 }
 
 // State role (waves 0 and 1, half = wave): rows 64 half .. 64 half + 63 of the strip, S[mt]
-// the accumulator of row tile mt (rows 64 half + 16 mt + 4 lg4 + r, column li).
-__device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, int half, v4 (&S)[4]) {
-    const int li = lane & 15, lg4 = lane >> 4;
+// the accumulator of row tile mt (rows 64 half + 16 mt + 4 lg4 + r, column li). The state
+// is stored column by column ([d_v][d_k]), so the 4 rows of a lane are a float4. It is loaded
+// at the run's first chunk and at each sequence start (the next sequence's state is loaded a
+// chunk ahead), and stored after each sequence's last chunk and after the run's last.
+__device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t* lds, int lane, const ChainRun& run,
+                                                 int half, int h, int j0) {
+    const int li = lane & 15, lg4 = lane >> 4, n = run.n;
+    auto st_of = [&](int s) {
+        return p.state + ((size_t)s * p.L.h_v + h) * kD * kD + (size_t)(j0 + li) * kD + 64 * half + 4 * lg4;
+    };
+    auto st_load = [&](int s, v4 (&X)[4]) {
+        const float* st = st_of(s);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) X[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
+    };
+    auto st_store = [&](int s, const v4 (&X)[4]) {
+        float* st = st_of(s);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = X[mt];
+    };
+    // Chunks c_k, c_{k+1}, c_{k+2} (clamped to the run's last): each record is loaded two chunks
+    // before the one that decides on it.
+    RunChunk rc = run_chunk(p, run, run.a), rn = run_chunk(p, run, run.a + min(1, n - 1)),
+             rn2 = run_chunk(p, run, run.a + min(2, n - 1));
+    v4 S[4], Sn[4];
+    st_load(rc.s, S);
+    if (n > 1 && rn.starts()) st_load(rn.s, Sn);
     // Lane offsets in a key slot: K of k-steps 2 half + a, K^T of channel tiles 4 half + 2 a + j.
     int koff[2], toff[2];
 #pragma unroll
@@ -1059,9 +1090,22 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
         for (int mt = 0; mt < 4; ++mt) S[mt] *= gam;
         mfma4_split(KT[0], dh[0], dl[0], S);
         mfma4_split(KT[1], dh[1], dl[1], S);
-        if (k + 1 < n) { load_k(q1); hand_and_w(); }
+        if (k + 1 < n) {
+            if (rn.starts()) {                              // chunk c_k ended its sequence
+                st_store(rc.s, S);
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) S[mt] = Sn[mt];
+            }
+            rc = rn;
+            rn = rn2;
+            if (k + 2 < n && rn.starts()) st_load(rn.s, Sn);
+            rn2 = run_chunk(p, run, run.a + min(k + 3, n - 1));
+            load_k(q1);
+            hand_and_w();
+        }
         q = q1;
     }
+    st_store(rc.s, S);
 }
 
 // The strip's v columns, built by the output waves: wave r builds row tile r of V. x rows
@@ -1071,12 +1115,12 @@ __device__ __forceinline__ void chain_state_role(uint8_t* lds, int lane, int n, 
 // (their V rows are zeroed).
 struct XStage { uint32_t w[3]; };
 template <int DC>
-__device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo& sg, int k, int h, int strip, int r,
+__device__ __forceinline__ void stage_load(const PrefillParams& p, const RunChunk& rc, int h, int strip, int r,
                                            int lane, XStage& xs) {
     const Layer& L = p.L;
     const int ch = v_channel(L, h, strip * kStrip + 2 * (lane & 7));
-    const int pos0 = (sg.k0 + k) * kChunk + 16 * r - 3, last = sg.hi - sg.lo - 1;
-    const uint16_t* hist = p.conv_state + ((size_t)sg.s * L.C + ch) * (DC - 1) + (DC - 1);
+    const int pos0 = rc.t0 - rc.lo + 16 * r - 3, last = rc.hi - rc.lo - 1;
+    const uint16_t* hist = p.conv_state + ((size_t)rc.s * L.C + ch) * (DC - 1) + (DC - 1);
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int pos = pos0 + 8 * i + (lane >> 3);        // >= 0 for i > 0
@@ -1084,7 +1128,7 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const SeqGeo&
             const int hp = max(pos, -(DC - 1));             // rows before -(DC-1) feed no output
             xs.w[i] = (uint32_t)hist[hp] | ((uint32_t)hist[hp + (DC - 1)] << 16);
         } else {
-            xs.w[i] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(sg.lo + min(pos, last)) * L.C + ch);
+            xs.w[i] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(rc.lo + min(pos, last)) * L.C + ch);
         }
     }
 }
@@ -1196,9 +1240,9 @@ struct OutQ {
 struct OutM {
     bf8 mf[2][2];
 };
-__device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const SeqGeo& sg, int k, int h, int src,
+__device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const ChainRun& run, int k, int h, int src,
                                                  int r, int lane, OutQ& x) {
-    const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
+    const size_t c = (size_t)(run.wk + min(k, run.n - 1));
     const uint16_t* Qf = p.ws.Qf + (c * p.L.h_k + src) * kFragW;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
@@ -1206,9 +1250,9 @@ __device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const S
         for (int pl = 0; pl < 2; ++pl) x.qf[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(r, ks, 4, pl, lane));
     x.g = *reinterpret_cast<const v4*>(p.ws.G + (c * p.L.h_v + h) * 2 * kChunk + kChunk + 16 * r + 4 * (lane >> 4));
 }
-__device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const SeqGeo& sg, int k, int h, int r,
+__device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const ChainRun& run, int k, int h, int r,
                                                  int lane, OutM& x) {
-    const size_t c = (size_t)(sg.wk + min(k, sg.n - 1));
+    const size_t c = (size_t)(run.wk + min(k, run.n - 1));
     const uint8_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragMBytes;
     // Row tiles 0 and 1 end before token 32, so their k-step 1 of M (tokens 32..63) is zero.
 #pragma unroll
@@ -1220,7 +1264,7 @@ __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const S
 
 template <int DC, bool SILU>
 __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_t* lds, int lane, int r,
-                                                  const SeqGeo& sg, int h, int src, int strip) {
+                                                  const ChainRun& run, int h, int src, int strip) {
     const Layer& L = p.L;
     const int li = lane & 15, lg4 = lane >> 4, j0 = strip * kStrip;
     float cw[DC];                                           // conv weights of the lane's v channel
@@ -1229,30 +1273,33 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 #pragma unroll
         for (int i = 0; i < DC; ++i) cw[i] = bf16_to_f32(wp[i]);
     }
+    const int n = run.n;
+    // Chunks c_k, c_{k+1}, c_{k+2} of the run (clamped to its last).
+    RunChunk r0 = run_chunk(p, run, run.a), r1 = run_chunk(p, run, run.a + min(1, n - 1)), r2 = run_chunk(p, run, run.a + min(2, n - 1));
     XStage xs;
-    stage_load<DC>(p, sg, 0, h, strip, r, lane, xs);
-    stage_conv<DC, SILU>(lds, xs, r, lane, cw, seq_chunk(sg, 0).len);
-    if (sg.n > 1) stage_load<DC>(p, sg, 1, h, strip, r, lane, xs);
+    stage_load<DC>(p, r0, h, strip, r, lane, xs);
+    stage_conv<DC, SILU>(lds, xs, r, lane, cw, r0.len());
+    if (n > 1) stage_load<DC>(p, r1, h, strip, r, lane, xs);
     OutQ q0, q1;
     OutM m0, m1;
-    chain_out_load_q(p, sg, 0, h, src, r, lane, q0);
-    chain_out_load_m(p, sg, 0, h, r, lane, m0);
-    chain_out_load_q(p, sg, 1, h, src, r, lane, q1);
-    chain_out_load_m(p, sg, 1, h, r, lane, m1);
+    chain_out_load_q(p, run, 0, h, src, r, lane, q0);
+    chain_out_load_m(p, run, 0, h, r, lane, m0);
+    chain_out_load_q(p, run, 1, h, src, r, lane, q1);
+    chain_out_load_m(p, run, 1, h, r, lane, m1);
     const lds_u8* hbase = lane_at(lds, kOffH + lane * 16);
     const size_t row = (size_t)L.h_v * kD;
     v4 o;
     // A window buffer for o starts at the window's first token.
     int tw0 = 0, tw1;
     if (p.o_win) window_tokens(p, tw0, tw1);
-    auto store = [&](int k) {
-        const ChunkGeo g = seq_chunk(sg, k);
+    auto store = [&](const RunChunk& g) {
         const size_t ob = ((size_t)g.t0 * L.h_v + h) * kD + j0 + li;
         const size_t obw = ((size_t)(g.t0 - tw0) * L.h_v + h) * kD + j0 + li;
+        const int len = g.len();
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int t = 16 * r + 4 * lg4 + i;
-            if (t < g.len) {
+            if (t < len) {
                 if (p.o) p.o[obw + (size_t)t * row] = o[i];
                 if (p.o_bf16) p.o_bf16[ob + (size_t)t * row] = f32_to_bf16(o[i]);
             }
@@ -1275,11 +1322,11 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * Q.g[i];
-        if (k + 1 < sg.n) {                                 // row tile r of chunk c_{k+1}'s V
-            stage_conv<DC, SILU>(lds, xs, r, lane, cw, seq_chunk(sg, k + 1).len);
-            if (k + 2 < sg.n) stage_load<DC>(p, sg, k + 2, h, strip, r, lane, xs);
+        if (k + 1 < n) {                                    // row tile r of chunk c_{k+1}'s V
+            stage_conv<DC, SILU>(lds, xs, r, lane, cw, r1.len());
+            if (k + 2 < n) stage_load<DC>(p, r2, h, strip, r, lane, xs);
         }
-        if (k + 2 < sg.n) chain_out_load_q(p, sg, k + 2, h, src, r, lane, Q);
+        if (k + 2 < n) chain_out_load_q(p, run, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
         // M D: tokens 0-31 for every row tile, tokens 32-63 for row tiles 2 and 3 only.
         bf8 db[2][2];
@@ -1302,13 +1349,16 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = a0[i] + a1[i] + a2[i];
-        store(k);
-        if (k + 2 < sg.n) chain_out_load_m(p, sg, k + 2, h, r, lane, M);
+        store(r0);
+        if (k + 2 < n) chain_out_load_m(p, run, k + 2, h, r, lane, M);
+        r0 = r1;
+        r1 = r2;
+        r2 = run_chunk(p, run, run.a + min(k + 3, n - 1));
     };
     lds_barrier();                                          // alpha_0
-    for (int k = 0; k < sg.n; k += 2) {
+    for (int k = 0; k < n; k += 2) {
         step(k, q0, m0);
-        if (k + 1 < sg.n) step(k + 1, q1, m1);
+        if (k + 1 < n) step(k + 1, q1, m1);
     }
 }
 
@@ -1316,19 +1366,20 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 // chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads and
 // loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and the 6
 // nonzero fragments of T') into the value slot and waits for the copies before the barrier.
-// In the window that holds the sequence's last chunk it also writes, in alpha_0, the new
-// rolling conv history of the workgroup's channels: its share of the sequence's q/k channels
-// (the h_v * 8 workgroups of a sequence split them into contiguous ranges; the chunk kernel has
-// read their old history) and the strip's 16 v channels (whose old history the output waves
-// read before the first window's alpha_0). Nothing else in this kernel writes conv_state.
-__device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const SeqGeo& sg,
+// In alpha_k of a sequence's last chunk it also writes the new rolling conv history of the
+// workgroup's channels: its share of the sequence's q/k channels (the h_v * 8 workgroups that
+// run the sequence split them into contiguous ranges; the chunk kernel has read their old
+// history) and the strip's 16 v channels (whose old history the output waves have read into
+// the V of the sequence's first chunk by then, at the latest in beta of the chunk before it).
+// Nothing else in this kernel writes conv_state.
+__device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const ChainRun& run,
                                                 int h, int strip, int src) {
     typedef __attribute__((address_space(3))) u4x lds_u4;
     const Layer& L = p.L;
     v4 eg;
     u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
     auto load = [&](int k) {
-        const size_t chh = (size_t)(sg.wk + min(k, sg.n - 1)) * L.h_v + h;
+        const size_t chh = (size_t)(run.wk + min(k, run.n - 1)) * L.h_v + h;
         eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
         const uint8_t* tsrc = p.ws.Tf + chh * kTriFragBytes;
 #pragma unroll
@@ -1344,7 +1395,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
     };
     auto copy_keys = [&](int k) {
-        const uint8_t* g = p.ws.Kp + ((size_t)(sg.wk + k) * L.h_k + src) * kKSlot + lane * 16;
+        const uint8_t* g = p.ws.Kp + ((size_t)(run.wk + k) * L.h_k + src) * kKSlot + lane * 16;
         lds_u8* d = (lds_u8*)lds + kOffK + (k % kKSlots) * kKSlot;
 #pragma unroll
         for (int i = 0; i < kKSlot / kPlane; ++i) __builtin_amdgcn_global_load_lds(g + i * kPlane, d + i * kPlane, 16, 0, 0);
@@ -1359,20 +1410,30 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         __asm__ volatile("" ::: "memory");
     };
 
+    const int n = run.n;
+    // The lane's channels of a commit: q/k channel cq (at most 64 per workgroup, since
+    // h_k <= h_v) and, in lanes 0-15, v channel cv.
+    const int ng = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + ng - 1) / ng;
+    const bool has_q = lane < per && gi * per + lane < cqk, has_v = lane < kStrip;
+    const int cq = has_q ? gi * per + lane : 0, cv = v_channel(L, h, strip * kStrip + (lane & (kStrip - 1)));
+    RunChunk rc = run_chunk(p, run, run.a);                      // chunk c_k
     copy_keys(0);
     load(0);
     produce();
     wait_barrier();                                         // alpha_0
-    if (sg.last) {
-        const int G = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + G - 1) / G;
-        const int ch_hi = min(cqk, (gi + 1) * per);
-        for (int c = gi * per + lane; c < ch_hi; c += kWave) commit_history(p, c, sg.lo, sg.hi - sg.lo, sg.s);
-        if (lane < kStrip) commit_history(p, v_channel(L, h, strip * kStrip + lane), sg.lo, sg.hi - sg.lo, sg.s);
-    }
-    for (int k = 0; k < sg.n; ++k) {
+    for (int k = 0; k < n; ++k) {
+        // After a sequence's last chunk, its new histories: loaded before this chunk's copies
+        // are issued, stored in beta_k.
+        const RunChunk cur = rc;
+        HistNew hq, hv;
+        if (cur.ends()) {
+            hq = hist_fetch(p, cq, cur.lo, cur.hi - cur.lo, cur.s);
+            hv = hist_fetch(p, cv, cur.lo, cur.hi - cur.lo, cur.s);
+        }
+        if (k + 1 < n) rc = run_chunk(p, run, run.a + k + 1);
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
         // in beta_{k-2}; they are read from alpha_{k+1} on.
-        if (k + 1 < sg.n) {
+        if (k + 1 < n) {
             copy_keys(k + 1);
             load(k + 1);
         }
@@ -1381,7 +1442,11 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (k + 1 < sg.n) produce();                        // waits for the loads, and so the copies
+        if (cur.ends()) {
+            if (has_q) hist_put(p, cq, cur.s, hq);
+            if (has_v) hist_put(p, cv, cur.s, hv);
+        }
+        if (k + 1 < n) produce();                           // waits for the loads, and so the copies
         wait_barrier();                                     // alpha_{k+1}: the copies have landed
     }
 }
@@ -1391,56 +1456,53 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     __shared__ __align__(16) uint8_t lds[kChainLds];
 
     const Layer& L = p.L;
-    // XCD-aware mapping: the 8 strips of one (sequence, head) pair share an XCD, so its L2
-    // serves the pair's chunk operands to all of them.
-    // Slot j of a window takes the j-th non-empty sequence from the one of the window's first
-    // chunk on: a window of W chunks touches at most W sequences.
+    // XCD-aware mapping: the 8 strips of one (head, group) pair share an XCD, so its L2 serves
+    // the chunk operands to all of them. Group g of G runs the window's chunks from the g-th of
+    // G near-equal shares on, each share's start moved to the next sequence start (group 0
+    // starts at the window's first chunk, continuing a sequence begun in an earlier window).
     const int lin = blockIdx.x, xcd = lin & 7, kq = lin >> 3;
     const int strip = kq & (kStrips - 1);
     const int pair = (kq / kStrips) * 8 + xcd;
-    if (pair >= min(p.n_seq, p.W) * L.h_v) return;
-    const int h = pair % L.h_v, src = src_of(L, h);
-    int s = 0;
-    if (!p.single) {
-        if (p.cb >= p.ws.chunk_off[p.n_seq]) return;        // past the last chunk
-        const int r = p.ws.seq_rank[p.ws.chunk_rec[p.cb].x] + pair / L.h_v;
-        if (r >= p.ws.seq_rank[p.n_seq]) return;
-        s = p.ws.seq_list[r];                                // its chunks may start past the window
+    if (pair >= p.G * L.h_v) return;
+    const int h = pair % L.h_v, grp = pair / L.h_v, src = src_of(L, h);
+    int nc;
+    if (p.single) {
+        int lo, hi;
+        seq_bounds(p, 0, lo, hi);
+        nc = (hi - lo + kChunk - 1) / kChunk;
+    } else {
+        nc = p.ws.chunk_off[p.n_seq];
     }
-    SeqGeo sg;
-    sg.s = s;
-    seq_bounds(p, s, sg.lo, sg.hi);
-    // the sequence's chunks c0 .. c_end - 1, clipped to the window
-    const int c0 = p.single ? 0 : p.ws.chunk_off[s];
-    const int c_end = p.single ? (sg.hi - sg.lo + kChunk - 1) / kChunk : p.ws.chunk_off[s + 1];
-    const int lo_c = max(c0, p.cb), hi_c = min(c_end, p.cb + p.W);
-    sg.n = hi_c - lo_c;
-    if (sg.n <= 0) return;
-    sg.k0 = lo_c - c0;
-    sg.wk = lo_c - p.cb;
-    sg.last = hi_c == c_end;
+    const int nw = min(p.W, nc - p.cb);                     // the window's chunks
+    if (nw <= 0) return;
+    auto share_start = [&](int g) {
+        if (g == 0) return p.cb;
+        if (g >= p.G) return p.cb + nw;
+        const int x = p.cb + (int)((long long)g * nw / p.G);
+        const int4 r = p.ws.chunk_rec[x];
+        return r.y == r.z ? x : min(p.ws.chunk_off[r.x + 1], p.cb + nw);
+    };
+    ChainRun run;
+    run.lo = run.hi = 0;
+    if (p.single) seq_bounds(p, 0, run.lo, run.hi);
+    run.a = share_start(grp);
+    run.n = share_start(grp + 1) - run.a;
+    if (run.n <= 0) return;
+    run.wk = run.a - p.cb;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int lane = threadIdx.x & (kWave - 1), li = lane & 15, lg4 = lane >> 4;
+    const int lane = threadIdx.x & (kWave - 1);
     const int j0 = strip * kStrip;
 
     if (w <= 1) {
-        // State rows 64 w + 16 mt + 4 lg4 + i (k index), column j0 + li (v index); the state is
-        // stored column by column ([d_v][d_k]), so the 4 rows are a float4.
-        float* st = p.state + ((size_t)s * L.h_v + h) * kD * kD + (size_t)(j0 + li) * kD + 64 * w + 4 * lg4;
-        v4 S[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) S[mt] = *reinterpret_cast<const v4*>(st + 16 * mt);
-        chain_state_role(lds, lane, sg.n, w, S);
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) *reinterpret_cast<v4*>(st + 16 * mt) = S[mt];
+        chain_state_role(p, lds, lane, run, w, h, j0);
     } else if (w == 4) {
-        chain_d_role(lds, lane, sg.n);
+        chain_d_role(lds, lane, run.n);
     } else if (w == 5) {
-        chain_feed_role(p, lds, lane, sg, h, strip, src);
+        chain_feed_role(p, lds, lane, run, h, strip, src);
     } else {
         // Row tiles 0, 1 on waves 2, 3 and 3, 2 on waves 6, 7: each SIMD's pair runs 3 of M D's
         // 6 k-steps (2-4% faster than tiles 2, 3 on waves 6, 7).
-        chain_output_role<DC, SILU>(p, lds, lane, w < 4 ? w - 2 : 9 - w, sg, h, src, strip);
+        chain_output_role<DC, SILU>(p, lds, lane, w < 4 ? w - 2 : 9 - w, run, h, src, strip);
     }
 }
 
@@ -1484,20 +1546,21 @@ static size_t prefill_ws_bytes(const ix_gdn_cfg* cfg, int n_seq, int T, size_t W
     return b;
 }
 
-// The default workspace: windows of at most kDefaultWindow chunks (8,192 tokens). The chunk
-// kernel and the chain never overlap, so a long batch in such windows takes about as long as in
-// one window, and the workspace stops growing with total_T (only the chunk tables do, 16 bytes
-// per chunk).
-constexpr size_t kDefaultWindow = 128;
+// Windows of at most kMaxWindow chunks (5,120 tokens): the chunk operands of one window (146 MiB
+// at the Qwen3-Next head layout) then stay in MI355X's 256 MB Infinity Cache between the chunk
+// kernel writing them and the chain reading them (configuration 4: 1.60 ms in 80-chunk windows,
+// 1.80 ms in 112-chunk ones). The default workspace holds such a window, so it stops growing
+// with total_T (only the chunk tables do, 16 bytes per chunk).
+constexpr size_t kMaxWindow = 80;
 
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kDefaultWindow), false);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kMaxWindow), false);
 }
 
 extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kDefaultWindow), true);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kMaxWindow), true);
 }
 
 extern "C" size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T,
@@ -1542,17 +1605,17 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     const bool gwin = gate && !o;
     const size_t NCmax = max_chunks(n_seq, total_T);
     if (workspace_bytes < prefill_ws_bytes(cfg, n_seq, total_T, 1, gwin)) return hipErrorInvalidValue;
-    size_t W = 1, W_hi = NCmax;
+    size_t W = 1, W_hi = std::min(NCmax, kMaxWindow);
     while (W < W_hi) {
         const size_t mid = (W + W_hi + 1) / 2;
         if (prefill_ws_bytes(cfg, n_seq, total_T, mid, gwin) <= workspace_bytes) W = mid;
         else W_hi = mid - 1;
     }
+    W = (NCmax + (NCmax + W - 1) / W - 1) / ((NCmax + W - 1) / W);   // windows of equal size
     size_t off[kWsSections];
     const size_t need = ws_layout(cfg, n_seq, total_T, W, off);
     const long long NC = (long long)NCmax;
-    const long long pairs = (long long)n_seq * cfg->h_v;
-    if (NC * cfg->h_v > 0x7fffffffLL || ((pairs + 7) / 8) * 8 * kStrips > 0x7fffffffLL) return hipErrorInvalidValue;
+    if (NC * cfg->h_v > 0x7fffffffLL) return hipErrorInvalidValue;
     const long long rows = (long long)total_T * cfg->h_v;
     if (gate && (rows + 3) / 4 > 0x7fffffffLL) return hipErrorInvalidValue;
 
@@ -1566,9 +1629,14 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     p.o_win = gwin;
     if (gwin) p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + need);   // the norm's input
 
+    // Chain workgroups: (v head, strip, group), G groups splitting each window's chunks at
+    // sequence starts; one group while the h_v * 8 (head, strip) runs fill every CU.
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess) (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    p.G = p.single ? 1 : std::max(1, std::min(n_seq, cus / (cfg->h_v * kStrips)));
+
     if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
-    // chain workgroups: (sequence slot, v head, strip), at most min(n_seq, W) slots per window
-    const long long groups = ((long long)std::min((size_t)n_seq, W) * cfg->h_v + 7) / 8;
+    const long long groups = ((long long)p.G * cfg->h_v + 7) / 8;
     const dim3 cgrid((unsigned)(groups * 8 * kStrips)), cblock(kChainWaves * kWave);
     const bool silu = cfg->conv_act == IX_GDN_ACT_SILU;
     const OutGate og = make_out_gate(gate);

@@ -161,21 +161,22 @@ hipError_t ix_gdn_decode_gated(const ix_gdn_cfg* cfg, int B, const uint16_t* x, 
                                hipStream_t s IX_GDN_DEFAULT_STREAM);
 
 /* Bytes of device workspace for ix_gdn_prefill over n_seq sequences and total_T tokens in
- * windows of at most 128 chunks of 64 tokens (about 2 MiB per chunk at the Qwen3-Next head
- * layout: 270 MiB at most, plus 16 bytes per chunk of tables). A batch of up to 8,192 tokens
- * runs as one window; longer ones take about as long in windows as in one. */
+ * windows of at most 80 chunks of 64 tokens (1.83 MiB per chunk at the Qwen3-Next head layout:
+ * 146 MiB at most, plus 16 bytes per chunk of tables). A batch of up to 5,120 tokens runs as
+ * one window. Windows are never longer, whatever the workspace: a window's chunk operands then
+ * stay in the GPU's Infinity Cache between the two kernels that write and read them. */
 size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T);
 
 /* Bytes of device workspace for ix_gdn_prefill (gated = 0) or ix_gdn_prefill_gated (gated = 1)
  * in windows of window_chunks 64-token chunks: the chunk tables (16 bytes per chunk) plus the
  * chunk operands of one window. Any workspace of at least the size for window_chunks = 1 works;
- * the prefill then runs in windows of as many chunks as the workspace holds, one after the
- * other, with results identical to the one-window run. 0 for invalid arguments. Addition; no
+ * the prefill then runs in equal windows of at most as many chunks as the workspace holds
+ * (and at most 80), one after the other, with results identical to the one-window run. 0 for invalid arguments. Addition; no
  * reference counterpart (for callers that bound device memory independently of total_T). */
 size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T, int window_chunks,
                                             int gated);
 
-/* Chunked (WY-form, chunk 64) prefill of n_seq packed sequences, the same math as
+/* Chunked (64-token chunks) prefill of n_seq packed sequences, the same math as
  * total_T applications of ix_gdn_decode:
  *   cu_seqlens [n_seq+1] int32 device offsets (cu_seqlens[0] = 0, non-decreasing)
  *   x [total_T][C] bf16; a, b [total_T][h_v] bf16

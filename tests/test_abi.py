@@ -132,15 +132,15 @@ def test_prefill_validation_without_launch():
     assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 100, 1, gated=True) > small
     # the window operands do not grow with tokens; only the chunk tables do (16 bytes a chunk)
     assert bx.ix_gdn_prefill_window_workspace_size(cfg, 2, 64 * 1000, 1) - small <= 1000 * 16 + 512
-    # the default size: windows of at most 128 chunks
-    at128 = bx.ix_gdn_prefill_window_workspace_size(cfg, 1, 64 * 127, 128)
-    assert bx.ix_gdn_prefill_workspace_size(cfg, 1, 64 * 127) == at128      # one window
+    # the default size: windows of at most 80 chunks
+    at80 = bx.ix_gdn_prefill_window_workspace_size(cfg, 1, 64 * 79, 80)
+    assert bx.ix_gdn_prefill_workspace_size(cfg, 1, 64 * 79) == at80        # one window
     for T in (64 * 1000, 64 * 100000):
         big = bx.ix_gdn_prefill_workspace_size(cfg, 1, T)
-        assert big == bx.ix_gdn_prefill_window_workspace_size(cfg, 1, T, 128)
-        assert big - at128 <= (T // 64) * 16 + 512
+        assert big == bx.ix_gdn_prefill_window_workspace_size(cfg, 1, T, 80)
+        assert big - at80 <= (T // 64) * 16 + 512
         assert bx.ix_gdn_prefill_gated_workspace_size(cfg, 1, T) == \
-            bx.ix_gdn_prefill_window_workspace_size(cfg, 1, T, 128, gated=True)
+            bx.ix_gdn_prefill_window_workspace_size(cfg, 1, T, 80, gated=True)
     p = ctypes.c_void_p(1 << 20)
 
     def call(n_seq, T, ws, nbytes, c=cfg):
