@@ -29,9 +29,10 @@
 //                  (diagonal blocks by substitution, the rest by block forward substitution)
 //                  and T' = T diag(beta); it writes the chain's operands in their final
 //                  layouts: key planes, Q, M and T' as split-bf16 MFMA fragments, decay factors
-//   chain_kernel   per (sequence, v head, 16-column state strip): walks the window's chunks of
-//                  its sequence in order, two phases per chunk (roles below), and writes the
-//                  outputs, the state and, with the sequence's last chunk, the new conv history
+//   chain_kernel   per (v head, 16-column state strip, group of sequences): walks the window's
+//                  chunks of its sequences in order, across sequence boundaries, two phases per
+//                  chunk (roles below), and writes the outputs, the states and, after each
+//                  sequence's last chunk, its new conv history
 //   out_gate_*     (ix_gdn_prefill_gated) the gated RMS output norm of every (token, head) row
 // Every dense product runs on split-bf16 MFMA (three bf16 products per fp32 product, ~2^-16
 // relative error); only the 16 x 16 diagonal blocks of T are inverted in fp32 arithmetic.
@@ -811,11 +812,14 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 }
 
 // ---------------------------------------------------------------------------------------
-// chain: one workgroup per (sequence, v head, 16-column state strip), 8 waves
+// chain: one workgroup per (v head, 16-column state strip, group), 8 waves
 // ---------------------------------------------------------------------------------------
 // Columns of the state are independent, so a head's chain splits into 8 strips of 16
-// columns, and each strip's workgroup walks its sequence's chunks in order. For chunk c_k,
-// with S_k the strip at its start,
+// columns, and each strip's workgroup walks a run of the window's chunks in order: all of them
+// (one group, when the h_v * 8 strips fill the CUs) or a share ending at a sequence start. At
+// a sequence boundary the state waves store the finished state and continue with the next
+// sequence's (loaded a chunk ahead); the other roles only follow each chunk's record. For
+// chunk c_k, with S_k the strip at its start,
 //     W_k     = K_k S_k                                            (64 x 16)
 //     D_k     = T'_k (V_k - diag(Gam_k) W_k)
 //     S_{k+1} = gam_k S_k + K_k^T Dg_k,  Dg_k = diag(E_k) D_k,  gam_k = Gam_k[63]
@@ -962,9 +966,6 @@ __device__ __forceinline__ void mfma2_split(const bf8 (&a)[4][2], const bf8& bh,
 }
 
 
-// A workgroup's share of its sequence in the window: n chunks, the first being chunk k0 of the
-// sequence (tokens lo + 64 k0 on); chunk k (0-based) of the n has its operands at window slot
-// wk + k. last: the window holds the sequence's last chunk.
 // A chain workgroup's run: the window's chunks a .. a + n - 1, consecutive chunks of one or more
 // consecutive sequences; wk = a - cb, the first one's place in the window; lo, hi: the bounds
 // of the only sequence when n_seq == 1.
