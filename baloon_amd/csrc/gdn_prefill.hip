@@ -830,19 +830,20 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 //            S_k = gam S_{k-1} + K_{k-1}^T Dg_{k-1} on their rows (K^T read in beta_{k-1}),
 //            hand S_k over split and form their half of W_k (the sum over their 64 channels,
 //            K read as the products need it);
-//   beta_k   the D wave (4) adds the halves and forms D_k, handing over D_k (fp32) for the
-//            outputs and Dg_k (split) with gam_k for the state waves.
+//   beta_k   the D wave (4) and the feed wave (5) add the halves and form D_k, row tiles 0, 1
+//            and 2, 3, handing over D_k (fp32) for the outputs and Dg_k (split) with gam_k
+//            for the state waves.
 // Products take their k index in accumulator row order (kperm), so an accumulator tile pair,
-// split to bf16 hi/lo, is the next product's B operand as it stands. The D wave reads chunk
-// c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
+// split to bf16 hi/lo, is the next product's B operand as it stands. The D and feed waves read
+// chunk c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
 // The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
 // alpha_{k+1}, with Q, M and Gam loaded from the workspace two chunks ahead; in beta_k each
 // also builds row tile r of chunk c_{k+1}'s V (the conv of the strip's v channels) into the
 // value slot. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
 // with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
-// until beta_{k-2}), and in beta_k writes chunk c_{k+1}'s decay factors and T' fragments into
-// the value slot from registers loaded in alpha_k; it also writes the new rolling conv history
-// of the workgroup's channels.
+// until beta_{k-2}), and writes the new rolling conv history of the workgroup's channels; the
+// D wave writes chunk c_{k+1}'s decay factors and T' fragments into the value slot in beta_k
+// from registers loaded in alpha_k.
 // A last alpha_n finishes S_n (state waves) and O_{n-1} (output waves).
 // Waves w and w + 4 share a SIMD: the state waves' partners (the D wave, the feed wave) only
 // read and copy in alpha, where the state waves work.
@@ -1167,62 +1168,92 @@ __device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int r
     __asm__ volatile("" ::: "memory");
 }
 
-// D role (wave 4): per chunk, D = T' (V - diag(Gam) (W_0 + W_1)) from the state waves' halves of
-// W, with V, the decay factors and T' read from the value slot in the preceding alpha.
-__device__ __forceinline__ void chain_d_role(uint8_t* lds, int lane, int n) {
-    const int lg4 = lane >> 4;
+// D = T' X, X = V - diag(Gam) (W_0 + W_1), from the state waves' halves of W, with V, the decay
+// factors and T' read in the preceding alpha; row tiles 0, 1 (T' (0, 0), (1, 0), tokens 0-31)
+// by the D wave, row tiles 2, 3 (T' (2, 0), (3, 0), (2, 1), (3, 1)) by the feed wave, each
+// handing over its tiles of D (fp32, for the outputs) and its k-step of Dg = diag(E) D (split,
+// for the state waves).
+// X row tiles mt .. mt + NT - 1 of one chunk.
+template <int NT>
+__device__ __forceinline__ void d_x(const lds_u8* wb, const v4* V, const v4* Gm, int mt0, v4* X) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int mt = mt0 + t;
+        const v4 w0 = *(const lds_v4*)(wb + mt * kPlane), w1 = *(const lds_v4*)(wb + (4 + mt) * kPlane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) X[t][e] = fmaf(-Gm[t][e], w0[e] + w1[e], V[t][e]);
+    }
+}
+// Dg k-step ks (row tiles 2 ks, 2 ks + 1) split, and the two D row tiles in fp32.
+__device__ __forceinline__ void d_hand(uint8_t* lds, int lane, int ks, const v4* E, const v4* D) {
+    bf8 dh, dl;
+    split_tiles(E[0] * D[0], E[1] * D[1], dh, dl);
+    lds_u8* gb = (lds_u8*)lds + kOffG + lane * 16;
+    *(lds_bf8*)(gb + (2 * ks) * kPlane) = dh;
+    *(lds_bf8*)(gb + (2 * ks + 1) * kPlane) = dl;
+    lds_u8* hb = (lds_u8*)lds + kOffH + kHandS + lane * 16;
+    *(lds_v4*)(hb + (2 * ks) * kPlane) = D[0];
+    *(lds_v4*)(hb + (2 * ks + 1) * kPlane) = D[1];
+}
+
+// D role (wave 4): row tiles 0 and 1 of D, and gam. In alpha_k it also loads chunk c_{k+1}'s
+// decay factors and T' from the workspace, and writes them (E, then Gam, and the 6 nonzero
+// fragments of T') into the value slot in beta_k, once the feed wave has read chunk c_k's.
+__device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* lds, int lane, const ChainRun& run,
+                                             int h) {
+    typedef __attribute__((address_space(3))) u4x lds_u4;
+    const int lg4 = lane >> 4, n = run.n;
+    v4 eg;
+    u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
+    auto load = [&](int k) {
+        const size_t chh = (size_t)(run.wk + min(k, run.n - 1)) * p.L.h_v + h;
+        eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
+        const uint8_t* tsrc = p.ws.Tf + chh * kTriFragBytes;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) {
+            const int e = i >> 1, mt = e < 4 ? e : e - 2, ks = e < 4 ? 0 : 1;    // slot entry e, plane i & 1
+            tf[i] = load_tri_frag(tsrc, mt, ks, i & 1, lane);
+        }
+    };
+    auto produce = [&]() {
+        if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + 4 * kPlane + lane * 16) = eg;
+        lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
+#pragma unroll
+        for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
+    };
+    load(0);
+    produce();
     const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
     const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
     const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
-    lds_u8* hb = lane_at(lds, kOffH + kHandS + lane * 16);
-    lds_u8* gb = lane_at(lds, kOffG + lane * 16);
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // alpha_k: chunk c_k in the value slot
-        v4 V[4], E[4], Gm[4];
+        if (k + 1 < n) load(k + 1);
+        v4 V[2], E[2], Gm[2];
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < 2; ++mt) {
             V[mt] = *(const lds_v4*)(vb + mt * kPlane);
             E[mt] = *(const lds_v4*)(eb + mt * 64);
             Gm[mt] = *(const lds_v4*)(eb + 4 * kChunk + mt * 64);
         }
         const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kPlane +
                                                                             4 * kChunk + 4 * (kChunk - 1));
-        bf8 F0[4][2], F1[4][2];                             // T' (mt, 0), mt = 0..3; T' (2, 1), (3, 1)
+        bf8 F0[4][2];                                       // T' (mt, 0), mt = 0, 1
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl) {
+        for (int pl = 0; pl < 2; ++pl)
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt) F0[mt][pl] = *(const lds_bf8*)(fb + (2 * mt + pl) * kPlane);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) F1[j][pl] = *(const lds_bf8*)(fb + (2 * (4 + j) + pl) * kPlane);
-        }
+            for (int mt = 0; mt < 2; ++mt) F0[mt][pl] = *(const lds_bf8*)(fb + (2 * mt + pl) * kPlane);
         lds_barrier();                                      // beta_k: both halves of W_k handed over
-        v4 X[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-            const v4 w0 = *(const lds_v4*)(wb + mt * kPlane), w1 = *(const lds_v4*)(wb + (4 + mt) * kPlane);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) X[mt][e] = fmaf(-Gm[mt][e], w0[e] + w1[e], V[mt][e]);
-        }
-        bf8 xh[2], xl[2];
-        split_tiles(X[0], X[1], xh[0], xl[0]);
-        split_tiles(X[2], X[3], xh[1], xl[1]);
-        v4 D[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) D[m] = v4{0.f, 0.f, 0.f, 0.f};
-        mfma4_split(F0, xh[0], xl[0], D);                   // tokens 0-31 for every row tile
-        mfma2_split(F1, xh[1], xl[1], D + 2);               // tokens 32-63 for row tiles 2, 3
-        bf8 dh[2], dl[2];
-        split_tiles(E[0] * D[0], E[1] * D[1], dh[0], dl[0]);
-        split_tiles(E[2] * D[2], E[3] * D[3], dh[1], dl[1]);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            *(lds_bf8*)(gb + (2 * ks) * kPlane) = dh[ks];
-            *(lds_bf8*)(gb + (2 * ks + 1) * kPlane) = dl[ks];
-        }
+        v4 X[2];
+        d_x<2>(wb, V, Gm, 0, X);
+        bf8 xh, xl;
+        split_tiles(X[0], X[1], xh, xl);
+        v4 D[2] = {v4{0.f, 0.f, 0.f, 0.f}, v4{0.f, 0.f, 0.f, 0.f}};
+        mfma2_split(F0, xh, xl, D);                         // tokens 0-31
+        d_hand(lds, lane, 0, E, D);
         if (lane == 0) *(__attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane) = gam;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) *(lds_v4*)(hb + m * kPlane) = D[m];
+        if (k + 1 < n) produce();
     }
     lds_barrier();                                          // alpha_n
 }
@@ -1365,9 +1396,8 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 
 // Feed role (wave 5). In alpha_k it starts copying chunk c_{k+1}'s key planes (written by the
 // chunk kernel in this layout) into key slot (k+1) mod 3 with direct global-to-LDS loads and
-// loads chunk c_{k+1}'s decay factors and T'; in beta_k it writes those (E, then Gam, and the 6
-// nonzero fragments of T') into the value slot and waits for the copies before the barrier.
-// In alpha_k of a sequence's last chunk it also writes the new rolling conv history of the
+// reads what row tiles 2 and 3 of D_k need; in beta_k it forms them and waits for the copies
+// before the barrier. After a sequence's last chunk it also writes the new rolling conv history of the
 // workgroup's channels: its share of the sequence's q/k channels (the h_v * 8 workgroups that
 // run the sequence split them into contiguous ranges; the chunk kernel has read their old
 // history) and the strip's 16 v channels (whose old history the output waves have read into
@@ -1375,26 +1405,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 // Nothing else in this kernel writes conv_state.
 __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t* lds, int lane, const ChainRun& run,
                                                 int h, int strip, int src) {
-    typedef __attribute__((address_space(3))) u4x lds_u4;
     const Layer& L = p.L;
-    v4 eg;
-    u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
-    auto load = [&](int k) {
-        const size_t chh = (size_t)(run.wk + min(k, run.n - 1)) * L.h_v + h;
-        eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
-        const uint8_t* tsrc = p.ws.Tf + chh * kTriFragBytes;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const int e = i >> 1, mt = e < 4 ? e : e - 2, ks = e < 4 ? 0 : 1;    // slot entry e, plane i & 1
-            tf[i] = load_tri_frag(tsrc, mt, ks, i & 1, lane);
-        }
-    };
-    auto produce = [&]() {
-        if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + 4 * kPlane + lane * 16) = eg;
-        lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
-    };
     auto copy_keys = [&](int k) {
         const uint8_t* g = p.ws.Kp + ((size_t)(run.wk + k) * L.h_k + src) * kKSlot + lane * 16;
         lds_u8* d = (lds_u8*)lds + kOffK + (k % kKSlots) * kKSlot;
@@ -1419,10 +1430,31 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     const int cq = has_q ? gi * per + lane : 0, cv = v_channel(L, h, strip * kStrip + (lane & (kStrip - 1)));
     RunChunk rc = run_chunk(p, run, run.a);                      // chunk c_k
     copy_keys(0);
-    load(0);
-    produce();
     wait_barrier();                                         // alpha_0
+    const int lg4 = lane >> 4;
+    const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
+    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
+    const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
     for (int k = 0; k < n; ++k) {
+        // Row tiles 2, 3 of D_k: V, the decay factors and T' of chunk c_k read in alpha_k (T'
+        // from this wave's registers, before the next chunk's loads replace them).
+        v4 V[4], Gm[4], E[2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+            V[mt] = *(const lds_v4*)(vb + mt * kPlane);
+            Gm[mt] = *(const lds_v4*)(eb + 4 * kChunk + mt * 64);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) E[t] = *(const lds_v4*)(eb + (2 + t) * 64);
+        bf8 F0[4][2], F1[4][2];                             // T' (2, 0), (3, 0); T' (2, 1), (3, 1)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                F0[t][pl] = *(const lds_bf8*)(fb + (2 * (2 + t) + pl) * kPlane);
+                F1[t][pl] = *(const lds_bf8*)(fb + (2 * (4 + t) + pl) * kPlane);
+            }
         // After a sequence's last chunk, its new histories: loaded before this chunk's copies
         // are issued, stored in beta_k.
         const RunChunk cur = rc;
@@ -1434,20 +1466,27 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         if (k + 1 < n) rc = run_chunk(p, run, run.a + k + 1);
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
         // in beta_{k-2}; they are read from alpha_{k+1} on.
-        if (k + 1 < n) {
-            copy_keys(k + 1);
-            load(k + 1);
-        }
+        if (k + 1 < n) copy_keys(k + 1);
         // beta_k: nothing this wave wrote to LDS is pending; the copies and loads stay in flight.
         __asm__ volatile("" ::: "memory");
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
+        {
+            v4 X[4];
+            d_x<4>(wb, V, Gm, 0, X);
+            bf8 xh[2], xl[2];
+            split_tiles(X[0], X[1], xh[0], xl[0]);
+            split_tiles(X[2], X[3], xh[1], xl[1]);
+            v4 D[2] = {v4{0.f, 0.f, 0.f, 0.f}, v4{0.f, 0.f, 0.f, 0.f}};
+            mfma2_split(F0, xh[0], xl[0], D);               // tokens 0-31
+            mfma2_split(F1, xh[1], xl[1], D);               // tokens 32-63
+            d_hand(lds, lane, 1, E, D);
+        }
         if (cur.ends()) {
             if (has_q) hist_put(p, cq, cur.s, hq);
             if (has_v) hist_put(p, cv, cur.s, hv);
         }
-        if (k + 1 < n) produce();                           // waits for the loads, and so the copies
         wait_barrier();                                     // alpha_{k+1}: the copies have landed
     }
 }
@@ -1497,7 +1536,7 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     if (w <= 1) {
         chain_state_role(p, lds, lane, run, w, h, j0);
     } else if (w == 4) {
-        chain_d_role(lds, lane, run.n);
+        chain_d_role(p, lds, lane, run, h);
     } else if (w == 5) {
         chain_feed_role(p, lds, lane, run, h, strip, src);
     } else {
@@ -1612,7 +1651,6 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
         if (prefill_ws_bytes(cfg, n_seq, total_T, mid, gwin) <= workspace_bytes) W = mid;
         else W_hi = mid - 1;
     }
-    W = (NCmax + (NCmax + W - 1) / W - 1) / ((NCmax + W - 1) / W);   // windows of equal size
     size_t off[kWsSections];
     const size_t need = ws_layout(cfg, n_seq, total_T, W, off);
     const long long NC = (long long)NCmax;

@@ -170,8 +170,8 @@ size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total
 /* Bytes of device workspace for ix_gdn_prefill (gated = 0) or ix_gdn_prefill_gated (gated = 1)
  * in windows of window_chunks 64-token chunks: the chunk tables (16 bytes per chunk) plus the
  * chunk operands of one window. Any workspace of at least the size for window_chunks = 1 works;
- * the prefill then runs in equal windows of at most as many chunks as the workspace holds
- * (and at most 80), one after the other, with results identical to the one-window run. 0 for invalid arguments. Addition; no
+ * the prefill then runs in windows of as many chunks as the workspace holds (at most 80), one
+ * after the other, with results identical to the one-window run. 0 for invalid arguments. Addition; no
  * reference counterpart (for callers that bound device memory independently of total_T). */
 size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T, int window_chunks,
                                             int gated);
