@@ -862,7 +862,9 @@ constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlo
 constexpr int kXRows = 24;                              // an output wave's x staging: rows 16 r - 3 .. 16 r + 20
 constexpr int kXBytes = 4 * kXRows * kStrip * 2;        // 16 bf16 channels per row, 4 output waves
 constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
-constexpr int kChainLds = kOffX + kXBytes;              // 142,864 bytes
+constexpr int kMaxWindow = 80;                          // chunks of a window at most
+constexpr int kOffR = kOffX + kXBytes;                  // the run's chunk records
+constexpr int kChainLds = kOffR + kMaxWindow * 16;      // 144,144 bytes
 
 typedef __attribute__((address_space(3))) bf8 lds_bf8;
 typedef __attribute__((address_space(3))) v4 lds_v4;
@@ -978,20 +980,15 @@ struct RunChunk {
     __device__ bool starts() const { return t0 == lo; }               // the sequence's first chunk
     __device__ bool ends() const { return t0 + kChunk >= hi; }        // its last
 };
-__device__ __forceinline__ RunChunk run_chunk(const PrefillParams& p, const ChainRun& run, int c) {
+// Record k of the run, from the copy in LDS (kOffR) that every wave reads from before its
+// first phase.
+__device__ __forceinline__ RunChunk run_chunk(const uint8_t* lds, int k) {
+    const u4x v = *(const __attribute__((address_space(3))) u4x*)((const lds_u8*)lds + kOffR + 16 * k);
     RunChunk r;
-    if (p.single) {
-        r.s = 0;
-        r.lo = run.lo;
-        r.hi = run.hi;
-        r.t0 = run.lo + c * kChunk;
-    } else {
-        const int4 v = p.ws.chunk_rec[c];
-        r.s = v.x;
-        r.t0 = v.y;
-        r.lo = v.z;
-        r.hi = v.w;
-    }
+    r.s = (int)v.x;
+    r.t0 = (int)v.y;
+    r.lo = (int)v.z;
+    r.hi = (int)v.w;
     return r;
 }
 
@@ -1018,8 +1015,8 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
     };
     // Chunks c_k, c_{k+1}, c_{k+2} (clamped to the run's last): each record is loaded two chunks
     // before the one that decides on it.
-    RunChunk rc = run_chunk(p, run, run.a), rn = run_chunk(p, run, run.a + min(1, n - 1)),
-             rn2 = run_chunk(p, run, run.a + min(2, n - 1));
+    RunChunk rc = run_chunk(lds, 0), rn = run_chunk(lds, min(1, n - 1)),
+             rn2 = run_chunk(lds, min(2, n - 1));
     v4 S[4], Sn[4];
     st_load(rc.s, S);
     if (n > 1 && rn.starts()) st_load(rn.s, Sn);
@@ -1101,7 +1098,7 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
             rc = rn;
             rn = rn2;
             if (k + 2 < n && rn.starts()) st_load(rn.s, Sn);
-            rn2 = run_chunk(p, run, run.a + min(k + 3, n - 1));
+            rn2 = run_chunk(lds, min(k + 3, n - 1));
             load_k(q1);
             hand_and_w();
         }
@@ -1307,7 +1304,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     }
     const int n = run.n;
     // Chunks c_k, c_{k+1}, c_{k+2} of the run (clamped to its last).
-    RunChunk r0 = run_chunk(p, run, run.a), r1 = run_chunk(p, run, run.a + min(1, n - 1)), r2 = run_chunk(p, run, run.a + min(2, n - 1));
+    RunChunk r0 = run_chunk(lds, 0), r1 = run_chunk(lds, min(1, n - 1)), r2 = run_chunk(lds, min(2, n - 1));
     XStage xs;
     stage_load<DC>(p, r0, h, strip, r, lane, xs);
     stage_conv<DC, SILU>(lds, xs, r, lane, cw, r0.len());
@@ -1385,7 +1382,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         if (k + 2 < n) chain_out_load_m(p, run, k + 2, h, r, lane, M);
         r0 = r1;
         r1 = r2;
-        r2 = run_chunk(p, run, run.a + min(k + 3, n - 1));
+        r2 = run_chunk(lds, min(k + 3, n - 1));
     };
     lds_barrier();                                          // alpha_0
     for (int k = 0; k < n; k += 2) {
@@ -1428,7 +1425,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     const int ng = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + ng - 1) / ng;
     const bool has_q = lane < per && gi * per + lane < cqk, has_v = lane < kStrip;
     const int cq = has_q ? gi * per + lane : 0, cv = v_channel(L, h, strip * kStrip + (lane & (kStrip - 1)));
-    RunChunk rc = run_chunk(p, run, run.a);                      // chunk c_k
+    RunChunk rc = run_chunk(lds, 0);                      // chunk c_k
     copy_keys(0);
     wait_barrier();                                         // alpha_0
     const int lg4 = lane >> 4;
@@ -1463,7 +1460,7 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
             hq = hist_fetch(p, cq, cur.lo, cur.hi - cur.lo, cur.s);
             hv = hist_fetch(p, cv, cur.lo, cur.hi - cur.lo, cur.s);
         }
-        if (k + 1 < n) rc = run_chunk(p, run, run.a + k + 1);
+        if (k + 1 < n) rc = run_chunk(lds, k + 1);
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
         // in beta_{k-2}; they are read from alpha_{k+1} on.
         if (k + 1 < n) copy_keys(k + 1);
@@ -1529,6 +1526,14 @@ __global__ void __launch_bounds__(kChainWaves * kWave) chain_kernel(const Prefil
     run.n = share_start(grp + 1) - run.a;
     if (run.n <= 0) return;
     run.wk = run.a - p.cb;
+    // The run's chunk records, read by every role from LDS (n <= W <= kMaxWindow).
+    if ((int)threadIdx.x < run.n) {
+        const int t = threadIdx.x;
+        const int4 v = p.single ? int4{0, run.lo + (run.a + t) * kChunk, run.lo, run.hi} : p.ws.chunk_rec[run.a + t];
+        *(__attribute__((address_space(3))) u4x*)((lds_u8*)lds + kOffR + 16 * t) =
+            u4x{(uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w};
+    }
+    __syncthreads();
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int lane = threadIdx.x & (kWave - 1);
     const int j0 = strip * kStrip;
@@ -1591,16 +1596,16 @@ static size_t prefill_ws_bytes(const ix_gdn_cfg* cfg, int n_seq, int T, size_t W
 // kernel writing them and the chain reading them (configuration 4: 1.60 ms in 80-chunk windows,
 // 1.80 ms in 112-chunk ones). The default workspace holds such a window, so it stops growing
 // with total_T (only the chunk tables do, 16 bytes per chunk).
-constexpr size_t kMaxWindow = 80;
+using ixg::kMaxWindow;
 
 extern "C" size_t ix_gdn_prefill_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kMaxWindow), false);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), (size_t)kMaxWindow), false);
 }
 
 extern "C" size_t ix_gdn_prefill_gated_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T) {
     if (ix_gdn_check_cfg_(cfg) != hipSuccess || n_seq <= 0 || total_T < 0) return 0;
-    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), kMaxWindow), true);
+    return prefill_ws_bytes(cfg, n_seq, total_T, std::min(ixg::max_chunks(n_seq, total_T), (size_t)kMaxWindow), true);
 }
 
 extern "C" size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, int n_seq, int total_T,
@@ -1645,7 +1650,7 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     const bool gwin = gate && !o;
     const size_t NCmax = max_chunks(n_seq, total_T);
     if (workspace_bytes < prefill_ws_bytes(cfg, n_seq, total_T, 1, gwin)) return hipErrorInvalidValue;
-    size_t W = 1, W_hi = std::min(NCmax, kMaxWindow);
+    size_t W = 1, W_hi = std::min(NCmax, (size_t)kMaxWindow);
     while (W < W_hi) {
         const size_t mid = (W + W_hi + 1) / 2;
         if (prefill_ws_bytes(cfg, n_seq, total_T, mid, gwin) <= workspace_bytes) W = mid;
