@@ -837,7 +837,8 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 // split to bf16 hi/lo, is the next product's B operand as it stands. The D and feed waves read
 // chunk c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
 // The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
-// alpha_{k+1}, with Q, M and Gam loaded from the workspace two chunks ahead; in beta_k each
+// alpha_{k+1}, with Q and M loaded from the workspace two chunks ahead (Gam read from the value
+// slot in alpha_k); in beta_k each
 // also builds row tile r of chunk c_{k+1}'s V (the conv of the strip's v channels) into the
 // value slot. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
 // with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
@@ -1112,7 +1113,13 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
 // 16 v channels, one channel pair per lane: lane l loads pair l & 7 as one word. Rows before the
 // sequence start come from the old conv history, rows past its end repeat its last token
 // (their V rows are zeroed).
-struct XStage { uint32_t w[3]; };
+// Every load is issued on every call (a row before the sequence start takes its history word
+// in stage_conv), so each call issues the same memory operations and later waits can count them.
+struct XStage {
+    uint32_t w[3];
+    uint32_t h0, h1;      // the history pair of row 0 and whether row 0 lies before the sequence
+    bool hist;
+};
 template <int DC>
 __device__ __forceinline__ void stage_load(const PrefillParams& p, const RunChunk& rc, int h, int strip, int r,
                                            int lane, XStage& xs) {
@@ -1123,13 +1130,13 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const RunChun
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int pos = pos0 + 8 * i + (lane >> 3);        // >= 0 for i > 0
-        if (i == 0 && pos < 0) {
-            const int hp = max(pos, -(DC - 1));             // rows before -(DC-1) feed no output
-            xs.w[i] = (uint32_t)hist[hp] | ((uint32_t)hist[hp + (DC - 1)] << 16);
-        } else {
-            xs.w[i] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(rc.lo + min(pos, last)) * L.C + ch);
-        }
+        xs.w[i] = *reinterpret_cast<const uint32_t*>(p.x + (size_t)(rc.lo + max(min(pos, last), 0)) * L.C + ch);
     }
+    const int pos = pos0 + (lane >> 3);
+    const int hp = min(max(pos, -(DC - 1)), -1);            // rows before -(DC-1) feed no output
+    xs.h0 = hist[hp];
+    xs.h1 = hist[hp + (DC - 1)];
+    xs.hist = pos < 0;
 }
 // The conv of the staged rows into row tile r of the value slot, in the D wave's accumulator
 // layout: lane (li, lg4) holds V[16 r + 4 lg4 + e][channel li], e = 0..3, zero for rows at or
@@ -1145,7 +1152,9 @@ __device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int r
     // from reordering the two (the wave's own LDS accesses then complete in program order).
     __asm__ volatile("" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 3; ++i) *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) = xs.w[i];
+    for (int i = 0; i < 3; ++i)
+        *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) =
+            i == 0 && xs.hist ? xs.h0 | (xs.h1 << 16) : xs.w[i];
     __asm__ volatile("" ::: "memory");
     const int li = lane & 15, lg4 = lane >> 4, t0 = 16 * r + 4 * lg4;
     float xv[DC + 3];
@@ -1256,15 +1265,14 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
 }
 
 // Output role (waves 2, 3, 6, 7; row tile r): rows 16 r .. 16 r + 15 of every chunk's outputs,
-// O = diag(Gam) Q S + M D, with Q, M and Gam from the workspace, loaded two chunks ahead into
-// two alternating operand sets. In beta_k the wave forms diag(Gam) Q S of chunk c_k, builds row
-// tile r of chunk c_{k+1}'s V, then loads chunk c_{k+2}'s Q and Gam into the set it used and its
-// x rows; in alpha_{k+1} it adds M D, stores the rows and loads chunk c_{k+2}'s M. Row tile r of
-// chunk c_0's V is built before alpha_0, when the wave also reads the old conv history (wave 0's
-// first rows), which the feed wave replaces only after that barrier.
+// O = diag(Gam) Q S + M D, with Q and M from the workspace, loaded two chunks ahead into two
+// alternating operand sets, and Gam from the value slot, read in alpha_k. In beta_k the wave
+// forms diag(Gam) Q S of chunk c_k, builds row tile r of chunk c_{k+1}'s V, then loads chunk
+// c_{k+2}'s Q into the set it used and its x rows; in alpha_{k+1} it adds M D, stores the rows,
+// reads chunk c_{k+1}'s Gam and loads chunk c_{k+2}'s M. Row tile r of chunk c_0's V is built
+// before alpha_0, when the wave also reads the old conv history of the run's first sequence.
 struct OutQ {
     bf8 qf[4][2];
-    v4 g;                 // exp(G_t) at this lane's rows
 };
 struct OutM {
     bf8 mf[2][2];
@@ -1277,16 +1285,15 @@ __device__ __forceinline__ void chain_out_load_q(const PrefillParams& p, const C
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
         for (int pl = 0; pl < 2; ++pl) x.qf[ks][pl] = *reinterpret_cast<const bf8*>(Qf + frag_at(r, ks, 4, pl, lane));
-    x.g = *reinterpret_cast<const v4*>(p.ws.G + (c * p.L.h_v + h) * 2 * kChunk + kChunk + 16 * r + 4 * (lane >> 4));
 }
 __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const ChainRun& run, int k, int h, int r,
                                                  int lane, OutM& x) {
     const size_t c = (size_t)(run.wk + min(k, run.n - 1));
     const uint8_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragMBytes;
-    // Row tiles 0 and 1 end before token 32, so their k-step 1 of M (tokens 32..63) is zero.
+    // Row tiles 0 and 1 end before token 32: their k-step 1 of M (tokens 32..63) is zero, not
+    // stored, and loaded only to keep the number of loads fixed (M D does not use it).
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-        if (ks == 0 || r >= 2)
 #pragma unroll
             for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + 2 * frag_at(r, ks, 2, pl, lane));
 }
@@ -1308,7 +1315,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     XStage xs;
     stage_load<DC>(p, r0, h, strip, r, lane, xs);
     stage_conv<DC, SILU>(lds, xs, r, lane, cw, r0.len());
-    if (n > 1) stage_load<DC>(p, r1, h, strip, r, lane, xs);
+    stage_load<DC>(p, r1, h, strip, r, lane, xs);
     OutQ q0, q1;
     OutM m0, m1;
     chain_out_load_q(p, run, 0, h, src, r, lane, q0);
@@ -1321,6 +1328,11 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     // A window buffer for o starts at the window's first token.
     int tw0 = 0, tw1;
     if (p.o_win) window_tokens(p, tw0, tw1);
+    tw0 = __builtin_amdgcn_readfirstlane(tw0);              // waited for here, not in the loop
+    // exp(G_t) of chunk c_k at this lane's rows, read from the value slot in alpha_k (the D wave
+    // writes chunk c_{k+1}'s there in beta_k).
+    const lds_u8* gmb = lane_at(lds, kOffV + 4 * kPlane + 4 * kChunk + 64 * r + 16 * lg4);
+    v4 gam_k;
     auto store = [&](const RunChunk& g) {
         const size_t ob = ((size_t)g.t0 * L.h_v + h) * kD + j0 + li;
         const size_t obw = ((size_t)(g.t0 - tw0) * L.h_v + h) * kD + j0 + li;
@@ -1350,12 +1362,13 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
             a2 = mfma_bf16(Q.qf[ks][1], sb[ks][0], a2);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * Q.g[i];
-        if (k + 1 < n) {                                    // row tile r of chunk c_{k+1}'s V
-            stage_conv<DC, SILU>(lds, xs, r, lane, cw, r1.len());
-            if (k + 2 < n) stage_load<DC>(p, r2, h, strip, r, lane, xs);
-        }
-        if (k + 2 < n) chain_out_load_q(p, run, k + 2, h, src, r, lane, Q);
+        for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * gam_k[i];
+        // Row tile r of chunk c_{k+1}'s V, then chunk c_{k+2}'s x rows and Q. The loads are
+        // issued in every step (clamped to the run's last chunk), so that the waits for them
+        // count a fixed number of later operations.
+        stage_conv<DC, SILU>(lds, xs, r, lane, cw, r1.len());
+        stage_load<DC>(p, r2, h, strip, r, lane, xs);
+        chain_out_load_q(p, run, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
         // M D: tokens 0-31 for every row tile, tokens 32-63 for row tiles 2 and 3 only.
         bf8 db[2][2];
@@ -1379,12 +1392,14 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = a0[i] + a1[i] + a2[i];
         store(r0);
-        if (k + 2 < n) chain_out_load_m(p, run, k + 2, h, r, lane, M);
+        gam_k = *(const lds_v4*)gmb;                        // chunk c_{k+1}'s
+        chain_out_load_m(p, run, k + 2, h, r, lane, M);
         r0 = r1;
         r1 = r2;
         r2 = run_chunk(lds, min(k + 3, n - 1));
     };
     lds_barrier();                                          // alpha_0
+    gam_k = *(const lds_v4*)gmb;
     for (int k = 0; k < n; k += 2) {
         step(k, q0, m0);
         if (k + 1 < n) step(k + 1, q1, m1);
