@@ -1290,12 +1290,14 @@ __device__ __forceinline__ void chain_out_load_m(const PrefillParams& p, const C
                                                  int lane, OutM& x) {
     const size_t c = (size_t)(run.wk + min(k, run.n - 1));
     const uint8_t* Mf = p.ws.Mf + (c * p.L.h_v + h) * kFragMBytes;
-    // Row tiles 0 and 1 end before token 32: their k-step 1 of M (tokens 32..63) is zero, not
-    // stored, and loaded only to keep the number of loads fixed (M D does not use it).
+    // Row tiles 0 and 1 end before token 32: their k-step 1 of M (tokens 32..63) is zero and not
+    // stored; they load k-step 0 again in its place (a fixed number of loads, no extra bytes;
+    // M D does not use it).
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int pl = 0; pl < 2; ++pl) x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + 2 * frag_at(r, ks, 2, pl, lane));
+            for (int pl = 0; pl < 2; ++pl)
+                x.mf[ks][pl] = *reinterpret_cast<const bf8*>(Mf + 2 * frag_at(r, r >= 2 ? ks : 0, 2, pl, lane));
 }
 
 template <int DC, bool SILU>
