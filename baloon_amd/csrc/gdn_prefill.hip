@@ -838,9 +838,8 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 // chunk c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
 // The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
 // alpha_{k+1}, with Q and M loaded from the workspace two chunks ahead (Gam read from the value
-// slot in alpha_k); in beta_k each
-// also builds row tile r of chunk c_{k+1}'s V (the conv of the strip's v channels) into the
-// value slot. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
+// slot in alpha_k); they build row tile r of chunk c_{k+1}'s V (the conv of the strip's v
+// channels) half in alpha_k, half in beta_k. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
 // with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
 // until beta_{k-2}), and writes the new rolling conv history of the workgroup's channels; the
 // D wave writes chunk c_{k+1}'s decay factors and T' fragments into the value slot in beta_k
@@ -865,7 +864,10 @@ constexpr int kXBytes = 4 * kXRows * kStrip * 2;        // 16 bf16 channels per 
 constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
 constexpr int kMaxWindow = 80;                          // chunks of a window at most
 constexpr int kOffR = kOffX + kXBytes;                  // the run's chunk records
-constexpr int kChainLds = kOffR + kMaxWindow * 16;      // 144,144 bytes
+constexpr int kOffV1 = kOffR + kMaxWindow * 16;         // V of odd chunks (even ones at kOffV)
+constexpr int kChainLds = kOffV1 + 4 * kPlane;          // 148,240 bytes
+// V of chunk c_k (4 row tiles, accumulator layout): written in alpha_{k-1}, read in alpha_k.
+__device__ __forceinline__ int v_buf(int k) { return (k & 1) ? kOffV1 : kOffV; }
 
 typedef __attribute__((address_space(3))) bf8 lds_bf8;
 typedef __attribute__((address_space(3))) v4 lds_v4;
@@ -1142,35 +1144,44 @@ __device__ __forceinline__ void stage_load(const PrefillParams& p, const RunChun
 // layout: lane (li, lg4) holds V[16 r + 4 lg4 + e][channel li], e = 0..3, zero for rows at or
 // past len. The rows pass through the wave's own LDS staging area (row 16 r - 3 + i at 32 i
 // bytes). Same accumulation order as the fused kernels' conv.
-template <int DC, bool SILU>
+// PART 0 stages the rows and forms entries 0, 1; PART 1 forms entries 2, 3 from the staged
+// rows (the same wave, later); PART -1 does both.
+template <int DC, bool SILU, int PART = -1>
 __device__ __forceinline__ void stage_conv(uint8_t* lds, const XStage& xs, int r, int lane, const float (&w)[DC],
-                                           int len) {
+                                           int len, int vbuf) {
     typedef __attribute__((address_space(3))) uint32_t lds_u32;
     typedef __attribute__((address_space(3))) uint16_t lds_u16;
+    typedef float f2 __attribute__((ext_vector_type(2)));
     lds_u8* xst = (lds_u8*)lds + kOffX + r * kXRows * 32;
     // The words go in as 32-bit and come back as 16-bit values: the fences keep the compiler
     // from reordering the two (the wave's own LDS accesses then complete in program order).
     __asm__ volatile("" ::: "memory");
+    if constexpr (PART != 1) {
 #pragma unroll
-    for (int i = 0; i < 3; ++i)
-        *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) =
-            i == 0 && xs.hist ? xs.h0 | (xs.h1 << 16) : xs.w[i];
-    __asm__ volatile("" ::: "memory");
+        for (int i = 0; i < 3; ++i)
+            *(lds_u32*)(xst + (8 * i + (lane >> 3)) * 32 + 4 * (lane & 7)) =
+                i == 0 && xs.hist ? xs.h0 | (xs.h1 << 16) : xs.w[i];
+        __asm__ volatile("" ::: "memory");
+    }
+    constexpr int e0 = PART == 1 ? 2 : 0, ne = PART == -1 ? 4 : 2;
     const int li = lane & 15, lg4 = lane >> 4, t0 = 16 * r + 4 * lg4;
-    float xv[DC + 3];
+    float xv[ne + DC - 1];
 #pragma unroll
-    for (int j = 0; j < DC + 3; ++j)
-        xv[j] = __uint_as_float((uint32_t) * (const lds_u16*)(xst + (4 * lg4 - (DC - 1) + j + 3) * 32 + 2 * li) << 16);
-    v4 V;
+    for (int j = 0; j < ne + DC - 1; ++j)
+        xv[j] = __uint_as_float((uint32_t) * (const lds_u16*)(xst + (4 * lg4 - (DC - 1) + e0 + j + 3) * 32 + 2 * li)
+                                << 16);
+    float V[ne];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < ne; ++e) {
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < DC; ++i) acc = fmaf(xv[e + i], w[i], acc);
         if constexpr (SILU) acc = acc * sigmoid_f(acc);
-        V[e] = t0 + e < len ? acc : 0.0f;
+        V[e] = t0 + e0 + e < len ? acc : 0.0f;
     }
-    *(lds_v4*)((lds_u8*)lds + kOffV + r * kPlane + lane * 16) = V;
+    lds_u8* vd = (lds_u8*)lds + vbuf + r * kPlane + lane * 16;
+    if constexpr (PART == -1) *(lds_v4*)vd = v4{V[0], V[1], V[2], V[3]};
+    else *(__attribute__((address_space(3))) f2*)(vd + 4 * e0) = f2{V[0], V[1]};
     __asm__ volatile("" ::: "memory");
 }
 
@@ -1229,13 +1240,15 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
     };
     load(0);
     produce();
-    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* vb0 = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* vb1 = lane_at(lds, kOffV1 + lane * 16);
     const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
     const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
     for (int k = 0; k < n; ++k) {
         lds_barrier();                                      // alpha_k: chunk c_k in the value slot
         if (k + 1 < n) load(k + 1);
+        const lds_u8* vb = (k & 1) ? vb1 : vb0;
         v4 V[2], E[2], Gm[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
@@ -1267,10 +1280,13 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
 // Output role (waves 2, 3, 6, 7; row tile r): rows 16 r .. 16 r + 15 of every chunk's outputs,
 // O = diag(Gam) Q S + M D, with Q and M from the workspace, loaded two chunks ahead into two
 // alternating operand sets, and Gam from the value slot, read in alpha_k. In beta_k the wave
-// forms diag(Gam) Q S of chunk c_k, builds row tile r of chunk c_{k+1}'s V, then loads chunk
-// c_{k+2}'s Q into the set it used and its x rows; in alpha_{k+1} it adds M D, stores the rows,
-// reads chunk c_{k+1}'s Gam and loads chunk c_{k+2}'s M. Row tile r of chunk c_0's V is built
-// before alpha_0, when the wave also reads the old conv history of the run's first sequence.
+// forms diag(Gam) Q S of chunk c_k and the second half of row tile r of chunk c_{k+1}'s V, then
+// loads chunk c_{k+2}'s Q; in alpha_{k+1} it adds M D, stores the rows, reads chunk c_{k+1}'s
+// Gam, forms the first half of chunk c_{k+2}'s V tile (V is double-buffered: c_{k+2}'s is
+// written while the D and feed waves read c_{k+1}'s) and loads c_{k+3}'s x rows and c_{k+2}'s
+// M. Row tile r
+// of chunk c_0's V is built before alpha_0, when the wave also reads the old conv history of
+// the run's first sequence.
 struct OutQ {
     bf8 qf[4][2];
 };
@@ -1312,12 +1328,16 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         for (int i = 0; i < DC; ++i) cw[i] = bf16_to_f32(wp[i]);
     }
     const int n = run.n;
-    // Chunks c_k, c_{k+1}, c_{k+2} of the run (clamped to its last).
-    RunChunk r0 = run_chunk(lds, 0), r1 = run_chunk(lds, min(1, n - 1)), r2 = run_chunk(lds, min(2, n - 1));
-    XStage xs;
-    stage_load<DC>(p, r0, h, strip, r, lane, xs);
-    stage_conv<DC, SILU>(lds, xs, r, lane, cw, r0.len());
-    stage_load<DC>(p, r1, h, strip, r, lane, xs);
+    // Chunks c_k .. c_{k+3} of the run (clamped to its last).
+    RunChunk r0 = run_chunk(lds, 0), r1 = run_chunk(lds, min(1, n - 1)), r2 = run_chunk(lds, min(2, n - 1)),
+             r3 = run_chunk(lds, min(3, n - 1));
+    // x rows of chunk c_j in set j mod 2, loaded in alpha_{j-2}; row tile r of c_j's V built
+    // from them in alpha_{j-1} (entries 0, 1) and beta_{j-1} (entries 2, 3); chunk c_0's before
+    // alpha_0. The work splits so because the output waves have room in both phases.
+    XStage x0, x1;
+    stage_load<DC>(p, r0, h, strip, r, lane, x0);
+    stage_conv<DC, SILU>(lds, x0, r, lane, cw, r0.len(), v_buf(0));
+    stage_load<DC>(p, r1, h, strip, r, lane, x1);
     OutQ q0, q1;
     OutM m0, m1;
     chain_out_load_q(p, run, 0, h, src, r, lane, q0);
@@ -1348,7 +1368,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
             }
         }
     };
-    auto step = [&](int k, OutQ& Q, OutM& M) {
+    auto step = [&](int k, OutQ& Q, OutM& M, XStage& xa, XStage& xb) {
         lds_barrier();                                      // beta_k: S_k handed over
         bf8 sb[4][2];
 #pragma unroll
@@ -1365,11 +1385,10 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = (a0[i] + a1[i] + a2[i]) * gam_k[i];
-        // Row tile r of chunk c_{k+1}'s V, then chunk c_{k+2}'s x rows and Q. The loads are
-        // issued in every step (clamped to the run's last chunk), so that the waits for them
-        // count a fixed number of later operations.
-        stage_conv<DC, SILU>(lds, xs, r, lane, cw, r1.len());
-        stage_load<DC>(p, r2, h, strip, r, lane, xs);
+        // Entries 2, 3 of row tile r of chunk c_{k+1}'s V (0, 1 formed in alpha_k), then chunk
+        // c_{k+2}'s Q. Every step issues all its loads (clamped to the run's last chunk), so that
+        // the waits for them count a fixed number of later operations.
+        stage_conv<DC, SILU, 1>(lds, xa, r, lane, cw, r1.len(), v_buf(k + 1));
         chain_out_load_q(p, run, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
         // M D: tokens 0-31 for every row tile, tokens 32-63 for row tiles 2 and 3 only.
@@ -1395,16 +1414,23 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         for (int i = 0; i < 4; ++i) o[i] = a0[i] + a1[i] + a2[i];
         store(r0);
         gam_k = *(const lds_v4*)gmb;                        // chunk c_{k+1}'s
+        // Entries 0, 1 of row tile r of chunk c_{k+2}'s V (its x rows in xa), then chunk
+        // c_{k+3}'s x rows into xb (chunk c_{k+1}'s, staged in alpha_k), and chunk c_{k+2}'s M.
+        stage_conv<DC, SILU, 0>(lds, xa, r, lane, cw, r2.len(), v_buf(k + 2));
+        stage_load<DC>(p, r3, h, strip, r, lane, xb);
         chain_out_load_m(p, run, k + 2, h, r, lane, M);
         r0 = r1;
         r1 = r2;
-        r2 = run_chunk(lds, min(k + 3, n - 1));
+        r2 = r3;
+        r3 = run_chunk(lds, min(k + 4, n - 1));
     };
     lds_barrier();                                          // alpha_0
     gam_k = *(const lds_v4*)gmb;
+    stage_conv<DC, SILU, 0>(lds, x1, r, lane, cw, r1.len(), v_buf(1));
+    stage_load<DC>(p, r2, h, strip, r, lane, x0);
     for (int k = 0; k < n; k += 2) {
-        step(k, q0, m0);
-        if (k + 1 < n) step(k + 1, q1, m1);
+        step(k, q0, m0, x0, x1);
+        if (k + 1 < n) step(k + 1, q1, m1, x1, x0);
     }
 }
 
@@ -1447,13 +1473,15 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     wait_barrier();                                         // alpha_0
     const int lg4 = lane >> 4;
     const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
-    const lds_u8* vb = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* vb0 = lane_at(lds, kOffV + lane * 16);
+    const lds_u8* vb1 = lane_at(lds, kOffV1 + lane * 16);
     const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
     for (int k = 0; k < n; ++k) {
         // Row tiles 2, 3 of D_k: V, the decay factors and T' of chunk c_k read in alpha_k (T'
         // from this wave's registers, before the next chunk's loads replace them).
         v4 V[4], Gm[4], E[2];
+        const lds_u8* vb = (k & 1) ? vb1 : vb0;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) {
             V[mt] = *(const lds_v4*)(vb + mt * kPlane);
