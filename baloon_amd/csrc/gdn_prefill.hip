@@ -1087,6 +1087,10 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
             dh[ks] = *(const lds_bf8*)(gb + (2 * ks) * kPlane);
             dl[ks] = *(const lds_bf8*)(gb + (2 * ks + 1) * kPlane);
         }
+        // K of chunk c_{k+1} (in its slot since the end of beta_k) read now, behind Dg, so that
+        // its latency passes under the S update.
+        __asm__ volatile("" ::: "memory");
+        load_k(q1);
         const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) S[mt] *= gam;
@@ -1102,7 +1106,6 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
             rn = rn2;
             if (k + 2 < n && rn.starts()) st_load(rn.s, Sn);
             rn2 = run_chunk(lds, min(k + 3, n - 1));
-            load_k(q1);
             hand_and_w();
         }
         q = q1;
