@@ -1052,17 +1052,15 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
     // S_k handed over split (the outputs' B operand) and this wave's half of W_k = K_k S_k.
     auto hand_and_w = [&]() {
         bf8 sh[2], sl[2];
-        split_tiles(S[0], S[1], sh[0], sl[0]);
-        split_tiles(S[2], S[3], sh[1], sl[1]);
         v4 W[4];
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) W[mt] = v4{0.f, 0.f, 0.f, 0.f};
-        mfma4_split(KF[0], sh[0], sl[0], W);
-        mfma4_split(KF[1], sh[1], sl[1], W);
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
+            split_tiles(S[2 * a], S[2 * a + 1], sh[a], sl[a]);
             *(lds_bf8*)(hb + (2 * a) * kPlane) = sh[a];
             *(lds_bf8*)(hb + (2 * a + 1) * kPlane) = sl[a];
+            mfma4_split(KF[a], sh[a], sl[a], W);
         }
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) *(lds_v4*)(wb + mt * kPlane) = W[mt];
@@ -1094,8 +1092,17 @@ __device__ __forceinline__ void chain_state_role(const PrefillParams& p, uint8_t
         const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane);
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt) S[mt] *= gam;
-        mfma4_split(KT[0], dh[0], dl[0], S);
-        mfma4_split(KT[1], dh[1], dl[1], S);
+        // Row tiles 0, 1 first, so that their split and the first k-step of W need not wait
+        // for the last products of tiles 2, 3.
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int u = 0; u < 3; ++u)
+#pragma unroll
+                    for (int j = 2 * pr; j < 2 * pr + 2; ++j)
+                        S[j] = mfma_bf16(KT[ks][j][u == 2], u == 1 ? dl[ks] : dh[ks], S[j]);
         if (k + 1 < n) {
             if (rn.starts()) {                              // chunk c_k ended its sequence
                 st_store(rc.s, S);
