@@ -852,20 +852,19 @@ constexpr int kStrips = kD / kStrip;                    // 8
 constexpr int kChainWaves = 8;
 constexpr int kPlane = kWave * 16;                      // bytes of one fragment plane
 constexpr int kKSlots = 3;                              // key slots in a ring
-constexpr int kTSlot = 12 * kPlane;                     // T': its 6 nonzero fragments x 2 planes
 constexpr int kVSlot = 4 * kPlane + 2 * kChunk * 4;     // V (4 row tiles, accumulator layout), E, Gam
 constexpr int kHandS = 8 * kPlane;                      // S: 4 k-steps x 2 planes
 constexpr int kHandBytes = kHandS + 4 * kPlane;         // + D: 4 row tiles in fp32
 constexpr int kWBytes = 2 * 4 * kPlane;                 // the two halves of W: 4 row tiles in fp32 each
 constexpr int kDgBytes = 4 * kPlane + 16;               // Dg: 2 k-steps x 2 planes, then gam
-constexpr int kOffK = 0, kOffT = kOffK + kKSlots * kKSlot, kOffV = kOffT + kTSlot, kOffH = kOffV + kVSlot;
+constexpr int kOffK = 0, kOffV = kOffK + kKSlots * kKSlot, kOffH = kOffV + kVSlot;
 constexpr int kXRows = 24;                              // an output wave's x staging: rows 16 r - 3 .. 16 r + 20
 constexpr int kXBytes = 4 * kXRows * kStrip * 2;        // 16 bf16 channels per row, 4 output waves
 constexpr int kOffW = kOffH + kHandBytes, kOffG = kOffW + kWBytes, kOffX = kOffG + kDgBytes;
 constexpr int kMaxWindow = 80;                          // chunks of a window at most
 constexpr int kOffR = kOffX + kXBytes;                  // the run's chunk records
 constexpr int kOffV1 = kOffR + kMaxWindow * 16;         // V of odd chunks (even ones at kOffV)
-constexpr int kChainLds = kOffV1 + 4 * kPlane;          // 148,240 bytes
+constexpr int kChainLds = kOffV1 + 4 * kPlane;          // 135,952 bytes
 // V of chunk c_k (4 row tiles, accumulator layout): written in alpha_{k-1}, read in alpha_k.
 __device__ __forceinline__ int v_buf(int k) { return (k & 1) ? kOffV1 : kOffV; }
 
@@ -1223,41 +1222,40 @@ __device__ __forceinline__ void d_hand(uint8_t* lds, int lane, int ks, const v4*
     *(lds_v4*)(hb + (2 * ks + 1) * kPlane) = D[1];
 }
 
-// D role (wave 4): row tiles 0 and 1 of D, and gam. In alpha_k it also loads chunk c_{k+1}'s
-// decay factors and T' from the workspace, and writes them (E, then Gam, and the 6 nonzero
-// fragments of T') into the value slot in beta_k, once the feed wave has read chunk c_k's.
+// D role (wave 4): row tiles 0 and 1 of D (its T' fragments (0, 0), (1, 0) loaded into
+// registers a chunk ahead, in one of two sets), and gam. In alpha_k it also loads chunk
+// c_{k+1}'s decay factors and writes them (E, then Gam) into the value slot in beta_k, once the
+// feed wave has read chunk c_k's.
+struct DT {
+    u4x f[4];             // T' (0, 0) hi, lo, (1, 0) hi, lo
+};
 __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* lds, int lane, const ChainRun& run,
                                              int h) {
-    typedef __attribute__((address_space(3))) u4x lds_u4;
     const int lg4 = lane >> 4, n = run.n;
+    auto chh = [&](int k) { return (size_t)(run.wk + min(k, n - 1)) * p.L.h_v + h; };   // clamped
+    auto tload = [&](int k, DT& t) {
+        const uint8_t* tsrc = p.ws.Tf + chh(k) * kTriFragBytes;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.f[i] = load_tri_frag(tsrc, i >> 1, 0, i & 1, lane);
+    };
     v4 eg;
-    u4x tf[12];                                             // T' (mt, 0), mt = 0..3, then (2, 1), (3, 1)
-    auto load = [&](int k) {
-        const size_t chh = (size_t)(run.wk + min(k, run.n - 1)) * p.L.h_v + h;
-        eg = *reinterpret_cast<const v4*>(p.ws.G + chh * 2 * kChunk + 4 * (lane & 31));
-        const uint8_t* tsrc = p.ws.Tf + chh * kTriFragBytes;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) {
-            const int e = i >> 1, mt = e < 4 ? e : e - 2, ks = e < 4 ? 0 : 1;    // slot entry e, plane i & 1
-            tf[i] = load_tri_frag(tsrc, mt, ks, i & 1, lane);
-        }
-    };
-    auto produce = [&]() {
+    auto eload = [&](int k) { eg = *reinterpret_cast<const v4*>(p.ws.G + chh(k) * 2 * kChunk + 4 * (lane & 31)); };
+    auto eput = [&]() {
         if (lane < 32) *(lds_v4*)((lds_u8*)lds + kOffV + 4 * kPlane + lane * 16) = eg;
-        lds_u8* dst = (lds_u8*)lds + kOffT + lane * 16;
-#pragma unroll
-        for (int i = 0; i < 12; ++i) *(lds_u4*)(dst + i * kPlane) = tf[i];
     };
-    load(0);
-    produce();
+    eload(0);
+    eput();
+    DT d0, d1;
+    tload(0, d0);
     const lds_u8* vb0 = lane_at(lds, kOffV + lane * 16);
     const lds_u8* vb1 = lane_at(lds, kOffV1 + lane * 16);
     const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
-    const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
-    for (int k = 0; k < n; ++k) {
+    // cur: chunk c_k's fragments; oth: reloaded with c_{k+1}'s (it held c_{k-1}'s).
+    auto step = [&](int k, const DT& cur, DT& oth) {
         lds_barrier();                                      // alpha_k: chunk c_k in the value slot
-        if (k + 1 < n) load(k + 1);
+        tload(k + 1, oth);
+        eload(k + 1);
         const lds_u8* vb = (k & 1) ? vb1 : vb0;
         v4 V[2], E[2], Gm[2];
 #pragma unroll
@@ -1268,12 +1266,12 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
         }
         const float gam = *(const __attribute__((address_space(3))) float*)((lds_u8*)lds + kOffV + 4 * kPlane +
                                                                             4 * kChunk + 4 * (kChunk - 1));
+        lds_barrier();                                      // beta_k: both halves of W_k handed over
         bf8 F0[4][2];                                       // T' (mt, 0), mt = 0, 1
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl)
+        for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int mt = 0; mt < 2; ++mt) F0[mt][pl] = *(const lds_bf8*)(fb + (2 * mt + pl) * kPlane);
-        lds_barrier();                                      // beta_k: both halves of W_k handed over
+            for (int pl = 0; pl < 2; ++pl) F0[mt][pl] = __builtin_bit_cast(bf8, cur.f[2 * mt + pl]);
         v4 X[2];
         d_x<2>(wb, V, Gm, 0, X);
         bf8 xh, xl;
@@ -1282,7 +1280,11 @@ __device__ __forceinline__ void chain_d_role(const PrefillParams& p, uint8_t* ld
         mfma2_split(F0, xh, xl, D);                         // tokens 0-31
         d_hand(lds, lane, 0, E, D);
         if (lane == 0) *(__attribute__((address_space(3))) float*)((lds_u8*)lds + kOffG + 4 * kPlane) = gam;
-        if (k + 1 < n) produce();
+        eput();                                             // chunk c_{k+1}'s (clamped: harmless at the end)
+    };
+    for (int k = 0; k < n; k += 2) {
+        step(k, d0, d1);
+        if (k + 1 < n) step(k + 1, d1, d0);
     }
     lds_barrier();                                          // alpha_n
 }
@@ -1478,18 +1480,33 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
     const int ng = L.h_v * kStrips, gi = h * kStrips + strip, cqk = 2 * L.h_k * kD, per = (cqk + ng - 1) / ng;
     const bool has_q = lane < per && gi * per + lane < cqk, has_v = lane < kStrip;
     const int cq = has_q ? gi * per + lane : 0, cv = v_channel(L, h, strip * kStrip + (lane & (kStrip - 1)));
-    RunChunk rc = run_chunk(lds, 0);                      // chunk c_k
+    // T' (2, 0), (3, 0), (2, 1), (3, 1), hi and lo each, of a chunk, in registers (one of two
+    // sets, loaded in alpha of the chunk before; clamped to the run's last chunk).
+    struct FT {
+        u4x f[8];
+    };
+    auto tload = [&](int k, FT& t) {
+        const uint8_t* tsrc = p.ws.Tf + ((size_t)(run.wk + min(k, n - 1)) * L.h_v + h) * kTriFragBytes;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = i >> 1, mt = 2 + (e & 1), ks = e >> 1;
+            t.f[i] = load_tri_frag(tsrc, mt, ks, i & 1, lane);
+        }
+    };
+    RunChunk rc = run_chunk(lds, 0);                        // chunk c_k
+    FT f0, f1;
+    tload(0, f0);
     copy_keys(0);
     wait_barrier();                                         // alpha_0
     const int lg4 = lane >> 4;
-    const lds_u8* fb = lane_at(lds, kOffT + lane * 16);
     const lds_u8* vb0 = lane_at(lds, kOffV + lane * 16);
     const lds_u8* vb1 = lane_at(lds, kOffV1 + lane * 16);
     const lds_u8* eb = lane_at(lds, kOffV + 4 * kPlane + 16 * lg4);
     const lds_u8* wb = lane_at(lds, kOffW + lane * 16);
-    for (int k = 0; k < n; ++k) {
-        // Row tiles 2, 3 of D_k: V, the decay factors and T' of chunk c_k read in alpha_k (T'
-        // from this wave's registers, before the next chunk's loads replace them).
+    // cur: chunk c_k's T'; oth: reloaded with c_{k+1}'s (it held c_{k-1}'s).
+    auto step = [&](int k, const FT& cur, FT& oth) {
+        // Row tiles 2, 3 of D_k: V and the decay factors of chunk c_k read in alpha_k.
+        tload(k + 1, oth);
         v4 V[4], Gm[4], E[2];
         const lds_u8* vb = (k & 1) ? vb1 : vb0;
 #pragma unroll
@@ -1499,21 +1516,13 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         }
 #pragma unroll
         for (int t = 0; t < 2; ++t) E[t] = *(const lds_v4*)(eb + (2 + t) * 64);
-        bf8 F0[4][2], F1[4][2];                             // T' (2, 0), (3, 0); T' (2, 1), (3, 1)
-#pragma unroll
-        for (int pl = 0; pl < 2; ++pl)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                F0[t][pl] = *(const lds_bf8*)(fb + (2 * (2 + t) + pl) * kPlane);
-                F1[t][pl] = *(const lds_bf8*)(fb + (2 * (4 + t) + pl) * kPlane);
-            }
         // After a sequence's last chunk, its new histories: loaded before this chunk's copies
         // are issued, stored in beta_k.
-        const RunChunk cur = rc;
+        const RunChunk cc = rc;
         HistNew hq, hv;
-        if (cur.ends()) {
-            hq = hist_fetch(p, cq, cur.lo, cur.hi - cur.lo, cur.s);
-            hv = hist_fetch(p, cv, cur.lo, cur.hi - cur.lo, cur.s);
+        if (cc.ends()) {
+            hq = hist_fetch(p, cq, cc.lo, cc.hi - cc.lo, cc.s);
+            hv = hist_fetch(p, cv, cc.lo, cc.hi - cc.lo, cc.s);
         }
         if (k + 1 < n) rc = run_chunk(lds, k + 1);
         // Chunk c_{k+1}'s keys go to the slot of chunk c_{k-2}, whose K^T the state waves read
@@ -1525,6 +1534,14 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
         {
+            bf8 F0[4][2], F1[4][2];                         // T' (2, 0), (3, 0); T' (2, 1), (3, 1)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int pl = 0; pl < 2; ++pl) {
+                    F0[t][pl] = __builtin_bit_cast(bf8, cur.f[2 * t + pl]);
+                    F1[t][pl] = __builtin_bit_cast(bf8, cur.f[4 + 2 * t + pl]);
+                }
             v4 X[4];
             d_x<4>(wb, V, Gm, 0, X);
             bf8 xh[2], xl[2];
@@ -1535,11 +1552,15 @@ __device__ __forceinline__ void chain_feed_role(const PrefillParams& p, uint8_t*
             mfma2_split(F1, xh[1], xl[1], D);               // tokens 32-63
             d_hand(lds, lane, 1, E, D);
         }
-        if (cur.ends()) {
-            if (has_q) hist_put(p, cq, cur.s, hq);
-            if (has_v) hist_put(p, cv, cur.s, hv);
+        if (cc.ends()) {
+            if (has_q) hist_put(p, cq, cc.s, hq);
+            if (has_v) hist_put(p, cv, cc.s, hv);
         }
         wait_barrier();                                     // alpha_{k+1}: the copies have landed
+    };
+    for (int k = 0; k < n; k += 2) {
+        step(k, f0, f1);
+        if (k + 1 < n) step(k + 1, f1, f0);
     }
 }
 
