@@ -1344,8 +1344,10 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     RunChunk r0 = run_chunk(lds, 0), r1 = run_chunk(lds, min(1, n - 1)), r2 = run_chunk(lds, min(2, n - 1)),
              r3 = run_chunk(lds, min(3, n - 1));
     // x rows of chunk c_j in set j mod 2, loaded in alpha_{j-2}; row tile r of c_j's V built
-    // from them in alpha_{j-1} (entries 0, 1) and beta_{j-1} (entries 2, 3); chunk c_0's before
-    // alpha_0. The work splits so because the output waves have room in both phases.
+    // from them in alpha_{j-1} (entries 0, 1; for r >= 2 in beta_{j-1} too) and beta_{j-1}
+    // (entries 2, 3); chunk c_0's before alpha_0. The work splits so because the output waves
+    // have room in both phases, waves 6 and 7 (r = 3, 2: their M D is twice as long, and they
+    // share SIMDs with waves 2 and 3) in beta only.
     XStage x0, x1;
     stage_load<DC>(p, r0, h, strip, r, lane, x0);
     stage_conv<DC, SILU>(lds, x0, r, lane, cw, r0.len(), v_buf(0));
@@ -1400,6 +1402,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         // Entries 2, 3 of row tile r of chunk c_{k+1}'s V (0, 1 formed in alpha_k), then chunk
         // c_{k+2}'s Q. Every step issues all its loads (clamped to the run's last chunk), so that
         // the waits for them count a fixed number of later operations.
+        if (r >= 2) stage_conv<DC, SILU, 0>(lds, xb, r, lane, cw, r1.len(), v_buf(k + 1));
         stage_conv<DC, SILU, 1>(lds, xa, r, lane, cw, r1.len(), v_buf(k + 1));
         chain_out_load_q(p, run, k + 2, h, src, r, lane, Q);
         lds_barrier();                                      // alpha_{k+1}: D_k handed over
@@ -1428,7 +1431,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
         gam_k = *(const lds_v4*)gmb;                        // chunk c_{k+1}'s
         // Entries 0, 1 of row tile r of chunk c_{k+2}'s V (its x rows in xa), then chunk
         // c_{k+3}'s x rows into xb (chunk c_{k+1}'s, staged in alpha_k), and chunk c_{k+2}'s M.
-        stage_conv<DC, SILU, 0>(lds, xa, r, lane, cw, r2.len(), v_buf(k + 2));
+        if (r < 2) stage_conv<DC, SILU, 0>(lds, xa, r, lane, cw, r2.len(), v_buf(k + 2));
         stage_load<DC>(p, r3, h, strip, r, lane, xb);
         chain_out_load_m(p, run, k + 2, h, r, lane, M);
         r0 = r1;
@@ -1438,7 +1441,7 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     };
     lds_barrier();                                          // alpha_0
     gam_k = *(const lds_v4*)gmb;
-    stage_conv<DC, SILU, 0>(lds, x1, r, lane, cw, r1.len(), v_buf(1));
+    if (r < 2) stage_conv<DC, SILU, 0>(lds, x1, r, lane, cw, r1.len(), v_buf(1));
     stage_load<DC>(p, r2, h, strip, r, lane, x0);
     for (int k = 0; k < n; k += 2) {
         step(k, q0, m0, x0, x1);
