@@ -243,7 +243,8 @@ def test_windows_match_one_window(cu, window):
 
 def test_windows_with_many_sequences():
     # 600 short sequences, a third of them empty, in windows of two chunks: each window's chain
-    # takes at most two sequence slots, found through the plan's list of non-empty sequences.
+    # workgroups walk its chunks across sequence boundaries, in 8 groups cut at sequence starts
+    # (h_v * 8 = 32 strips), resuming states and histories the previous windows left.
     cfg = bx.make_cfg(h_k=2, h_v=4)
     rng = np.random.default_rng(inputs.seed_for(4) + 9)
     lens = rng.integers(1, 100, 600)
