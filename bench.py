@@ -136,13 +136,18 @@ def heat(ms=40.0):
 
 def timed(stream, fn, n):
     """n calls of fn(i) between HIP events recorded on `stream`, right after heat(); every
-    status checked after."""
+    status checked after. The start event is queued behind a last ~0.5 ms of the heat work,
+    so that the GPU reaches it with the first calls already queued: the region times the
+    GPU's work, not the host's latency in issuing the first call."""
     import torch
 
     import baloon_amd as bx
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     heat()
+    with torch.cuda.stream(stream):
+        for _ in range(4):
+            _HEAT["buf"].mul_(1.0)
     e0.record(stream)
     rcs = [fn(i) for i in range(n)]
     e1.record(stream)
@@ -626,7 +631,7 @@ def latency_leg(O, iters=200, graph_steps=32, graph_replays=20):
     return round(eager_us, 2), round(graph_us, 2)
 
 
-def prefill_leg(O, T=4096, iters=10):
+def prefill_leg(O, T=4096, iters=30):
     """Configuration 3: ix_gdn_prefill of one T-token sequence from a zero state. Each call
     gets its own state and conv state, zeroed before the timed region (like every other
     input, they are resident in HBM when it starts; the kernels' work does not depend on
