@@ -261,6 +261,36 @@ def test_windows_with_many_sequences():
         np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("case", range(6))
+def test_random_batches(case):
+    # Seeded random batches: head layout, sequence count and lengths (empty ones included),
+    # initial state scale and window size drawn per case; against the oracle, and the windowed
+    # run bit-identical to the one-window run.
+    rng = np.random.default_rng(inputs.seed_for(4) + 1000 + case)
+    h_k, h_v = [(1, 1), (1, 2), (2, 4), (2, 6), (4, 8), (3, 3)][case]
+    cfg = bx.make_cfg(h_k=h_k, h_v=h_v, head_map=int(rng.integers(0, 2)), conv_act=int(rng.integers(0, 2)))
+    n = int(rng.integers(1, 10))
+    lens = rng.integers(0, 200, n)
+    lens[rng.random(n) < 0.2] = 0
+    lens[-1] = max(int(lens[-1]), 1)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    seed = inputs.seed_for(4) + 2000 + case
+    p = inputs.layer_params(cfg, seed)
+    tok = inputs.token_inputs(cfg, seed, T)
+    st = inputs.initial_states(cfg, seed, n, state_std=float(rng.choice([0.0, 0.02, 0.5])))
+    full = gpu_prefill(cfg, cu, tok, p, st)
+    cs, s, o, ob = full
+    rcs, rs, ro = oracle_prefill(cfg, cu, tok, p, st)
+    np.testing.assert_array_equal(cs, rcs)
+    assert oracle.rel_err(s, rs) <= TOL_STATE_REL
+    assert float(np.max(np.abs(o - ro))) <= TOL_O_ABS
+    np.testing.assert_array_equal(ob, bf16.from_f32(o))
+    win = gpu_prefill(cfg, cu, tok, p, st, window=int(rng.integers(1, 4)))
+    for a, b in zip(full, win):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_state_only_and_repeatable():
     cfg = bx.make_cfg()
     seed = inputs.seed_for(3) + 5
