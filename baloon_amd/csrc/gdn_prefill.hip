@@ -1369,16 +1369,32 @@ __device__ __forceinline__ void chain_output_role(const PrefillParams& p, uint8_
     // writes chunk c_{k+1}'s there in beta_k).
     const lds_u8* gmb = lane_at(lds, kOffV + 4 * kPlane + 4 * kChunk + 64 * r + 16 * lg4);
     v4 gam_k;
+    // o rows 16 r + 4 lg4 + i of a chunk at a lane offset fixed for the run, from a chunk base
+    // held in scalar registers; a full chunk stores without per-row tests.
+    const uint32_t lofs = (uint32_t)((16 * r + 4 * lg4) * (int)row + li);
     auto store = [&](const RunChunk& g) {
-        const size_t ob = ((size_t)g.t0 * L.h_v + h) * kD + j0 + li;
-        const size_t obw = ((size_t)(g.t0 - tw0) * L.h_v + h) * kD + j0 + li;
-        const int len = g.len();
+        const int t0 = __builtin_amdgcn_readfirstlane(g.t0), len = __builtin_amdgcn_readfirstlane(g.len());
+        const int tl = 16 * r + 4 * lg4;
+        if (p.o_bf16) {
+            uint16_t* ob = p.o_bf16 + ((size_t)t0 * L.h_v + h) * kD + j0;
+            if (len >= kChunk) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int t = 16 * r + 4 * lg4 + i;
-            if (t < len) {
-                if (p.o) p.o[obw + (size_t)t * row] = o[i];
-                if (p.o_bf16) p.o_bf16[ob + (size_t)t * row] = f32_to_bf16(o[i]);
+                for (int i = 0; i < 4; ++i) ob[lofs + (uint32_t)(i * (int)row)] = f32_to_bf16(o[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (tl + i < len) ob[lofs + (uint32_t)(i * (int)row)] = f32_to_bf16(o[i]);
+            }
+        }
+        if (p.o) {
+            float* ow = p.o + ((size_t)(t0 - tw0) * L.h_v + h) * kD + j0;
+            if (len >= kChunk) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ow[lofs + (uint32_t)(i * (int)row)] = o[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (tl + i < len) ow[lofs + (uint32_t)(i * (int)row)] = o[i];
             }
         }
     };
