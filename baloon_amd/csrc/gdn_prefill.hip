@@ -1710,19 +1710,6 @@ extern "C" size_t ix_gdn_prefill_window_workspace_size(const ix_gdn_cfg* cfg, in
     return prefill_ws_bytes(cfg, n_seq, total_T, W, gated != 0);
 }
 
-// CUs of the current device, queried once per device (the prefill's only device query).
-static int device_cus() {
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int cus = 256;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-        cached[dev] = cus;
-    }
-    return cached[dev];
-}
-
 // One window: the chunk kernel, then the chain. The conv activation and width are template
 // parameters: inlined into every unrolled conv output, a runtime choice would carry the
 // activation's code in the kernels that do not use it.
@@ -1784,7 +1771,7 @@ static hipError_t prefill_impl(const ix_gdn_cfg* cfg, int n_seq, int total_T, co
     // Chain workgroups: (v head, strip, group), G groups splitting each window's chunks at
     // sequence starts; one group while the h_v * 8 (head, strip) runs fill every CU.
     p.G = 1;
-    if (!p.single) p.G = std::max(1, std::min(n_seq, device_cus() / (cfg->h_v * kStrips)));
+    if (!p.single) p.G = std::max(1, std::min(n_seq, ixg::device_cu_count(s) / (cfg->h_v * kStrips)));
 
     if (!p.single) hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, p);
     const long long groups = ((long long)p.G * cfg->h_v + 7) / 8;
