@@ -834,16 +834,18 @@ __global__ void __launch_bounds__(kChunkThreads) __attribute__((amdgpu_waves_per
 //            and 2, 3, handing over D_k (fp32) for the outputs and Dg_k (split) with gam_k
 //            for the state waves.
 // Products take their k index in accumulator row order (kperm), so an accumulator tile pair,
-// split to bf16 hi/lo, is the next product's B operand as it stands. The D and feed waves read
-// chunk c_k's V, decay factors and T' from the value slot in alpha_k, while the state waves work.
+// split to bf16 hi/lo, is the next product's B operand as it stands. The D and feed waves keep
+// their T' fragments in registers (loaded a chunk ahead) and read chunk c_k's V and decay
+// factors from the value slot in alpha_k, while the state waves work.
 // The output waves (2, 3, 6, 7; row tile r) form diag(Gam) Q S in beta_k and add M D in
 // alpha_{k+1}, with Q and M loaded from the workspace two chunks ahead (Gam read from the value
 // slot in alpha_k); they build row tile r of chunk c_{k+1}'s V (the conv of the strip's v
-// channels) half in alpha_k, half in beta_k. The feed wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3
-// with direct global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read
-// until beta_{k-2}), and writes the new rolling conv history of the workgroup's channels; the
-// D wave writes chunk c_{k+1}'s decay factors and T' fragments into the value slot in beta_k
-// from registers loaded in alpha_k.
+// channels), half in alpha_k and half in beta_k for r < 2, all in beta_k for r >= 2. The feed
+// wave (5) copies chunk c_{k+1}'s key planes into key slot (k+1) mod 3 with direct
+// global-to-LDS loads issued in alpha_k (the slot last held chunk c_{k-2}, read until
+// beta_{k-2}), and writes the new rolling conv history of the workgroup's channels; the D
+// wave writes chunk c_{k+1}'s decay factors into the value slot in beta_k from registers
+// loaded in alpha_k.
 // A last alpha_n finishes S_n (state waves) and O_{n-1} (output waves).
 // Waves w and w + 4 share a SIMD: the state waves' partners (the D wave, the feed wave) only
 // read and copy in alpha, where the state waves work.
